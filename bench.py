@@ -1,0 +1,194 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 token sampler (one MI355X).
+
+Workload (BASELINE.json metric): sampled rows/s at V=152064, B=256 -- the
+Qwen2.5 configuration (top_k=0, top_p=0.95, T=1.0, rep=1.0, N(0,2^2)
+logits): the full-vocabulary path.  A "step" is one gs_sample_batch over the
+B resident rows.  Also reported: p50 us per single-row sample at V=32000
+(configuration c1, 256 sequential gs_sample calls, reference LCG stream,
+seed 42), the dominant kernel's HBM roofline fraction, and the CPU oracle
+(restatement of src/sampler.rs) timed on this host as a baseline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gguf-rs-cli_amd"))
+
+PEAK_HBM_GBS = 8000.0   # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bench_c3(gs, torch, steps, warmup):
+    import workloads
+    w = workloads.make("c3")
+    B, V = w["B"], w["V"]
+    d_lg = torch.from_numpy(w["logits"]).cuda()
+    d_u = torch.from_numpy(w["u"]).cuda()
+    d_tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    d_st = torch.zeros(B, dtype=torch.int32, device="cuda")
+    s = gs.Sampler(1.0, 0, 0.95, 1.0, seed=42)
+    s.reserve(B, V)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        s.sample_batch(d_lg, d_tok, u=d_u, status=d_st, stream=stream)
+    torch.cuda.synchronize()
+    assert int((d_st != 0).sum()) == 0, "sampler reported row errors"
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        s.sample_batch(d_lg, d_tok, u=d_u, status=d_st, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    per_row = workloads.algorithmic_bytes_per_row(V, 0)
+    tokens = d_tok.cpu().numpy().astype(np.int64)
+    return dict(B=B, V=V, ms=ms, bytes=per_row * B, tokens=tokens, w=w)
+
+
+def bench_c1_latency(gs, torch, steps=256):
+    import workloads
+    w = workloads.make("c1", steps=steps)
+    V, W = w["V"], w["W"]
+    d_lg = torch.from_numpy(w["logits"]).cuda()
+    d_win = torch.from_numpy(w["init_recent"].view(np.int32)).cuda().reshape(1, W)
+    d_tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = gs.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
+    torch.cuda.synchronize()
+    # warm up on a copy of the stream position, then restart at seed 42
+    for t in range(8):
+        s.sample(d_lg[t], d_win[0])
+    s.set_seed(w["seed"])
+    lat = []
+    toks = []
+    for t in range(steps):
+        t0 = time.perf_counter()
+        tok = s.sample(d_lg[t], d_win[0])
+        t1 = time.perf_counter()
+        lat.append((t1 - t0) * 1e6)
+        toks.append(tok)
+        d_tok.fill_(tok)
+        gs.window_push(d_win, d_tok, t)
+    torch.cuda.synchronize()
+    return dict(p50_us=statistics.median(lat), p90_us=sorted(lat)[int(0.9 * len(lat))],
+                tokens=np.array(toks), w=w)
+
+
+def kernel_only_c1(gs, torch, reps=200):
+    """Device time of one single-row kernel at V=32000 (batch entry, B=1)."""
+    import workloads
+    w = workloads.make("c1", steps=1)
+    d_lg = torch.from_numpy(w["logits"]).cuda()
+    d_win = torch.from_numpy(w["init_recent"].view(np.int32)).cuda().reshape(1, w["W"])
+    d_u = torch.zeros(1, dtype=torch.float32, device="cuda")
+    d_tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = gs.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
+    st = torch.cuda.current_stream()
+    for _ in range(10):
+        s.sample_batch(d_lg, d_tok, recent=d_win, u=d_u, stream=st)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(reps):
+        s.sample_batch(d_lg, d_tok, recent=d_win, u=d_u, stream=st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3
+
+
+def cpu_baseline(c3):
+    """The oracle (C restatement of src/sampler.rs, full sort per row) over
+    the whole c3 batch, once with all host threads (<= 16) and once on one
+    thread for a quarter of the rows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    w = c3["w"]
+    nthr = min(16, os.cpu_count() or 1)
+    t0 = oracle.now()
+    tok = oracle.sample_batch(w["logits"], w["params"], w["u"], nthreads=nthr)
+    t1 = oracle.now()
+    nb = w["B"] // 4
+    t2 = oracle.now()
+    oracle.sample_batch(w["logits"][:nb], w["params"][:nb], w["u"][:nb], nthreads=1)
+    t3 = oracle.now()
+    match = int((tok == c3["tokens"]).sum())
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=w["B"] / (t1 - t0), unit="rows/s", cores=nthr, kind="port",
+                sample="c3 batch: %d rows x V=%d, full sort per row (%d threads); "
+                       "1-thread on %d rows: %.1f rows/s; host %s, nproc %d"
+                       % (w["B"], w["V"], nthr, nb, nb / (t3 - t2), cpu_model, os.cpu_count()),
+                single_thread_rows_per_s=nb / (t3 - t2), gpu_tokens_match=match)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: the sampler's rows are independent and this "
+              "build runs on a single MI355X (--gpus %d not supported)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import gs_sampler as gs
+    gs.load_library()
+    torch.cuda.init()
+    c3 = bench_c3(gs, torch, args.steps, args.warmup)
+    log("c3: %.3f ms/step" % c3["ms"])
+    c1 = bench_c1_latency(gs, torch)
+    log("c1: p50 %.1f us" % c1["p50_us"])
+    c1k = kernel_only_c1(gs, torch)
+    log("c1 kernel: %.1f us" % c1k)
+    value = c3["B"] / (c3["ms"] / 1e3)
+    achieved = c3["bytes"] / (c3["ms"] / 1e3) / 1e9
+    out = {
+        "metric": "sampled rows/s at V=152064 B=256 (HBM GB/s, % peak); p50 us/row at V=32000 B=1",
+        "value": value,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": c3["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy N(0,2^2) logits resident in HBM)",
+        "config": {"workload": "c3 Qwen2.5 V=152064 B=256 top_k=0 top_p=0.95 T=1.0 rep=1.0",
+                   "global_batch": c3["B"], "vocab": c3["V"], "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "kernel": "gs::sample_rows_kernel", "bytes_per_launch": c3["bytes"]},
+        "c1_latency": {"p50_us": c1["p50_us"], "p90_us": c1["p90_us"], "kernel_us": c1k,
+                       "V": 32000, "B": 1, "steps": 256},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(c3)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,261 @@
+// gs_api.cpp -- C ABI of the gfx950 token sampler (declared in include/gs_sampler.h).
+//
+// Host side of the drop-in for gguf-rs-cli src/sampler.rs.  Owns the
+// sampler's LCG state (src/sampler.rs:3-12), device staging for the
+// single-row call and the scratch of the full-vocabulary path.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+#include <new>
+
+#include "../../include/gs_sampler.h"
+#include "gs_kernels.hpp"
+#include "gs_lcg.hpp"
+
+struct gs_sampler {
+    gs_params params;
+    uint64_t state;              // LCG state (pre-update value of the next draw)
+    int device;
+    hipStream_t stream;          // stream of the synchronous single-row call
+    float *d_row;                // staging for host logits
+    size_t row_cap;
+    uint32_t *d_rec;             // staging for host recent ids
+    size_t rec_cap;
+    uint32_t *h_tok;             // pinned, mapped: kernel writes the token here
+    int32_t *h_status;
+    uint32_t *d_tok_map;         // device aliases of h_tok / h_status
+    int32_t *d_status_map;
+    uint32_t *scratch;           // full-vocabulary path
+    size_t scratch_elems;
+};
+
+namespace {
+
+bool is_device_ptr(const void *p)
+{
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) { (void)hipGetLastError(); return false; }
+    return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged;
+}
+
+int grow(void **buf, size_t *cap, size_t need_bytes)
+{
+    if (*cap >= need_bytes) return GS_OK;
+    if (*buf) { (void)hipFree(*buf); *buf = nullptr; *cap = 0; }
+    if (hipMalloc(buf, need_bytes) != hipSuccess) { (void)hipGetLastError(); *buf = nullptr; return GS_ERR_NOMEM; }
+    *cap = need_bytes;
+    return GS_OK;
+}
+
+bool needs_full_path(const gs_params &p, size_t V)
+{
+    if (!(p.temperature > 0.0f) || V <= 1) return false;
+    size_t keep = (p.top_k > 0 && p.top_k < V) ? p.top_k : V;
+    return keep >= V || keep > (size_t)gs::kMaxTopK;
+}
+
+int reserve_scratch(gs_sampler *s, size_t rows, size_t V)
+{
+    size_t elems = rows * 4 * V;
+    size_t cap = s->scratch_elems * sizeof(uint32_t);
+    void *p = s->scratch;
+    int rc = grow(&p, &cap, elems * sizeof(uint32_t));
+    s->scratch = (uint32_t *)p;
+    s->scratch_elems = cap / sizeof(uint32_t);
+    return rc;
+}
+
+} // namespace
+
+extern "C" {
+
+int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out)
+{
+    if (!params || !out) return GS_ERR_INVALID;
+    *out = nullptr;
+    gs_sampler *s = new (std::nothrow) gs_sampler();
+    if (!s) return GS_ERR_NOMEM;
+    memset(s, 0, sizeof(*s));
+    s->params = *params;
+    s->state = seed;
+    if (hipGetDevice(&s->device) != hipSuccess) { delete s; return GS_ERR_HIP; }
+    if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) { delete s; return GS_ERR_HIP; }
+    if (hipHostMalloc((void **)&s->h_tok, 64, hipHostMallocMapped) != hipSuccess ||
+        hipHostGetDevicePointer((void **)&s->d_tok_map, s->h_tok, 0) != hipSuccess) {
+        gs_sampler_destroy(s);
+        return GS_ERR_HIP;
+    }
+    s->h_status = (int32_t *)(s->h_tok + 4);
+    s->d_status_map = (int32_t *)(s->d_tok_map + 4);
+    *out = s;
+    return GS_OK;
+}
+
+int gs_sampler_destroy(gs_sampler *s)
+{
+    if (!s) return GS_ERR_INVALID;
+    int dev;
+    (void)hipGetDevice(&dev);
+    (void)hipSetDevice(s->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->d_row) (void)hipFree(s->d_row);
+    if (s->d_rec) (void)hipFree(s->d_rec);
+    if (s->scratch) (void)hipFree(s->scratch);
+    if (s->h_tok) (void)hipHostFree(s->h_tok);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    (void)hipSetDevice(dev);
+    delete s;
+    return GS_OK;
+}
+
+int gs_sampler_set_params(gs_sampler *s, const gs_params *params)
+{
+    if (!s || !params) return GS_ERR_INVALID;
+    s->params = *params;
+    return GS_OK;
+}
+
+int gs_sampler_set_seed(gs_sampler *s, uint64_t seed)
+{
+    if (!s) return GS_ERR_INVALID;
+    s->state = seed;
+    return GS_OK;
+}
+
+int gs_sampler_get_state(const gs_sampler *s, uint64_t *state)
+{
+    if (!s || !state) return GS_ERR_INVALID;
+    *state = s->state;
+    return GS_OK;
+}
+
+int gs_sampler_set_state(gs_sampler *s, uint64_t state)
+{
+    if (!s) return GS_ERR_INVALID;
+    s->state = state;
+    return GS_OK;
+}
+
+int gs_sampler_reserve(gs_sampler *s, size_t B, size_t V)
+{
+    if (!s || V > GS_MAX_VOCAB) return GS_ERR_INVALID;
+    return reserve_scratch(s, B, V);
+}
+
+int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *recent, size_t W,
+              uint32_t *out_token)
+{
+    if (!s || !out_token || (V > 0 && !logits) || (W > 0 && !recent)) return GS_ERR_INVALID;
+    if (V > GS_MAX_VOCAB) return GS_ERR_UNSUPPORTED;
+    if (W > (size_t)gs::kMaxWindow) return GS_ERR_UNSUPPORTED;
+    int rc;
+    const float *d_logits = logits;
+    if (V > 0 && !is_device_ptr(logits)) {
+        void *p = s->d_row;
+        rc = grow(&p, &s->row_cap, V * sizeof(float));
+        s->d_row = (float *)p;
+        if (rc) return rc;
+        if (hipMemcpyAsync(s->d_row, logits, V * sizeof(float), hipMemcpyHostToDevice, s->stream) != hipSuccess)
+            return GS_ERR_HIP;
+        d_logits = s->d_row;
+    }
+    const uint32_t *d_rec = recent;
+    if (W > 0 && !is_device_ptr(recent)) {
+        void *p = s->d_rec;
+        rc = grow(&p, &s->rec_cap, W * sizeof(uint32_t));
+        s->d_rec = (uint32_t *)p;
+        if (rc) return rc;
+        if (hipMemcpyAsync(s->d_rec, recent, W * sizeof(uint32_t), hipMemcpyHostToDevice, s->stream) != hipSuccess)
+            return GS_ERR_HIP;
+        d_rec = s->d_rec;
+    }
+    if (needs_full_path(s->params, V) && (rc = reserve_scratch(s, 1, V))) return rc;
+    gs::RowArgs a;
+    memset(&a, 0, sizeof(a));
+    a.logits = d_logits ? d_logits : s->d_row;
+    a.ld = V;
+    a.V = (int)V;
+    a.params = nullptr;
+    a.uparams = s->params;
+    a.recent = W ? d_rec : nullptr;
+    a.ld_recent = W;
+    a.recent_len = nullptr;
+    a.W = (int)W;
+    a.u = nullptr;
+    a.lcg_state = s->state;
+    a.tokens = s->d_tok_map;
+    a.status = s->d_status_map;
+    a.scratch = s->scratch;
+    a.scratch_stride = 4 * V;
+    if (gs::launch_sample_rows(a, 1, s->stream) != hipSuccess) return GS_ERR_HIP;
+    if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
+    if (s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, 1);   // one draw iff T > 0
+    int st = *(volatile int32_t *)s->h_status;
+    if (st != GS_OK) return st;
+    *out_token = *(volatile uint32_t *)s->h_tok;
+    return GS_OK;
+}
+
+int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld,
+                    const gs_params *d_params, const uint32_t *d_recent, size_t ld_recent,
+                    const uint32_t *d_recent_len, size_t W, const float *d_u,
+                    uint32_t *d_tokens, int32_t *d_status, void *stream)
+{
+    if (!s || !d_tokens || (B > 0 && V > 0 && !d_logits) || ld < V) return GS_ERR_INVALID;
+    if (d_recent && ld_recent < W) return GS_ERR_INVALID;
+    if (!d_u && d_params) return GS_ERR_INVALID;   // LCG draws need host-known T per row
+    if (V > GS_MAX_VOCAB || B > 0x7fffffff) return GS_ERR_UNSUPPORTED;
+    if (d_recent && W > (size_t)gs::kMaxWindow) return GS_ERR_UNSUPPORTED;
+    if (B == 0) return GS_OK;
+    int rc;
+    if ((d_params || needs_full_path(s->params, V)) && (rc = reserve_scratch(s, B, V))) return rc;
+    gs::RowArgs a;
+    memset(&a, 0, sizeof(a));
+    a.logits = d_logits;
+    a.ld = ld;
+    a.V = (int)V;
+    a.params = d_params;
+    a.uparams = s->params;
+    a.recent = d_recent;
+    a.ld_recent = ld_recent;
+    a.recent_len = d_recent_len;
+    a.W = d_recent ? (int)W : 0;
+    a.u = d_u;
+    a.lcg_state = s->state;
+    a.tokens = d_tokens;
+    a.status = d_status;
+    a.scratch = s->scratch;
+    a.scratch_stride = 4 * V;
+    if (gs::launch_sample_rows(a, (int)B, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+    if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
+    return GS_OK;
+}
+
+int gs_window_push(uint32_t *d_window, size_t B, size_t ld, size_t W, size_t pos,
+                   const uint32_t *d_tokens, void *stream)
+{
+    if (!d_window || !d_tokens || W == 0 || ld < W || B > 0x7fffffff) return GS_ERR_INVALID;
+    if (B == 0) return GS_OK;
+    return gs::launch_window_push(d_window, (int)B, ld, (int)W, pos, d_tokens, (hipStream_t)stream) == hipSuccess
+               ? GS_OK : GS_ERR_HIP;
+}
+
+int gs_synth_logits(float *d_out, size_t B, size_t V, size_t ld, uint64_t seed, uint64_t counter0,
+                    float sigma, void *stream)
+{
+    if (!d_out || ld < V || B > 0x7fffffff || V > 0x7fffffff) return GS_ERR_INVALID;
+    if (B == 0 || V == 0) return GS_OK;
+    return gs::launch_synth(d_out, (int)B, (int)V, ld, seed, counter0, sigma, (hipStream_t)stream) == hipSuccess
+               ? GS_OK : GS_ERR_HIP;
+}
+
+int gs_limits(uint32_t *max_vocab, uint32_t *max_window)
+{
+    if (max_vocab) *max_vocab = GS_MAX_VOCAB;
+    if (max_window) *max_window = (uint32_t)gs::kMaxWindow;
+    return GS_OK;
+}
+
+const char *gs_version(void) { return "gs_sampler 0.1 gfx950"; }
+
+} // extern "C"

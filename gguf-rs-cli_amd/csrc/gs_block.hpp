@@ -1,0 +1,219 @@
+// gs_block.hpp -- block-level building blocks (1024 threads = 16 wave64).
+#pragma once
+#include "gs_device.hpp"
+
+namespace gs {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+__device__ __forceinline__ uint64_t lanemask_lt() { return (1ull << lane_id()) - 1ull; }
+
+// ---------------------------------------------------------------------------
+// Exact emulation of a sequential f32 running sum.
+//
+// The reference accumulates in f32, one element at a time, in sorted order
+// (src/sampler.rs:54 softmax sum, :61-63 nucleus cumsum, :67 renormalising sum,
+// :74-75 multinomial CDF).  Sequential rounding is order dependent, so a tree
+// reduction would not reproduce it.  It can still be evaluated in parallel:
+//
+// While the running sum s stays inside one binade [2^e, 2^(e+1)), every
+// partial sum is an integer multiple of g = 2^(e-23), and
+//     RN(s + a) = s + g * RNE_g(a)
+// where RNE_g(a) is a rounded to an integer count of g.  Rounding ties (a an
+// odd multiple of g/2) go to the even mantissa, so they depend only on the
+// parity of s/g.  Hence, inside a binade, the sum is a prefix sum of integers
+// whose elements are functions of one parity bit: f(p) = K + ((p + K) & 1) for
+// a tie, f(p) = k otherwise.  Such functions compose associatively,
+//     (f;h)(p) = f(p) + h((p + f(p)) & 1),
+// so a block-wide scan gives every partial sum exactly.  The first element
+// whose partial sum would leave the binade is evaluated with one real f32
+// add, and the scan restarts from there.  The number of restarts is bounded
+// by the number of binades the sum passes through (about 30 for p-sums).
+//
+// Subnormal sums need no special case: [0, 2^-125) has the single grid 2^-149,
+// which is the e = -126 case.
+// ---------------------------------------------------------------------------
+struct ParFn { uint32_t f0, f1; };               // increment for parity 0 / 1
+constexpr uint32_t kSat = 1u << 25;              // saturate: past any crossing
+
+__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b)
+{
+    uint32_t s = a + b;
+    return s > kSat ? kSat : s;
+}
+__device__ __forceinline__ uint32_t par_apply(const ParFn &f, uint32_t p) { return p ? f.f1 : f.f0; }
+__device__ __forceinline__ ParFn par_compose(const ParFn &a, const ParFn &b)
+{
+    ParFn r;
+    r.f0 = sat_add(a.f0, par_apply(b, (a.f0) & 1u));
+    r.f1 = sat_add(a.f1, par_apply(b, (1u + a.f1) & 1u));
+    return r;
+}
+
+// Binade exponent used for the grid of s (s >= 0, finite); subnormals -> -126.
+__device__ __forceinline__ int grid_exp(float s)
+{
+    int e = (int)((__float_as_uint(s) >> 23) & 0xff) - 127;
+    return e < -126 ? -126 : e;
+}
+
+// Increment function of summand a at grid exponent e.
+__device__ __forceinline__ ParFn elem_fn(float a, int e)
+{
+    float m = ldexpf(a, 23 - e);           // exact power-of-two scaling
+    ParFn f;
+    if (!(m < (float)kSat)) { f.f0 = f.f1 = kSat; return f; }
+    float fl = floorf(m);
+    float fr = m - fl;                      // exact
+    uint32_t K = (uint32_t)fl;
+    if (fr == 0.5f) { f.f0 = K + (K & 1u); f.f1 = K + ((K + 1u) & 1u); }
+    else { uint32_t k = K + (fr > 0.5f ? 1u : 0u); f.f0 = f.f1 = k; }
+    return f;
+}
+
+struct SeqSmem {
+    ParFn wave_tot[kWaves];
+    int first;
+    float s;
+    int start;
+};
+
+// Block-wide exclusive scan of ParFn in thread order; returns the exclusive
+// prefix for this thread.
+__device__ __forceinline__ ParFn block_scan_excl(ParFn v, SeqSmem &sm)
+{
+    const int lane = lane_id(), w = wave_id();
+    ParFn incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        ParFn o;
+        o.f0 = __shfl_up(incl.f0, d, 64);
+        o.f1 = __shfl_up(incl.f1, d, 64);
+        if (lane >= d) incl = par_compose(o, incl);
+    }
+    if (lane == 63) sm.wave_tot[w] = incl;
+    __syncthreads();
+    ParFn pre = {0u, 0u};
+    for (int i = 0; i < w; i++) pre = par_compose(pre, sm.wave_tot[i]);
+    ParFn ex;
+    ex.f0 = __shfl_up(incl.f0, 1, 64);
+    ex.f1 = __shfl_up(incl.f1, 1, 64);
+    if (lane == 0) { ex.f0 = 0u; ex.f1 = 0u; }
+    return par_compose(pre, ex);
+}
+
+// Sequential accumulation s_{j+1} = RN(s_j + a(j)), j in [0, n), s_0 = s_init,
+// stopping at the first j with pred(s_{j+1}).  Returns that j (or n) and the
+// running sum at the stop (or at the end) in *s_out.  `a` must be a pure
+// function of j; it is evaluated by several threads.  All threads must call.
+constexpr int kSeqPer = 4;                        // elements per thread per tile
+template <class LoadA, class Pred>
+__device__ int block_seqsum(LoadA a, int n, float s_init, Pred pred, float *s_out, SeqSmem &sm)
+{
+    const int t = threadIdx.x;
+    float s = s_init;
+    int pos = 0;
+    // Leading steps from s == 0 are done one at a time (0 + a == a exactly).
+    while (pos < n && s == 0.0f) {
+        s = s + a(pos);
+        if (pred(s)) { *s_out = s; return pos; }
+        pos++;
+    }
+    const int tile = kThreads * kSeqPer;
+    while (pos < n) {
+        const int tend = min(pos + tile, n);
+        float av[kSeqPer];
+#pragma unroll
+        for (int q = 0; q < kSeqPer; q++) {
+            int j = pos + t * kSeqPer + q;
+            av[q] = (j < tend) ? a(j) : 0.0f;
+        }
+        int start = pos;
+        for (;;) {
+            const int e = grid_exp(s);
+            const uint32_t M = (uint32_t)ldexpf(s, 23 - e);   // exact, < 2^24
+            ParFn fn[kSeqPer];
+            ParFn loc = {0u, 0u};
+#pragma unroll
+            for (int q = 0; q < kSeqPer; q++) {
+                int j = pos + t * kSeqPer + q;
+                if (j >= start && j < tend) fn[q] = elem_fn(av[q], e);
+                else { fn[q].f0 = 0u; fn[q].f1 = 0u; }
+                loc = par_compose(loc, fn[q]);
+            }
+            if (t == 0) sm.first = 0x7fffffff;
+            ParFn ex = block_scan_excl(loc, sm);   // contains a barrier
+            // Walk my elements.
+            const uint32_t pM = M & 1u;
+            uint32_t before = par_apply(ex, pM);
+            int my_first = 0x7fffffff;
+#pragma unroll
+            for (int q = 0; q < kSeqPer; q++) {
+                int j = pos + t * kSeqPer + q;
+                uint32_t inc = par_apply(fn[q], (pM + before) & 1u);
+                uint32_t after = sat_add(before, inc);
+                if (j >= start && j < tend && my_first == 0x7fffffff) {
+                    bool cross = (M + after) >= (1u << 24);
+                    bool stop = !cross && pred(ldexpf((float)(M + after), e - 23));
+                    if (cross || stop) my_first = j;
+                }
+                before = after;
+            }
+            if (my_first != 0x7fffffff) atomicMin(&sm.first, my_first);
+            __syncthreads();
+            const int first = sm.first;
+            if (first == 0x7fffffff) {
+                // Whole remainder of the tile stays in the binade: the thread
+                // owning the last element publishes the new sum.
+                int last = tend - 1;
+                int owner = (last - pos) / kSeqPer;
+                if (t == owner) {
+                    uint32_t b2 = par_apply(ex, pM);
+#pragma unroll
+                    for (int q = 0; q < kSeqPer; q++) {
+                        int j = pos + t * kSeqPer + q;
+                        if (j <= last) b2 = sat_add(b2, par_apply(fn[q], (pM + b2) & 1u));
+                    }
+                    sm.s = ldexpf((float)(M + b2), e - 23);
+                }
+                __syncthreads();
+                s = sm.s;
+                __syncthreads();
+                break;
+            }
+            // Event at `first`: the owner evaluates it exactly.
+            int owner = (first - pos) / kSeqPer;
+            if (t == owner) {
+                uint32_t b2 = par_apply(ex, pM);
+                float sb = s;
+                float sa = s;
+#pragma unroll
+                for (int q = 0; q < kSeqPer; q++) {
+                    int j = pos + t * kSeqPer + q;
+                    if (j >= start && j < first) b2 = sat_add(b2, par_apply(fn[q], (pM + b2) & 1u));
+                    if (j == first) {
+                        sb = ldexpf((float)(M + b2), e - 23);  // exact sum before `first`
+                        sa = sb + av[q];                        // the reference's f32 add
+                    }
+                }
+                sm.s = sa;
+                sm.start = pred(sa) ? -1 - first : first + 1;
+            }
+            __syncthreads();
+            s = sm.s;
+            const int nxt = sm.start;
+            __syncthreads();
+            if (nxt < 0) { *s_out = s; return -1 - nxt; }
+            start = nxt;
+            if (start >= tend) break;
+        }
+        pos = tend;
+    }
+    *s_out = s;
+    return n;
+}
+
+} // namespace gs

@@ -1,0 +1,36 @@
+// gs_kernels.hpp -- launch interface between the C ABI and the kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/gs_sampler.h"
+
+namespace gs {
+
+constexpr int kMaxWindow = 1024;   // unique penalized ids held in the LDS hash
+constexpr int kMaxTopK = 1024;     // largest k served by the LDS top-k path
+
+struct RowArgs {
+    const float *logits;
+    size_t ld;
+    int V;
+    const gs_params *params;       // per row, or null
+    gs_params uparams;             // used when params == null
+    const uint32_t *recent;
+    size_t ld_recent;
+    const uint32_t *recent_len;
+    int W;
+    const float *u;                // per-row draws, or null
+    uint64_t lcg_state;            // used when u == null: row b draws jump(state, b)
+    uint32_t *tokens;
+    int32_t *status;
+    uint32_t *scratch;             // full-vocabulary path: 4*V u32 per row
+    size_t scratch_stride;         // u32 elements per row
+};
+
+hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st);
+hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
+                              const uint32_t *tok, hipStream_t st);
+hipError_t launch_synth(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0,
+                        float sigma, hipStream_t st);
+
+} // namespace gs

@@ -1,0 +1,261 @@
+"""Python host binding of the gfx950 token sampler (libgs_sampler.so).
+
+Mirrors the reference interface of gguf-rs-cli's src/sampler.rs:
+
+    set_seed(s)                                          src/sampler.rs:5
+    sample(logits, temperature, top_k, top_p,
+           rep_penalty, recent) -> int                   src/sampler.rs:35-36
+
+with the same argument meaning, the same process-global LCG stream
+(one draw per call iff temperature > 0) and errors where the reference
+panics (NaN logits, empty logits with T > 0).  It adds the `Sampler`
+object (construction = params + seed) and a batched entry over B rows of
+device-resident logits.
+
+The library must be built (gguf-rs-cli_amd/build.py).  There is no CPU
+fallback: if the HIP library is missing, importing this module fails.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgs_sampler.so")
+
+GS_OK = 0
+GS_ERR_INVALID = -1
+GS_ERR_EMPTY = -2
+GS_ERR_NAN = -3
+GS_ERR_HIP = -5
+GS_ERR_NOMEM = -6
+GS_ERR_UNSUPPORTED = -7
+_ERRNAMES = {
+    GS_ERR_INVALID: "invalid argument",
+    GS_ERR_EMPTY: "empty logits (reference panics at pairs[0], src/sampler.rs:53)",
+    GS_ERR_NAN: "NaN logit (reference panics in partial_cmp().unwrap(), src/sampler.rs:17,45)",
+    GS_ERR_HIP: "HIP runtime error",
+    GS_ERR_NOMEM: "device allocation failed",
+    GS_ERR_UNSUPPORTED: "outside implemented limits",
+}
+
+# Symbols declared in include/gs_sampler.h.
+EXPORTS = [
+    "gs_sampler_create", "gs_sampler_destroy", "gs_sampler_set_params",
+    "gs_sampler_set_seed", "gs_sampler_get_state", "gs_sampler_set_state",
+    "gs_sampler_reserve", "gs_sample", "gs_sample_batch", "gs_window_push",
+    "gs_synth_logits", "gs_limits", "gs_version",
+]
+
+
+class SamplerError(RuntimeError):
+    def __init__(self, code, where=""):
+        self.code = code
+        super().__init__("%s: %s (%d)" % (where or "gs_sampler", _ERRNAMES.get(code, "error"), code))
+
+
+class GsParams(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_uint32),
+                ("top_p", ctypes.c_float), ("rep_penalty", ctypes.c_float)]
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    """Load libgs_sampler.so (raises OSError if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise OSError("libgs_sampler.so not built: run gguf-rs-cli_amd/build.py (%s)" % path)
+    lib = ctypes.CDLL(path)
+    P, U64, SZ, I = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_size_t, ctypes.c_int
+    sig = {
+        "gs_sampler_create": ([ctypes.POINTER(GsParams), U64, ctypes.POINTER(P)], I),
+        "gs_sampler_destroy": ([P], I),
+        "gs_sampler_set_params": ([P, ctypes.POINTER(GsParams)], I),
+        "gs_sampler_set_seed": ([P, U64], I),
+        "gs_sampler_get_state": ([P, ctypes.POINTER(U64)], I),
+        "gs_sampler_set_state": ([P, U64], I),
+        "gs_sampler_reserve": ([P, SZ, SZ], I),
+        "gs_sample": ([P, P, SZ, P, SZ, ctypes.POINTER(ctypes.c_uint32)], I),
+        "gs_sample_batch": ([P, P, SZ, SZ, SZ, P, P, SZ, P, SZ, P, P, P, P], I),
+        "gs_window_push": ([P, SZ, SZ, SZ, SZ, P, P], I),
+        "gs_synth_logits": ([P, SZ, SZ, SZ, U64, U64, ctypes.c_float, P], I),
+        "gs_limits": ([ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)], I),
+        "gs_version": ([], ctypes.c_char_p),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = lib
+    return lib
+
+
+def _check(rc, where):
+    if rc != GS_OK:
+        raise SamplerError(rc, where)
+
+
+def _ptr(x):
+    """Device/host address of a torch tensor, numpy array, int or None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    if hasattr(x, "ctypes"):
+        return x.ctypes.data
+    raise TypeError("unsupported buffer type %r" % type(x))
+
+
+def _stream_handle(stream):
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream  # torch.cuda.Stream
+
+
+class Sampler:
+    """Sampler construction of the drop-in: the four scalars of
+    src/sampler.rs:35-36 plus the LCG seed of src/sampler.rs:3-5.
+    Defaults are the reference CLI's (src/main.rs:24-31, 48-49)."""
+
+    def __init__(self, temperature=0.7, top_k=40, top_p=0.9, rep_penalty=1.1, seed=42):
+        self._lib = load_library()
+        self._h = ctypes.c_void_p()
+        self.params = GsParams(temperature, top_k, top_p, rep_penalty)
+        _check(self._lib.gs_sampler_create(ctypes.byref(self.params), seed, ctypes.byref(self._h)),
+               "gs_sampler_create")
+
+    def close(self):
+        if self._h:
+            self._lib.gs_sampler_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_params(self, temperature, top_k, top_p, rep_penalty):
+        self.params = GsParams(temperature, top_k, top_p, rep_penalty)
+        _check(self._lib.gs_sampler_set_params(self._h, ctypes.byref(self.params)), "set_params")
+
+    def set_seed(self, seed):
+        _check(self._lib.gs_sampler_set_seed(self._h, seed), "set_seed")
+
+    @property
+    def state(self):
+        v = ctypes.c_uint64()
+        _check(self._lib.gs_sampler_get_state(self._h, ctypes.byref(v)), "get_state")
+        return v.value
+
+    @state.setter
+    def state(self, v):
+        _check(self._lib.gs_sampler_set_state(self._h, v), "set_state")
+
+    def reserve(self, B, V):
+        _check(self._lib.gs_sampler_reserve(self._h, B, V), "reserve")
+
+    def sample(self, logits, recent=()):
+        """sample(logits, recent) -> token; logits: numpy f32 (host) or a
+        torch f32 tensor (host or device).  Synchronous."""
+        import numpy as np
+        keep = []
+        if isinstance(logits, (list, tuple)):
+            logits = np.asarray(logits, dtype=np.float32)
+        if hasattr(logits, "dtype") and str(logits.dtype) not in ("float32", "torch.float32"):
+            raise TypeError("logits must be float32")
+        if hasattr(logits, "is_contiguous") and not logits.is_contiguous():
+            raise TypeError("logits must be contiguous")
+        if isinstance(logits, np.ndarray):
+            logits = np.ascontiguousarray(logits)
+            keep.append(logits)
+        V = int(logits.numel() if hasattr(logits, "numel") else logits.size)
+        if recent is None or (not hasattr(recent, "data_ptr") and not hasattr(recent, "ctypes")):
+            recent = np.ascontiguousarray(np.asarray(list(recent or ()), dtype=np.uint32))
+        keep.append(recent)
+        W = int(recent.numel() if hasattr(recent, "numel") else recent.size)
+        out = ctypes.c_uint32()
+        _check(self._lib.gs_sample(self._h, _ptr(logits), V, _ptr(recent) if W else None, W,
+                                   ctypes.byref(out)), "gs_sample")
+        return int(out.value)
+
+    def sample_batch(self, logits, tokens, params=None, recent=None, recent_len=None,
+                     u=None, status=None, stream=None, V=None, ld=None, W=None, ld_recent=None):
+        """Batched sampling over B device rows (torch tensors on cuda).
+        logits [B, ld] f32; tokens [B] int32/uint32; params [B, 4]-shaped
+        gs_params buffer (or None); recent [B, ld_recent] uint32 ids (or None);
+        u [B] f32 draws (or None = this sampler's LCG stream).  Asynchronous."""
+        B = int(logits.shape[0])
+        V = int(logits.shape[1]) if V is None else V
+        # a size-1 leading dimension may carry any stride (numpy gives 0)
+        ld = (int(logits.stride(0)) if B > 1 else V) if ld is None else ld
+        if recent is not None:
+            W = int(recent.shape[1]) if W is None else W
+            if ld_recent is None:
+                ld_recent = int(recent.stride(0)) if recent.shape[0] > 1 else W
+        else:
+            W, ld_recent = 0, 0
+        _check(self._lib.gs_sample_batch(
+            self._h, _ptr(logits), B, V, ld, _ptr(params), _ptr(recent), ld_recent,
+            _ptr(recent_len), W, _ptr(u), _ptr(tokens), _ptr(status),
+            _stream_handle(stream)), "gs_sample_batch")
+
+
+def window_push(window, tokens, pos, W=None, stream=None):
+    lib = load_library()
+    B = int(window.shape[0])
+    W = int(window.shape[1]) if W is None else W
+    ld = int(window.stride(0)) if B > 1 else int(window.shape[1])
+    _check(lib.gs_window_push(_ptr(window), B, ld, W, pos, _ptr(tokens),
+                              _stream_handle(stream)), "gs_window_push")
+
+
+def synth_logits(out, seed, counter0, sigma, V=None, stream=None):
+    lib = load_library()
+    B = int(out.shape[0])
+    V = int(out.shape[1]) if V is None else V
+    ld = int(out.stride(0)) if B > 1 else int(out.shape[1])
+    _check(lib.gs_synth_logits(_ptr(out), B, V, ld, seed, counter0, sigma,
+                               _stream_handle(stream)), "gs_synth_logits")
+
+
+def params_array(rows):
+    """Pack [(T, top_k, top_p, rep), ...] as a numpy structured array whose
+    bytes are B gs_params (16 bytes each)."""
+    import numpy as np
+    dt = np.dtype([("temperature", "<f4"), ("top_k", "<u4"), ("top_p", "<f4"), ("rep_penalty", "<f4")])
+    return np.array([tuple(r) for r in rows], dtype=dt)
+
+
+# ---- the reference's free-function API over a process-global sampler -----
+_global = None
+_global_seed = 12345  # src/sampler.rs:3
+
+
+def _get_global():
+    global _global
+    if _global is None:
+        _global = Sampler(0.7, 40, 0.9, 1.1, seed=_global_seed)
+    return _global
+
+
+def set_seed(s):
+    """src/sampler.rs:5"""
+    global _global_seed
+    _global_seed = s
+    if _global is not None:
+        _global.set_seed(s)
+
+
+def sample(logits, temperature, top_k, top_p, rep_penalty, recent):
+    """src/sampler.rs:35-36 -- returns the token id.  Raises SamplerError
+    where the reference panics."""
+    g = _get_global()
+    g.set_params(temperature, top_k, top_p, rep_penalty)
+    return g.sample(logits, recent)

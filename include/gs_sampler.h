@@ -1,0 +1,127 @@
+/*
+ * gs_sampler.h -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * Drop-in for gguf-rs-cli's sampler (src/sampler.rs).  The reference API is a
+ * crate-internal Rust free function plus a process-global LCG:
+ *
+ *   pub fn set_seed(s: u64)                                  src/sampler.rs:5
+ *   pub fn sample(logits: &mut Vec<f32>, temperature: f32,
+ *                 top_k: usize, top_p: f32, rep_penalty: f32,
+ *                 recent: &[u32]) -> usize                   src/sampler.rs:35-36
+ *
+ * Its one caller is the decode loop, src/main.rs:280 (seed set at :54).
+ * Every entry point returns an int status: GS_OK (0) or a negative GS_ERR_*.
+ * The statuses stand in for the reference's panics: NaN logits
+ * (src/sampler.rs:17,45 partial_cmp().unwrap()) and empty logits with T > 0
+ * (src/sampler.rs:53 pairs[0]).
+ *
+ * Buffers are caller-owned.  Batched calls are asynchronous and ordered on
+ * the given HIP stream (NULL = the default stream).  No torch types appear in
+ * this interface.
+ */
+#ifndef GS_SAMPLER_H
+#define GS_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_OK               0
+#define GS_ERR_INVALID    (-1)  /* bad argument (null pointer, size out of range) */
+#define GS_ERR_EMPTY      (-2)  /* V == 0 with T > 0: reference panics at pairs[0] */
+#define GS_ERR_NAN        (-3)  /* NaN logit with V > 1: reference panics in partial_cmp */
+#define GS_ERR_HIP        (-5)  /* a HIP runtime call failed */
+#define GS_ERR_NOMEM      (-6)  /* device allocation failed */
+#define GS_ERR_UNSUPPORTED (-7) /* request outside the implemented limits */
+
+/* Sampler parameters: the four scalars of src/sampler.rs:35-36 (16 bytes).
+ * Defaults of the reference CLI (src/main.rs:24-31): T 0.7, k 40, p 0.9, rep 1.1. */
+typedef struct gs_params {
+    float temperature;  /* <= 0: greedy (src/sampler.rs:39) */
+    uint32_t top_k;     /* 0 or >= V: no truncation (src/sampler.rs:48-50) */
+    float top_p;        /* >= 1: no nucleus cut (src/sampler.rs:59) */
+    float rep_penalty;  /* == 1: no penalty (src/sampler.rs:24) */
+} gs_params;
+
+typedef struct gs_sampler gs_sampler;
+
+/* Library limits (also returned by gs_limits). */
+#define GS_MAX_VOCAB   (1u << 22)  /* 4,194,304 logits per row */
+#define GS_MAX_WINDOW  1024u       /* recent-window length per row */
+
+/* ---- sampler object: "Sampler construction" of the drop-in -------------
+ * Replaces set_seed (src/sampler.rs:5) plus the four scalars the caller
+ * passes on every call (src/main.rs:280).  `seed` initialises the sampler's
+ * own copy of the reference LCG (src/sampler.rs:3-12).  The sampler binds to
+ * the HIP device current at creation. */
+int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out);
+int gs_sampler_destroy(gs_sampler *s);
+int gs_sampler_set_params(gs_sampler *s, const gs_params *params);
+/* set_seed (src/sampler.rs:5) for this sampler's stream. */
+int gs_sampler_set_seed(gs_sampler *s, uint64_t seed);
+/* Raw LCG state, so a decode trace can be checkpointed and resumed. */
+int gs_sampler_get_state(const gs_sampler *s, uint64_t *state);
+int gs_sampler_set_state(gs_sampler *s, uint64_t state);
+
+/* Pre-allocate the full-vocabulary scratch (16*V bytes per row) for batches
+ * of up to B rows, e.g. before capturing gs_sample_batch into a HIP graph
+ * (the batch call otherwise allocates on first use). */
+int gs_sampler_reserve(gs_sampler *s, size_t B, size_t V);
+
+/* ---- single row: sample(logits, recent) -> token -------------------------
+ * Replaces sampler::sample (src/sampler.rs:35-79) at its call site
+ * src/main.rs:280.  `logits` and `recent` may be host or device pointers.
+ * One LCG draw is consumed iff temperature > 0, as in the reference.
+ * Synchronous: returns after the token is in *out_token.
+ * Unlike the reference, `logits` is not modified (the reference leaves it
+ * penalized and divided by T; its only caller discards it, src/main.rs:305). */
+int gs_sample(gs_sampler *s, const float *logits, size_t V,
+              const uint32_t *recent, size_t W, uint32_t *out_token);
+
+/* ---- batched: B independent rows (new; no reference counterpart beyond
+ * calling src/sampler.rs:35 once per row) ----------------------------------
+ * d_logits   : device, row b at d_logits + b*ld (ld >= V), f32.
+ * d_params   : device, B gs_params (heterogeneous rows), or NULL = the
+ *              sampler's params for every row.
+ * d_recent   : device, row b's window at d_recent + b*ld_recent, or NULL.
+ * d_recent_len: device, B lengths (<= W), or NULL = W for every row.
+ * d_u        : device, B uniform draws in [0,1), or NULL = the sampler's LCG
+ *              stream (row b gets the b-th next draw; the host state advances
+ *              by B if T > 0, by 0 if T <= 0).  NULL requires d_params NULL.
+ * d_tokens   : device, B uint32 outputs.
+ * d_status   : device, B int32 per-row statuses (GS_OK/GS_ERR_NAN/...), or NULL.
+ * stream     : hipStream_t (NULL = default stream).
+ * Scratch for rows that need the full-vocabulary path is owned by the
+ * sampler and grows on demand (allocation happens outside kernels, before
+ * the launch). */
+int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V,
+                    size_t ld, const gs_params *d_params,
+                    const uint32_t *d_recent, size_t ld_recent,
+                    const uint32_t *d_recent_len, size_t W, const float *d_u,
+                    uint32_t *d_tokens, int32_t *d_status, void *stream);
+
+/* ---- device-resident decode helpers (decode loop, src/main.rs:279-311) ---
+ * Append each row's token to its ring window: window[b*ld + (pos % W)] =
+ * tokens[b].  The penalty only depends on how often each id occurs in the
+ * window, so a ring is equivalent to the reference's FIFO (src/main.rs:302-303)
+ * once the window is full. */
+int gs_window_push(uint32_t *d_window, size_t B, size_t ld, size_t W, size_t pos,
+                   const uint32_t *d_tokens, void *stream);
+
+/* Synthetic logits for device-resident benchmarks and tests:
+ * out[b*ld + c] = sigma * IrwinHall4(splitmix64(seed ^ splitmix64(counter0 + b*V + c))).
+ * Deterministic and reproducible on the host. */
+int gs_synth_logits(float *d_out, size_t B, size_t V, size_t ld, uint64_t seed,
+                    uint64_t counter0, float sigma, void *stream);
+
+/* Library limits and build identification. */
+int gs_limits(uint32_t *max_vocab, uint32_t *max_window);
+const char *gs_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GS_SAMPLER_H */

@@ -1,0 +1,242 @@
+"""GPU parity: the HIP sampler (through the C ABI) against the CPU oracle on
+the same seeded inputs.  Integer outputs (token ids) must be identical.
+
+The oracle's tie order (value descending, index ascending) stands in for the
+reference's unspecified sort_unstable_by order on equal keys (src/sampler.rs:45).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _t
+    if not _t.cuda.is_available():
+        pytest.skip("no GPU")
+    return _t
+
+
+def run_batch(gs, torch, logits, params=None, u=None, recent=None, uniform=None, seed=0):
+    """Sample B rows on the GPU; returns (tokens int64 numpy, status numpy)."""
+    B, V = logits.shape
+    d_lg = torch.from_numpy(np.ascontiguousarray(logits)).cuda()
+    d_tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    d_st = torch.full((B,), 99, dtype=torch.int32, device="cuda")
+    d_u = torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).cuda() if u is not None else None
+    d_rec = torch.from_numpy(np.ascontiguousarray(recent, dtype=np.uint32).view(np.int32)).cuda() \
+        if recent is not None else None
+    d_pr = None
+    if params is not None:
+        d_pr = torch.from_numpy(np.ascontiguousarray(params).view(np.uint8)).cuda()
+    up = uniform or (0.7, 40, 0.9, 1.1)
+    s = gs.Sampler(*up, seed=seed)
+    s.sample_batch(d_lg, d_tok, params=d_pr, recent=d_rec, u=d_u, status=d_st)
+    torch.cuda.synchronize()
+    tok = d_tok.cpu().numpy().astype(np.int64)
+    st = d_st.cpu().numpy()
+    return tok, st, s
+
+
+def check_tokens(name, got, want, st=None):
+    if st is not None:
+        assert (st == 0).all(), (name, np.unique(st))
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, "%s: %d/%d rows differ, first %s got %s want %s" % (
+        name, bad.size, got.size, bad[:5], got[bad[:5]], want[bad[:5]])
+
+
+# --- golden vectors (independent pure-Python restatement) ---------------------
+def test_golden_cases(gpu, torch):
+    import json, os
+    cases = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "sampler_cases.json")))
+    for c in cases:
+        _say("golden", c["name"], "V", len(c["logits"]))
+        x = np.array([c["logits"]], np.float32)
+        rec = np.array([c["recent"]], np.uint32) if c["recent"] else None
+        tok, st, _ = run_batch(gpu, torch, x, u=[c["u"]], recent=rec,
+                               uniform=(c["T"], c["k"], c["p"], c["rep"]))
+        assert st[0] == 0, c["name"]
+        assert tok[0] == c["token"], (c["name"], tok[0], c["token"])
+
+
+# --- the five configurations (row counts reduced where the oracle is slow) ---
+def test_c2_llama3(gpu, torch, oracle):
+    import workloads
+    w = workloads.make("c2", B=16)
+    _say("c2 B=16 V", w["V"])
+    tok, st, _ = run_batch(gpu, torch, w["logits"], params=w["params"], u=w["u"], recent=w["recent"])
+    want = oracle.sample_batch(w["logits"], w["params"], w["u"], recent=w["recent"], nthreads=8,
+                               fast_topk=True)
+    check_tokens("c2", tok, want, st)
+
+
+def test_c3_qwen_full_vocab(gpu, torch, oracle):
+    import workloads
+    w = workloads.make("c3", B=6)
+    _say("c3 B=6 V", w["V"])
+    tok, st, _ = run_batch(gpu, torch, w["logits"], params=w["params"], u=w["u"])
+    want = oracle.sample_batch(w["logits"], w["params"], w["u"], nthreads=6)
+    check_tokens("c3", tok, want, st)
+
+
+def test_c4_gemma_hetero(gpu, torch, oracle):
+    import workloads
+    w = workloads.make("c4", B=16)
+    _say("c4 B=16 V", w["V"], "k", list(w["params"]["top_k"]))
+    tok, st, _ = run_batch(gpu, torch, w["logits"], params=w["params"], u=w["u"], recent=w["recent"])
+    want = oracle.sample_batch(w["logits"], w["params"], w["u"], recent=w["recent"], nthreads=8)
+    check_tokens("c4", tok, want, st)
+    # top_k == 1 rows are the argmax of the penalized, scaled logits
+    for b in np.nonzero(w["params"]["top_k"] == 1)[0]:
+        assert tok[b] == want[b]
+
+
+def test_c1_decode_trace(gpu, torch, oracle):
+    """Sequential single-row calls on the sampler's own LCG stream (seed 42)."""
+    import workloads
+    w = workloads.make("c1", steps=64)
+    _say("c1 steps", w["steps"])
+    s = gpu.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
+    recent = list(w["init_recent"])
+    got = []
+    for t in range(w["steps"]):
+        tok = s.sample(w["logits"][t], np.array(recent, np.uint32))
+        got.append(tok)
+        recent.append(tok)
+        if len(recent) > w["W"]:
+            recent.pop(0)
+    want = oracle.decode_trace(w["logits"], w["T"], w["k"], w["p"], w["rep"], w["W"],
+                               w["init_recent"], w["seed"])
+    check_tokens("c1", np.array(got), want)
+    _, st = workloads.lcg_stream(w["seed"], w["steps"])
+    assert s.state == st
+
+
+def test_c5_device_loop(gpu, torch, oracle):
+    """Device-resident loop: on-device logits, ring window, LCG draws."""
+    import workloads
+    w = workloads.make("c5", B=4, steps=6)
+    B, V, W, steps = w["B"], w["V"], w["W"], w["steps"]
+    _say("c5 B", B, "steps", steps)
+    d_lg = torch.empty((B, V), dtype=torch.float32, device="cuda")
+    d_win = torch.from_numpy(w["window"].view(np.int32)).cuda()
+    d_tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    s = gpu.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
+    toks = []
+    for t in range(steps):
+        gpu.synth_logits(d_lg, w["synth_seed"], t * B * V, w["sigma"])
+        s.sample_batch(d_lg, d_tok, recent=d_win)
+        gpu.window_push(d_win, d_tok, t)
+        toks.append(d_tok.cpu().numpy().astype(np.int64))
+    u, _ = workloads.lcg_stream(w["seed"], steps * B)
+    want, win = oracle.device_loop(B, V, steps, w["synth_seed"], w["sigma"],
+                                   (w["T"], w["k"], w["p"], w["rep"]), w["window"], u, nthreads=4)
+    check_tokens("c5", np.array(toks), want)
+    assert (d_win.cpu().numpy().view(np.uint32) == win).all()
+
+
+def test_synth_matches_host(gpu, torch, oracle):
+    d = torch.empty((3, 1000), dtype=torch.float32, device="cuda")
+    gpu.synth_logits(d, 77, 5, 3.0)
+    h = oracle.synth_logits(3000, 77, 5, 3.0).reshape(3, 1000)
+    assert (d.cpu().numpy().view(np.uint32) == h.view(np.uint32)).all()
+
+
+# --- edge cases the reference's code paths reach -----------------------------
+def test_edge_cases(gpu, torch, oracle):
+    rng = np.random.default_rng(7)
+    V = 4096
+    cases = []
+    x = np.zeros(V, np.float32)
+    cases.append(("all_equal_k0", x, (1.0, 0, 0.9, 1.0)))
+    cases.append(("all_equal_k40", x, (1.0, 40, 0.9, 1.0)))
+    cases.append(("all_equal_k2000", x, (1.0, 2000, 0.95, 1.0)))
+    x = (rng.integers(-3, 3, V) / 2).astype(np.float32)
+    cases.append(("ties_k100", x, (0.7, 100, 0.9, 1.1)))
+    cases.append(("ties_k0", x, (0.7, 0, 0.9, 1.1)))
+    x = np.full(V, -np.inf, np.float32)
+    x[[5, 77, 900]] = [1.0, 2.0, 1.5]
+    cases.append(("masked_k40", x, (1.0, 40, 0.99, 1.0)))
+    cases.append(("masked_k0", x, (1.0, 0, 0.99, 1.0)))
+    x = rng.standard_normal(V).astype(np.float32)
+    x[10] = np.inf
+    cases.append(("posinf_k0", x, (1.0, 0, 0.9, 1.0)))
+    cases.append(("posinf_k5", x, (1.0, 5, 0.9, 1.0)))
+    x = rng.standard_normal(V).astype(np.float32)
+    cases.append(("k_eq_V", x, (0.9, V, 0.8, 1.2)))
+    cases.append(("k_1500_fullpath", x, (0.9, 1500, 0.8, 1.2)))
+    cases.append(("k1", x, (0.9, 1, 0.5, 1.3)))
+    cases.append(("greedy", x, (0.0, 40, 0.9, 1.3)))
+    cases.append(("greedy_neg", x, (-1.0, 40, 0.9, 1.0)))
+    cases.append(("top_p_0", x, (1.3, 0, 0.0, 1.0)))
+    cases.append(("top_p_1", x, (1.3, 0, 1.0, 1.0)))
+    cases.append(("tiny_T", x, (1e-3, 0, 0.9, 1.0)))
+    cases.append(("big_T", x, (50.0, 0, 0.95, 1.0)))
+    xz = x.copy()
+    xz[::7] = -0.0
+    xz[3::7] = 0.0
+    cases.append(("signed_zeros", xz, (1.0, 0, 0.97, 1.0)))
+    x = (rng.standard_normal(V) * 30).astype(np.float32)
+    cases.append(("peaked_k0", x, (1.0, 0, 0.9, 1.0)))
+    rec = np.concatenate([rng.integers(0, V, 60), [0, 0, 0, V + 5, 2 ** 32 - 1]]).astype(np.uint32)
+    for name, x, (T, k, p, rep) in cases:
+        for u in (0.0, 0.37, 0.9999):
+            _say("edge", name, "u", u)
+            tok, st, _ = run_batch(gpu, torch, x[None, :], u=[u], recent=rec[None, :],
+                                   uniform=(T, k, p, rep))
+            want = oracle.sample(x, T, k, p, rep, rec, r=u)
+            assert st[0] == 0, (name, st[0])
+            assert tok[0] == want, (name, u, tok[0], want)
+
+
+def test_errors(gpu, torch):
+    x = np.ones((3, 100), np.float32)
+    x[1, 50] = np.nan
+    tok, st, _ = run_batch(gpu, torch, x, u=[0.1, 0.1, 0.1], uniform=(0.7, 40, 0.9, 1.0))
+    assert list(st) == [0, gpu.GS_ERR_NAN, 0]
+    tok, st, _ = run_batch(gpu, torch, x, u=[0.1, 0.1, 0.1], uniform=(0.0, 40, 0.9, 1.0))
+    assert list(st) == [0, gpu.GS_ERR_NAN, 0]
+    tok, st, _ = run_batch(gpu, torch, x, u=[0.1, 0.1, 0.1], uniform=(0.7, 0, 0.9, 1.0))
+    assert list(st) == [0, gpu.GS_ERR_NAN, 0]
+    s = gpu.Sampler(0.7, 40, 0.9, 1.0, seed=1)
+    with pytest.raises(gpu.SamplerError):
+        s.sample(np.zeros(0, np.float32))
+    assert s.sample(np.array([np.nan], np.float32)) == 0
+
+
+def test_lcg_batch_stream(gpu, torch, oracle):
+    """u == NULL: row b takes the b-th next draw of the sampler's stream."""
+    import workloads
+    rng = np.random.default_rng(3)
+    B, V = 8, 2000
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    tok, st, s = run_batch(gpu, torch, x, uniform=(1.0, 0, 0.95, 1.0), seed=99)
+    u, nxt = workloads.lcg_stream(99, B)
+    pr = workloads.params_rows([(1.0, 0, 0.95, 1.0)] * B)
+    want = oracle.sample_batch(x, pr, u)
+    check_tokens("lcg_batch", tok, want, st)
+    assert s.state == nxt
+
+
+def test_reference_free_function_api(gpu, oracle):
+    """set_seed + sample(logits, T, k, p, rep, recent) with the global stream."""
+    import gs_sampler
+    rng = np.random.default_rng(5)
+    gs_sampler.set_seed(42)
+    oracle.set_seed(42)
+    for i in range(10):
+        x = (rng.standard_normal(3000) * 3).astype(np.float32)
+        T = 0.0 if i == 4 else 0.8
+        rec = rng.integers(0, 3000, 32)
+        a = gs_sampler.sample(x, T, 40, 0.9, 1.1, rec)
+        b = oracle.sample(x, T, 40, 0.9, 1.1, rec)
+        assert a == b
