@@ -22,6 +22,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-function-calls=false",
     "-Wall", "-Wno-unused-function",
 ]
 SOURCES = ["gs_kernels.hip", "gs_api.cpp"]

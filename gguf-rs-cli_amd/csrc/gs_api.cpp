@@ -27,6 +27,8 @@ struct gs_sampler {
     int32_t *d_status_map;
     uint32_t *scratch;           // full-vocabulary path
     size_t scratch_elems;
+    int32_t *fb;                 // per-row fallback flags of the full-vocabulary path
+    size_t fb_cap;
 };
 
 namespace {
@@ -56,7 +58,11 @@ bool needs_full_path(const gs_params &p, size_t V)
 
 int reserve_scratch(gs_sampler *s, size_t rows, size_t V)
 {
-    size_t elems = rows * 4 * V;
+    void *f = s->fb;
+    int rcf = grow(&f, &s->fb_cap, (rows ? rows : 1) * sizeof(int32_t));
+    s->fb = (int32_t *)f;
+    if (rcf) return rcf;
+    size_t elems = rows * gs::scratch_u32_per_row(V);
     size_t cap = s->scratch_elems * sizeof(uint32_t);
     void *p = s->scratch;
     int rc = grow(&p, &cap, elems * sizeof(uint32_t));
@@ -101,6 +107,7 @@ int gs_sampler_destroy(gs_sampler *s)
     if (s->d_row) (void)hipFree(s->d_row);
     if (s->d_rec) (void)hipFree(s->d_rec);
     if (s->scratch) (void)hipFree(s->scratch);
+    if (s->fb) (void)hipFree(s->fb);
     if (s->h_tok) (void)hipHostFree(s->h_tok);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     (void)hipSetDevice(dev);
@@ -186,8 +193,10 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     a.tokens = s->d_tok_map;
     a.status = s->d_status_map;
     a.scratch = s->scratch;
-    a.scratch_stride = 4 * V;
-    if (gs::launch_sample_rows(a, 1, s->stream) != hipSuccess) return GS_ERR_HIP;
+    a.scratch_stride = gs::scratch_u32_per_row(V);
+    a.fb = s->fb;
+    const bool full = needs_full_path(s->params, V);
+    if (gs::launch_sample_rows(a, 1, !full, full, s->stream) != hipSuccess) return GS_ERR_HIP;
     if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
     if (s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, 1);   // one draw iff T > 0
     int st = *(volatile int32_t *)s->h_status;
@@ -225,8 +234,11 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, si
     a.tokens = d_tokens;
     a.status = d_status;
     a.scratch = s->scratch;
-    a.scratch_stride = 4 * V;
-    if (gs::launch_sample_rows(a, (int)B, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+    a.scratch_stride = gs::scratch_u32_per_row(V);
+    a.fb = s->fb;
+    const bool full = d_params || needs_full_path(s->params, V);
+    const bool small = d_params || !needs_full_path(s->params, V);
+    if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
     if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
     return GS_OK;
 }

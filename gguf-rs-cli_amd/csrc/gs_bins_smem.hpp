@@ -1,0 +1,30 @@
+// gs_bins_smem.hpp -- LDS layout of the binned full-vocabulary path.
+#pragma once
+#include <stdint.h>
+
+namespace gs {
+
+constexpr int kBins = 4096;        // bins of d' = y - m0 over [-kDLo, kDUp]
+constexpr int kOverCap = 256;      // elements above the bin range (d' > kDUp)
+constexpr int kMaxGroups = 256;    // runs of consecutive collected bins
+
+struct BinsSmem {
+    uint32_t cnt[kBins];           // pass 1: count; then collected bin -> cursor, bulk bin -> run index
+    uint32_t off[kBins + 1];       // list segment of bin b: [off[b], off[b+1])
+    uint64_t esum[kBins];          // bulk bin: sum of seq-1 increments
+    uint64_t k23[kBins];           // bulk bin: seq-2 increments (low 32) | seq-3 increments (high 32)
+    uint32_t meta[kBins];          // flags, tie count and grid exponents
+    uint64_t over[kOverCap];       // (key << 32) | ~idx of d' > kDUp
+    uint32_t gbeg[kMaxGroups];     // group g: list range [gbeg, gend)
+    uint32_t gend[kMaxGroups];
+    uint64_t run[kMaxGroups + 1];  // bulk increment sum of run g (between groups g-1 and g)
+    uint32_t runt[kMaxGroups + 1]; // seq-1 rounding ties inside run g
+    int runb[kMaxGroups + 1];      // packed grid exponents and flags of run g
+    uint32_t wbase[kMaxGroups + 1];// walk array: position of run g's marker
+    float m0, m, S, s2, Spred, s2lo, s2hi, Slo, Shi;
+    float hw2, hw3, inv_spred, inv_s2c;
+    int ngroups, ndefer, nover, fail, ncollect;
+    int cut_g, cut_j, tok;
+};
+
+} // namespace gs

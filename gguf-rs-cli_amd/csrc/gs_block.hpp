@@ -44,7 +44,12 @@ __device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b)
     uint32_t s = a + b;
     return s > kSat ? kSat : s;
 }
-__device__ __forceinline__ uint32_t par_apply(const ParFn &f, uint32_t p) { return p ? f.f1 : f.f0; }
+// Branchless select (a ternary on the two fields gets lowered to an indexed
+// load from a stack copy, which the backend places in LDS).
+__device__ __forceinline__ uint32_t par_apply(const ParFn &f, uint32_t p)
+{
+    return f.f0 ^ ((f.f0 ^ f.f1) & (0u - (p & 1u)));
+}
 __device__ __forceinline__ ParFn par_compose(const ParFn &a, const ParFn &b)
 {
     ParFn r;
@@ -63,15 +68,46 @@ __device__ __forceinline__ int grid_exp(float s)
 // Increment function of summand a at grid exponent e.
 __device__ __forceinline__ ParFn elem_fn(float a, int e)
 {
-    float m = ldexpf(a, 23 - e);           // exact power-of-two scaling
+    const float m = ldexpf(a, 23 - e);     // exact power-of-two scaling
+    const bool big = !(m < (float)kSat);
+    const float fl = floorf(m);
+    const float fr = m - fl;               // exact
+    const uint32_t K = big ? 0u : (uint32_t)fl;
+    const uint32_t k = K + (fr > 0.5f ? 1u : 0u);
+    const bool tie = fr == 0.5f;
     ParFn f;
-    if (!(m < (float)kSat)) { f.f0 = f.f1 = kSat; return f; }
-    float fl = floorf(m);
-    float fr = m - fl;                      // exact
-    uint32_t K = (uint32_t)fl;
-    if (fr == 0.5f) { f.f0 = K + (K & 1u); f.f1 = K + ((K + 1u) & 1u); }
-    else { uint32_t k = K + (fr > 0.5f ? 1u : 0u); f.f0 = f.f1 = k; }
+    f.f0 = big ? kSat : (tie ? K + (K & 1u) : k);
+    f.f1 = big ? kSat : (tie ? K + ((K + 1u) & 1u) : k);
     return f;
+}
+
+// Wave64 inclusive scan of ParFn with DPP moves (no LDS): Hillis-Steele
+// inside each 16-lane row (row_shr 1, 2, 4, 8), then row_bcast:15 and
+// row_bcast:31 across rows.  The operator is not commutative, so the value
+// from the lower lane is always the left operand.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ void dpp_step(ParFn &v, bool take)
+{
+    ParFn o;
+    o.f0 = dpp_mov<CTRL>(v.f0);
+    o.f1 = dpp_mov<CTRL>(v.f1);
+    if (take) v = par_compose(o, v);
+}
+__device__ __forceinline__ ParFn wave_scan_incl(ParFn v)
+{
+    const int lane = lane_id(), rl = lane & 15;
+    dpp_step<0x111>(v, rl >= 1);      // row_shr:1
+    dpp_step<0x112>(v, rl >= 2);      // row_shr:2
+    dpp_step<0x114>(v, rl >= 4);      // row_shr:4
+    dpp_step<0x118>(v, rl >= 8);      // row_shr:8
+    dpp_step<0x142>(v, (lane & 31) >= 16);   // row_bcast:15
+    dpp_step<0x143>(v, lane >= 32);          // row_bcast:31
+    return v;
 }
 
 struct SeqSmem {

@@ -14,25 +14,39 @@
 // block_seqsum (see gs_block.hpp).
 #include "gs_block.hpp"
 #include "gs_kernels.hpp"
+#include "gs_bins_smem.hpp"
 
 namespace gs {
+
+#ifdef GS_TIMING
+// Stage timestamps of row 0 (development builds only).
+__device__ uint64_t g_stamp[32];
+__device__ int g_fails[1024];
+__device__ unsigned g_row;
+#define GS_STAMP(i) do { if (blockIdx.x == g_row && threadIdx.x == 0) g_stamp[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define GS_STAMP(i) do { } while (0)
+#endif
 
 constexpr int kHashSlots = 2 * kMaxWindow;     // open addressing, load <= 1/2
 constexpr int kHistBins = 4096;                 // 12-bit radix digits
 constexpr int kCandCap = 2048;                  // LDS candidate capacity
 constexpr uint32_t kEmpty = 0xffffffffu;
 
-struct RowSmem {
-    uint32_t hkey[kHashSlots];                  // penalized ids
-    uint32_t hval[kHashSlots];                  // occurrence count, then f32 bits of the penalized logit
+struct TopkSmem {
     union {
         uint32_t hist[kHistBins];
         uint32_t wcnt[kWaves * 256];            // radix sort: per-wave digit counts
-        float ev[kHistBins];                    // candidates: exp values
+        float ev[kHistBins];
     } u;
     uint64_t cand[kCandCap];                    // (key << 32) | ~idx, sorted descending
-    SeqSmem seq;
     uint32_t base[256];
+};
+
+struct RowSmem {
+    uint32_t hkey[kHashSlots];                  // penalized ids
+    uint32_t hval[kHashSlots];                  // occurrence count, then f32 bits of the penalized logit
+    SeqSmem seq;
     int ncand;
     int nuniq;
     int flag_nan;
@@ -41,7 +55,12 @@ struct RowSmem {
     uint32_t red_u32[kWaves];
     float red_f32[kWaves];
     int red_i32[kWaves];
+    double red_f64[kWaves];
     int tok;
+    union {
+        TopkSmem tk;
+        BinsSmem bn;
+    } x;
 };
 
 // --------------------------------------------------------------------------
@@ -75,7 +94,11 @@ __device__ void build_penalty(RowSmem &sm, const float *row, int V, const uint32
         uint32_t h = hash_slot(id);
         for (;;) {
             uint32_t prev = atomicCAS(&sm.hkey[h], kEmpty, id);
-            if (prev == kEmpty || prev == id) { atomicAdd(&sm.hval[h], 1u); break; }
+            if (prev == kEmpty || prev == id) {
+                if (prev == kEmpty) atomicAdd(&sm.nuniq, 1);
+                atomicAdd(&sm.hval[h], 1u);
+                break;
+            }
             h = (h + 1) & (kHashSlots - 1);
         }
     }
@@ -112,6 +135,54 @@ __device__ int block_or(int v, RowSmem &sm)
     for (int i = 0; i < kWaves; i++) r |= sm.red_i32[i];
     __syncthreads();
     return r;
+}
+
+// --------------------------------------------------------------------------
+// Visit every element of a row once, f(index, value).  With a 16-byte
+// aligned row the loads are float4 and kUnroll of them are in flight per
+// thread before any is consumed (a row is 1024*16*kUnroll bytes per round).
+constexpr int kUnroll = 4;
+template <class F>
+__device__ __forceinline__ void row_for_each(const float *row, int V, bool aligned, F f)
+{
+    const int t = threadIdx.x;
+    if (aligned) {
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        const int n4 = V >> 2;
+        for (int base = 0; base < n4; base += kThreads * kUnroll) {
+            float4 v[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                int q = base + u * kThreads + t;
+                if (q < n4) v[u] = r4[q];
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                int q = base + u * kThreads + t;
+                if (q < n4) {
+                    f(4 * q + 0, v[u].x);
+                    f(4 * q + 1, v[u].y);
+                    f(4 * q + 2, v[u].z);
+                    f(4 * q + 3, v[u].w);
+                }
+            }
+        }
+        for (int i = (n4 << 2) + t; i < V; i += kThreads) f(i, row[i]);
+    } else {
+        for (int base = 0; base < V; base += kThreads * kUnroll) {
+            float v[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                int i = base + u * kThreads + t;
+                if (i < V) v[u] = row[i];
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                int i = base + u * kThreads + t;
+                if (i < V) f(i, v[u]);
+            }
+        }
+    }
 }
 
 // --------------------------------------------------------------------------
@@ -160,12 +231,83 @@ __device__ void greedy_row(RowSmem &sm, const float *row, int V, bool has_pen, i
 }
 
 // --------------------------------------------------------------------------
+// Wave-level softmax / nucleus / draw for n <= 256 survivors.  Every lane of
+// the wave runs the reference's sequential loops (src/sampler.rs:53-78) in
+// lockstep, reading the element of step j with v_readlane, so each f32 op is
+// the reference's op in the reference's order.  Lane l holds positions
+// l, l+64, l+128, l+192.
+constexpr int kWaveFinishMax = 256;
+
+__device__ __forceinline__ float rdl(float v, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+template <class YV, class IX>
+__device__ int finish_wave(int n, YV yv, IX idx, float top_p, float r)
+{
+    const int lane = lane_id();
+    const float m = yv(0);
+    if (isinf(m)) return (int)idx(n - 1);
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        int j = c * 64 + lane;
+        v[c] = (j < n) ? glibc_expf(yv(j) - m) : 0.0f;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int lim = min(64, n - c * 64);
+        for (int l = 0; l < lim; l++) sum += rdl(v[c], l);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = v[c] / sum;
+    int cut = n;
+    if (top_p < 1.0f) {
+        float cum = 0.0f;
+        bool done = false;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int lim = min(64, n - c * 64);
+            for (int l = 0; l < lim && !done; l++) {
+                cum += rdl(v[c], l);
+                if (cum >= top_p) { cut = c * 64 + l + 1; done = true; }
+            }
+        }
+        const float s2 = cum;   // the renormalising sum (src/sampler.rs:67) equals the running sum at the cut
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = v[c] / s2;
+    }
+    float cum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int lim = min(64, cut - c * 64);
+        for (int l = 0; l < lim; l++) {
+            cum += rdl(v[c], l);
+            if (r < cum) return (int)idx(c * 64 + l);
+        }
+    }
+    return (int)idx(cut - 1);
+}
+
+// --------------------------------------------------------------------------
 // Softmax, nucleus and draw over n candidates sorted descending.  yv(j) gives
 // the scaled logit of candidate j, idx(j) its token id.  Mirrors
 // src/sampler.rs:53-78 exactly (block_seqsum reproduces every f32 sum).
 template <class YV, class IX>
 __device__ int finish_sorted(RowSmem &sm, int n, YV yv, IX idx, float top_p, float r)
 {
+    if (n <= kWaveFinishMax) {
+        if (wave_id() == 0) {
+            int tk = finish_wave(n, yv, idx, top_p, r);
+            if (lane_id() == 0) sm.tok = tk;
+        }
+        __syncthreads();
+        const int tk = sm.tok;
+        __syncthreads();
+        return tk;
+    }
     const float m = yv(0);
     if (isinf(m)) {
         // y - m is NaN for some element (src/sampler.rs:54), every probability
@@ -193,7 +335,7 @@ __device__ int finish_sorted(RowSmem &sm, int n, YV yv, IX idx, float top_p, flo
 }
 
 // --------------------------------------------------------------------------
-// Bitonic sort of sm.cand[0..P) descending, P a power of two.
+// Bitonic sort of sm.x.tk.cand[0..P) descending, P a power of two.
 __device__ void bitonic_desc(RowSmem &sm, int P)
 {
     for (int k = 2; k <= P; k <<= 1) {
@@ -201,9 +343,9 @@ __device__ void bitonic_desc(RowSmem &sm, int P)
             for (int i = threadIdx.x; i < P; i += kThreads) {
                 int l = i ^ j;
                 if (l > i) {
-                    uint64_t a = sm.cand[i], b = sm.cand[l];
+                    uint64_t a = sm.x.tk.cand[i], b = sm.x.tk.cand[l];
                     bool desc = (i & k) == 0;
-                    if (desc ? (a < b) : (a > b)) { sm.cand[i] = b; sm.cand[l] = a; }
+                    if (desc ? (a < b) : (a > b)) { sm.x.tk.cand[i] = b; sm.x.tk.cand[l] = a; }
                 }
             }
             __syncthreads();
@@ -236,31 +378,105 @@ __device__ uint32_t block_excl_u32(uint32_t v, uint32_t *tot, RowSmem &sm)
 }
 
 // --------------------------------------------------------------------------
-// Top-k path.  Returns the token (or sets *status).
-__device__ int topk_row(RowSmem &sm, const float *row, int V, int k, float T, float top_p,
-                        bool has_pen, float r, int *status)
+// Radix-select step over the histogram sm.x.tk.u.hist[0..nbins): the bin holding
+// the need-th largest key (need >= 1) and the count of keys in higher bins.
+// If fewer than `need` keys exist, returns bin 0.
+__device__ void select_bin(RowSmem &sm, uint32_t nbins, uint32_t need, uint32_t *bin, uint32_t *above)
 {
     const int t = threadIdx.x;
+    const uint32_t per = (nbins + kThreads - 1) / kThreads;
+    uint32_t mine = 0;
+    for (uint32_t q = 0; q < per; q++) {
+        uint32_t bt = t * per + q;            // index from the top
+        if (bt < nbins) mine += sm.x.tk.u.hist[nbins - 1 - bt];
+    }
+    if (t == 0) { sm.sel_prefix = 0; sm.sel_above = 0; }
+    uint32_t tot;
+    uint32_t ex = block_excl_u32(mine, &tot, sm);   // contains barriers
+    if (ex < need && ex + mine >= need) {
+        uint32_t c = ex;
+        for (uint32_t q = 0; q < per; q++) {
+            uint32_t bt = t * per + q;
+            uint32_t b = nbins - 1 - bt;
+            uint32_t h = sm.x.tk.u.hist[b];
+            if (c + h >= need) { sm.sel_prefix = b; sm.sel_above = c; break; }
+            c += h;
+        }
+    }
+    __syncthreads();
+    *bin = sm.sel_prefix;
+    *above = sm.sel_above;
+    __syncthreads();
+}
+
+// Sort sm.x.tk.cand[0..n) descending (keys are unique).  Rank sort for n <= 1024:
+// every element counts the larger keys (broadcast LDS reads), one scatter.
+__device__ void sort_cand_desc(RowSmem &sm, int n)
+{
+    const int t = threadIdx.x;
+    if (n > 1024) {
+        int P = 1;
+        while (P < n) P <<= 1;
+        for (int i = n + t; i < P; i += kThreads) sm.x.tk.cand[i] = 0ull;
+        __syncthreads();
+        bitonic_desc(sm, P);
+        return;
+    }
+    uint64_t *tmp = reinterpret_cast<uint64_t *>(sm.x.tk.u.hist);   // 2048 u64 of scratch
+    for (int i = t; i < n; i += kThreads) tmp[i] = sm.x.tk.cand[i];
+    __syncthreads();
+    if (t < n) {
+        const uint64_t me = tmp[t];
+        int r = 0;
+        int j = 0;
+        for (; j + 4 <= n; j += 4)
+            r += (tmp[j] > me) + (tmp[j + 1] > me) + (tmp[j + 2] > me) + (tmp[j + 3] > me);
+        for (; j < n; j++) r += tmp[j] > me;
+        sm.x.tk.cand[r] = me;
+    }
+    __syncthreads();
+}
+
+// --------------------------------------------------------------------------
+// Top-k path.
+//
+// XSPACE = true selects on the keys of the raw (penalized) logits x instead
+// of y = x / T.  Division by T > 0 is monotone, so the order by x refines the
+// order by y; it differs only where distinct x round to the same y.  After the
+// survivors are sorted by y, the selection is accepted only if every element
+// left out maps to a y strictly below the k-th survivor's y; otherwise the
+// caller reruns with XSPACE = false (select directly on y).  This keeps the
+// division out of the per-element loop.
+// Returns the token; *ok = false asks for the y-space rerun.
+template <bool XSPACE>
+__device__ int topk_row(RowSmem &sm, const float *row, int V, int k, float T, float top_p,
+                        bool has_pen, float r, bool aligned, int *status, bool *ok)
+{
+    const int t = threadIdx.x;
+    *ok = true;
+    auto keyof = [&](float x) { return XSPACE ? f2key(x) : f2key(x / T); };
     // Radix select over the 32-bit keys in 3 levels: 12, 12, 8 bits.
     uint32_t prefix = 0;        // key bits above `shift` fixed so far
     int shift = 32;
     uint32_t above = 0;         // elements with key strictly above the in-play range
     int nan = 0;
-    const int widths[3] = {12, 12, 8};
-    int level = 0;
     bool fits = false;
-    for (level = 0; level < 3; level++) {
-        const int wbits = widths[level];
+    for (int level = 0; level < 3; level++) {
+        const int wbits = level < 2 ? 12 : 8;
         const int nsh = shift - wbits;
         const uint32_t nbins = 1u << wbits;
-        for (uint32_t i = t; i < nbins; i += kThreads) sm.u.hist[i] = 0;
+        for (uint32_t i = t; i < nbins; i += kThreads) sm.x.tk.u.hist[i] = 0;
         __syncthreads();
-        for (int i = t; i < V; i += kThreads) {
-            float y = row[i] / T;
-            if (level == 0) nan |= isnan(y);
-            uint32_t key = f2key(y);
-            if (shift == 32 || (key >> shift) == prefix)
-                atomicAdd(&sm.u.hist[(key >> nsh) & (nbins - 1)], 1u);
+        if (level == 0) {
+            row_for_each(row, V, aligned, [&](int, float x) {
+                nan |= (int)isnan(x) | ((int)isinf(x) & (int)isinf(T));
+                atomicAdd(&sm.x.tk.u.hist[keyof(x) >> nsh], 1u);
+            });
+        } else {
+            row_for_each(row, V, aligned, [&](int, float x) {
+                uint32_t key = keyof(x);
+                if ((key >> shift) == prefix) atomicAdd(&sm.x.tk.u.hist[(key >> nsh) & (nbins - 1)], 1u);
+            });
         }
         __syncthreads();
         if (has_pen) {
@@ -268,69 +484,54 @@ __device__ int topk_row(RowSmem &sm, const float *row, int V, int k, float T, fl
             for (int s = t; s < kHashSlots; s += kThreads) {
                 uint32_t id = sm.hkey[s];
                 if (id == kEmpty) continue;
-                uint32_t kr = f2key(row[id] / T);
-                uint32_t kp = f2key(__uint_as_float(sm.hval[s]) / T);
-                if (shift == 32 || (kr >> shift) == prefix) atomicSub(&sm.u.hist[(kr >> nsh) & (nbins - 1)], 1u);
-                if (shift == 32 || (kp >> shift) == prefix) atomicAdd(&sm.u.hist[(kp >> nsh) & (nbins - 1)], 1u);
+                uint32_t kr = keyof(row[id]);
+                uint32_t kp = keyof(__uint_as_float(sm.hval[s]));
+                if (shift == 32 || (kr >> shift) == prefix) atomicSub(&sm.x.tk.u.hist[(kr >> nsh) & (nbins - 1)], 1u);
+                if (shift == 32 || (kp >> shift) == prefix) atomicAdd(&sm.x.tk.u.hist[(kp >> nsh) & (nbins - 1)], 1u);
             }
             __syncthreads();
         }
         if (level == 0 && block_or(nan, sm)) { *status = GS_ERR_NAN; return 0; }
-        // Find the bin holding the k-th largest: scan bins from the top.
-        // Thread t owns bins [c*t, c*t+c) counted from the top.
-        const uint32_t per = (nbins + kThreads - 1) / kThreads;
-        uint32_t mine = 0;
-        for (uint32_t q = 0; q < per; q++) {
-            uint32_t bt = t * per + q;            // index from the top
-            if (bt < nbins) mine += sm.u.hist[nbins - 1 - bt];
-        }
-        uint32_t tot;
-        uint32_t ex = block_excl_u32(mine, &tot, sm);
-        const uint32_t need = (uint32_t)k - above;
-        if (ex < need && ex + mine >= need) {
-            uint32_t c = ex;
-            for (uint32_t q = 0; q < per; q++) {
-                uint32_t bt = t * per + q;
-                uint32_t b = nbins - 1 - bt;
-                uint32_t h = sm.u.hist[b];
-                if (c + h >= need) { sm.sel_prefix = b; sm.sel_above = c; break; }
-                c += h;
-            }
-        }
-        __syncthreads();
-        const uint32_t b = sm.sel_prefix;
-        const uint32_t in_bin = sm.u.hist[b];
-        above += sm.sel_above;
+        GS_STAMP(2);
+        uint32_t b, sel_above;
+        select_bin(sm, nbins, (uint32_t)k - above, &b, &sel_above);
+        const uint32_t in_bin = sm.x.tk.u.hist[b];
+        above += sel_above;
         prefix = (shift == 32 ? 0u : (prefix << wbits)) | b;
         shift = nsh;
         __syncthreads();
         if (above + in_bin <= (uint32_t)kCandCap) { fits = true; break; }
     }
+    GS_STAMP(3);
+    if (XSPACE && !fits) { *ok = false; return 0; }
     // Collect candidates: key >> shift >= prefix (when the tie range fits),
     // else key > K* plus the first (k - above) ids equal to K* in index order.
     if (t == 0) sm.ncand = 0;
     __syncthreads();
-    const uint32_t kstar = prefix;  // valid as a full key only when !fits (shift == 0)
-    for (int i = t; i < V; i += kThreads) {
-        float y = row[i] / T;
-        uint32_t key = f2key(y);
+    const uint32_t kstar = prefix;  // a full key only when !fits (shift == 0)
+    row_for_each(row, V, aligned, [&](int i, float x) {
+        uint32_t key = keyof(x);
         bool take = fits ? ((key >> shift) >= prefix) : (key > kstar);
         if (take && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) {
             int slot = atomicAdd(&sm.ncand, 1);
-            sm.cand[slot] = cand_of(key, (uint32_t)i);
+            if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(x / T), (uint32_t)i);
         }
-    }
+    });
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {
             uint32_t id = sm.hkey[s];
             if (id == kEmpty) continue;
-            uint32_t key = f2key(__uint_as_float(sm.hval[s]) / T);
+            float x = __uint_as_float(sm.hval[s]);
+            uint32_t key = keyof(x);
             bool take = fits ? ((key >> shift) >= prefix) : (key > kstar);
-            if (take) { int slot = atomicAdd(&sm.ncand, 1); sm.cand[slot] = cand_of(key, id); }
+            if (take) {
+                int slot = atomicAdd(&sm.ncand, 1);
+                if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(x / T), id);
+            }
         }
     }
     __syncthreads();
-    if (!fits) {
+    if (!XSPACE && !fits) {
         // Ordered selection of the first `need` elements equal to K*.
         uint32_t need = (uint32_t)k - above;
         uint32_t taken = 0;
@@ -342,24 +543,116 @@ __device__ int topk_row(RowSmem &sm, const float *row, int V, int k, float T, fl
             uint32_t ex = block_excl_u32(eq ? 1u : 0u, &tot, sm);
             if (eq && taken + ex < need) {
                 int slot = atomicAdd(&sm.ncand, 1);
-                sm.cand[slot] = cand_of(kstar, (uint32_t)i);
+                if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(kstar, (uint32_t)i);
             }
             taken += tot;
         }
         __syncthreads();
     }
-    const int nc = sm.ncand;
-    int P = 1;
-    while (P < nc) P <<= 1;
-    for (int i = nc + t; i < P; i += kThreads) sm.cand[i] = 0ull;
-    __syncthreads();
-    bitonic_desc(sm, P);
+    GS_STAMP(4);
+    const int nc = min(sm.ncand, kCandCap);
+    sort_cand_desc(sm, nc);
+    GS_STAMP(5);
     const int n = k;   // nc >= k by construction
-    auto yv = [&](int j) { return key2f((uint32_t)(sm.cand[j] >> 32)); };
-    auto ix = [&](int j) { return ~(uint32_t)sm.cand[j]; };
+    if (XSPACE && shift < 32) {
+        // Elements left out have x-key < thr; their y is at most y_out.
+        const uint32_t thr = prefix << shift;
+        if (thr > 0x007fffffu) {   // below that key every real x is a candidate
+            float y_out = key2f(thr - 1u) / T;
+            uint32_t yk = (uint32_t)(sm.x.tk.cand[n - 1] >> 32);
+            if (!(f2key(y_out) < yk)) { *ok = false; __syncthreads(); return 0; }
+        }
+    }
+    auto yv = [&](int j) { return key2f((uint32_t)(sm.x.tk.cand[j] >> 32)); };
+    auto ix = [&](int j) { return ~(uint32_t)sm.x.tk.cand[j]; };
     *status = GS_OK;
     return finish_sorted(sm, n, yv, ix, top_p, r);
 }
+
+// --------------------------------------------------------------------------
+// Top-k path, one streaming pass plus one cached re-read.
+//
+// Pass 1 keeps only each thread's maximum raw logit (no atomics).  Among the
+// 1024 thread maxima, the (k + U)-th largest (U = distinct penalized ids)
+// is a lower bound tau on the k-th largest effective logit: those k + U
+// maxima are distinct elements and at most U of them are penalized, so at
+// least k unpenalized elements are >= tau.  Pass 2 collects every element
+// whose effective logit is >= tau, they are sorted by y = x / T and the
+// selection is accepted as in topk_row<true> (no element left out may tie
+// the k-th y).  Returns ok = false when the bound is unusable (k + U > 1024,
+// too many elements above tau); the caller then runs the radix select.
+__device__ int topk_row_tmax(RowSmem &sm, const float *row, int V, int k, float T, float top_p,
+                             bool has_pen, int nuniq, float r, bool aligned, int *status, bool *ok)
+{
+    const int t = threadIdx.x;
+    *ok = false;
+    const uint32_t need = (uint32_t)k + (uint32_t)nuniq;
+    if (need > (uint32_t)kThreads) return 0;
+    float tmax = -INFINITY;
+    bool any = false;
+    int nan = 0;
+    row_for_each(row, V, aligned, [&](int, float x) {
+        nan |= (int)isnan(x) | ((int)isinf(x) & (int)isinf(T));
+        tmax = fmaxf(tmax, x);
+        any = true;
+    });
+    if (block_or(nan, sm)) { *ok = true; *status = GS_ERR_NAN; return 0; }
+    GS_STAMP(2);
+    const uint32_t tk = any ? f2key(tmax) : 0u;
+    // Two 12-bit radix levels over the 1024 thread maxima.
+    uint32_t prefix = 0, above = 0;
+    for (int level = 0; level < 2; level++) {
+        const int sh = level == 0 ? 20 : 8;
+        for (int i = t; i < 4096; i += kThreads) sm.x.tk.u.hist[i] = 0;
+        __syncthreads();
+        if (level == 0 || (tk >> 20) == prefix) atomicAdd(&sm.x.tk.u.hist[(tk >> sh) & 4095u], 1u);
+        __syncthreads();
+        uint32_t b, ab;
+        select_bin(sm, 4096, need - above, &b, &ab);
+        above += ab;
+        prefix = level == 0 ? b : ((prefix << 12) | b);
+    }
+    const uint32_t tau = prefix << 8;   // >= need thread maxima have key >= tau
+    GS_STAMP(3);
+    if (t == 0) sm.ncand = 0;
+    __syncthreads();
+    row_for_each(row, V, aligned, [&](int i, float x) {
+        if (f2key(x) >= tau && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) {
+            int slot = atomicAdd(&sm.ncand, 1);
+            if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(x / T), (uint32_t)i);
+        }
+    });
+    if (has_pen) {
+        for (int s = t; s < kHashSlots; s += kThreads) {
+            uint32_t id = sm.hkey[s];
+            if (id == kEmpty) continue;
+            float x = __uint_as_float(sm.hval[s]);
+            if (f2key(x) >= tau) {
+                int slot = atomicAdd(&sm.ncand, 1);
+                if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(x / T), id);
+            }
+        }
+    }
+    __syncthreads();
+    GS_STAMP(4);
+    const int nc = sm.ncand;
+    __syncthreads();
+    if (nc > kCandCap || nc < k) return 0;
+    sort_cand_desc(sm, nc);
+    GS_STAMP(5);
+    if (tau > 0x007fffffu) {
+        float y_out = key2f(tau - 1u) / T;
+        uint32_t yk = (uint32_t)(sm.x.tk.cand[k - 1] >> 32);
+        if (!(f2key(y_out) < yk)) return 0;
+    }
+    *ok = true;
+    auto yv = [&](int j) { return key2f((uint32_t)(sm.x.tk.cand[j] >> 32)); };
+    auto ix = [&](int j) { return ~(uint32_t)sm.x.tk.cand[j]; };
+    *status = GS_OK;
+    return finish_sorted(sm, k, yv, ix, top_p, r);
+}
+
+#include "gs_bins.hpp"
 
 // --------------------------------------------------------------------------
 // Full-vocabulary path: stable LSD radix sort of (~key, index) in scratch.
@@ -391,18 +684,18 @@ __device__ int full_row(RowSmem &sm, const float *row, int V, int keep, float T,
     uint32_t *src_k = kA, *src_i = iA, *dst_k = kB, *dst_i = iB;
     for (int pass = 0; pass < 4; pass++) {
         const int sh = pass * 8;
-        for (int i = t; i < 256; i += kThreads) sm.base[i] = 0;
+        for (int i = t; i < 256; i += kThreads) sm.x.tk.base[i] = 0;
         __syncthreads();
-        for (int i = t; i < V; i += kThreads) atomicAdd(&sm.base[(src_k[i] >> sh) & 255u], 1u);
+        for (int i = t; i < V; i += kThreads) atomicAdd(&sm.x.tk.base[(src_k[i] >> sh) & 255u], 1u);
         __syncthreads();
         if (t == 0) {
             uint32_t run = 0;
-            for (int d = 0; d < 256; d++) { uint32_t c = sm.base[d]; sm.base[d] = run; run += c; }
+            for (int d = 0; d < 256; d++) { uint32_t c = sm.x.tk.base[d]; sm.x.tk.base[d] = run; run += c; }
         }
         __syncthreads();
         constexpr int kSlots = 4;
         for (int tile = 0; tile < V; tile += kThreads * kSlots) {
-            for (int i = t; i < kWaves * 256; i += kThreads) sm.u.wcnt[i] = 0;
+            for (int i = t; i < kWaves * 256; i += kThreads) sm.x.tk.u.wcnt[i] = 0;
             __syncthreads();
             uint32_t dig[kSlots], rnk[kSlots], kk[kSlots], ii[kSlots];
             bool val[kSlots];
@@ -419,29 +712,29 @@ __device__ int full_row(RowSmem &sm, const float *row, int V, int keep, float T,
                     uint64_t bb = __ballot((d >> bit) & 1u);
                     peers &= ((d >> bit) & 1u) ? bb : ~bb;
                 }
-                uint32_t before = sm.u.wcnt[w * 256 + d];
+                uint32_t before = sm.x.tk.u.wcnt[w * 256 + d];
                 rnk[q] = before + (uint32_t)__popcll(peers & lanemask_lt());
                 // All lanes have read the counter before the leader bumps it
                 // (one wave executes in lockstep; the barrier makes it explicit).
                 __builtin_amdgcn_wave_barrier();
                 if (val[q] && (peers & lanemask_lt()) == 0)
-                    sm.u.wcnt[w * 256 + d] = before + (uint32_t)__popcll(peers);
+                    sm.x.tk.u.wcnt[w * 256 + d] = before + (uint32_t)__popcll(peers);
                 __builtin_amdgcn_wave_barrier();
             }
             __syncthreads();
             for (int d = t; d < 256; d += kThreads) {
-                uint32_t run = sm.base[d];
+                uint32_t run = sm.x.tk.base[d];
                 for (int ww = 0; ww < kWaves; ww++) {
-                    uint32_t c = sm.u.wcnt[ww * 256 + d];
-                    sm.u.wcnt[ww * 256 + d] = run;
+                    uint32_t c = sm.x.tk.u.wcnt[ww * 256 + d];
+                    sm.x.tk.u.wcnt[ww * 256 + d] = run;
                     run += c;
                 }
-                sm.base[d] = run;
+                sm.x.tk.base[d] = run;
             }
             __syncthreads();
             for (int q = 0; q < kSlots; q++) {
                 if (!val[q]) continue;
-                uint32_t dst = sm.u.wcnt[w * 256 + dig[q]] + rnk[q];
+                uint32_t dst = sm.x.tk.u.wcnt[w * 256 + dig[q]] + rnk[q];
                 dst_k[dst] = kk[q];
                 dst_i[dst] = ii[q];
             }
@@ -460,6 +753,19 @@ __device__ int full_row(RowSmem &sm, const float *row, int V, int keep, float T,
 }
 
 // --------------------------------------------------------------------------
+// Row paths: the small kernel serves greedy, degenerate and top-k rows; the
+// full-vocabulary rows go to the binned kernel and, when its checks fail, to
+// the sort kernel.  Each kernel derives the path from the row's parameters.
+__device__ __forceinline__ bool is_full_path(const gs_params &p, int V)
+{
+    if (!(p.temperature > 0.0f) || V < 2) return false;
+    const int keep = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
+    return !(keep < V && keep <= kMaxTopK);
+}
+
+enum { kModeSmall = 0, kModeBins = 1, kModeSort = 2 };
+
+template <int MODE>
 __global__ void __launch_bounds__(kThreads)
 sample_rows_kernel(RowArgs a)
 {
@@ -467,9 +773,17 @@ sample_rows_kernel(RowArgs a)
     const int b = blockIdx.x;
     const int t = threadIdx.x;
     const int V = a.V;
+    const gs_params p = a.params ? a.params[b] : a.uparams;
+    const bool full = is_full_path(p, V);
+    if (MODE == kModeSmall && full) return;
+    if (MODE != kModeSmall && !full) return;
+    if (MODE == kModeSort && a.fb != nullptr && a.fb[b] == 0) return;
+    GS_STAMP(8 * MODE);
+#ifdef GS_TIMING
+    const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
+#endif
     const float *row = a.logits + (size_t)b * a.ld;
-    gs_params p = a.params ? a.params[b] : a.uparams;
-    if (t == 0) sm.flag_nan = 0;
+    if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
 
     int tok = 0, status = GS_OK;
     const bool has_pen = (p.rep_penalty != 1.0f) && a.recent != nullptr;
@@ -481,42 +795,64 @@ sample_rows_kernel(RowArgs a)
     __syncthreads();
     if (has_pen) build_penalty(sm, row, V, a.recent + (size_t)b * a.ld_recent, W,
                                p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
-    const bool pen_active = has_pen;
+    GS_STAMP(8 * MODE + 1);
 
     // The uniform draw for this row (only consumed if T > 0).
-    float r = 0.0f;
-    if (a.u) r = a.u[b];
-    else r = lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
+    const float r = a.u ? a.u[b] : lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
+    const bool aligned = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+    const int keep = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
 
-    if (V == 0) {
-        tok = 0;
-        status = p.temperature > 0.0f ? GS_ERR_EMPTY : GS_OK;
-    } else if (!(p.temperature > 0.0f)) {
-        // src/sampler.rs:39: `if temperature <= 0.0` -- a NaN temperature is
-        // not <= 0, so it falls through to the division below.
-        if (p.temperature <= 0.0f) greedy_row(sm, row, V, pen_active, &tok, &status);
-        else {
-            // T is NaN: every scaled logit is NaN; sort panics for V > 1.
+    if (MODE == kModeSmall) {
+        if (V == 0) {
             tok = 0;
-            status = V > 1 ? GS_ERR_NAN : GS_OK;
+            status = p.temperature > 0.0f ? GS_ERR_EMPTY : GS_OK;
+        } else if (!(p.temperature > 0.0f)) {
+            // src/sampler.rs:39: `if temperature <= 0.0` -- a NaN temperature is
+            // not <= 0, so it falls through to the division below.
+            if (p.temperature <= 0.0f) greedy_row(sm, row, V, has_pen, &tok, &status);
+            else {
+                // T is NaN: every scaled logit is NaN; the sort panics for V > 1.
+                tok = 0;
+                status = V > 1 ? GS_ERR_NAN : GS_OK;
+            }
+        } else if (V == 1) {
+            tok = 0;   // a single pair: no comparison can panic; token 0.
+        } else if (sm.flag_nan) {
+            status = GS_ERR_NAN;
+        } else {
+            bool ok;
+            tok = topk_row_tmax(sm, row, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r,
+                                aligned, &status, &ok);
+            if (!ok)
+                tok = topk_row<true>(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, aligned,
+                                     &status, &ok);
+            if (!ok)
+                tok = topk_row<false>(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, aligned,
+                                      &status, &ok);
         }
-    } else if (V == 1) {
-        tok = 0;   // a single pair: no comparison can panic; token 0.
+    } else if (MODE == kModeBins) {
+        bool done = false;
+        if (sm.flag_nan) { status = GS_ERR_NAN; done = true; }
+        else if (aligned && keep == V) {
+            uint64_t *gl = reinterpret_cast<uint64_t *>(a.scratch + (size_t)b * a.scratch_stride);
+            const uint32_t lcap = (uint32_t)(a.scratch_stride / 2);
+            done = full_bins_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
+        }
+        if (t == 0) a.fb[b] = done ? 0 : 1;
+        if (!done) return;
     } else {
         if (sm.flag_nan) status = GS_ERR_NAN;
         else {
-            const int keep = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
-            if (keep < V && keep <= kMaxTopK)
-                tok = topk_row(sm, row, V, keep, p.temperature, p.top_p, pen_active, r, &status);
-            else {
-                const size_t off = (size_t)b * a.scratch_stride;
-                tok = full_row(sm, row, V, keep, p.temperature, p.top_p, pen_active, r,
-                               a.scratch + off, a.scratch + off + V,
-                               a.scratch + off + 2 * (size_t)V, a.scratch + off + 3 * (size_t)V,
-                               &status);
-            }
+            const size_t off = (size_t)b * a.scratch_stride;
+            tok = full_row(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, a.scratch + off,
+                           a.scratch + off + V, a.scratch + off + 2 * (size_t)V,
+                           a.scratch + off + 3 * (size_t)V, &status);
         }
     }
+    GS_STAMP(8 * MODE + 7);
+#ifdef GS_TIMING
+    if (t == 0 && b < 256 && MODE == kModeBins) g_fails[256 + b] = (int)(__builtin_amdgcn_s_memrealtime() - t_begin);
+#endif
     if (t == 0) {
         a.tokens[b] = (uint32_t)tok;
         if (a.status) a.status[b] = status;
@@ -541,11 +877,34 @@ __global__ void synth_kernel(float *out, int B, int V, size_t ld, uint64_t seed,
 
 } // namespace gs
 
+#ifdef GS_TIMING
+extern "C" int gs_debug_stamps(uint64_t *out)
+{
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_stamp), sizeof(uint64_t) * 32) == hipSuccess ? 0 : -5;
+}
+extern "C" int gs_debug_fails(int *out)
+{
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_fails), sizeof(int) * 1024) == hipSuccess ? 0 : -5;
+}
+extern "C" int gs_debug_row(unsigned row)
+{
+    return hipMemcpyToSymbol(HIP_SYMBOL(gs::g_row), &row, sizeof(row)) == hipSuccess ? 0 : -5;
+}
+extern "C" int gs_debug_clear(const uint64_t *zeros)
+{
+    return hipMemcpyToSymbol(HIP_SYMBOL(gs::g_stamp), zeros, sizeof(uint64_t) * 32) == hipSuccess ? 0 : -5;
+}
+#endif
+
 // Launch wrappers (host side of this translation unit).
 namespace gs {
-hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st)
+hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st)
 {
-    hipLaunchKernelGGL(sample_rows_kernel, dim3(B), dim3(kThreads), 0, st, a);
+    if (small) hipLaunchKernelGGL(sample_rows_kernel<kModeSmall>, dim3(B), dim3(kThreads), 0, st, a);
+    if (full) {
+        hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL(sample_rows_kernel<kModeSort>, dim3(B), dim3(kThreads), 0, st, a);
+    }
     return hipGetLastError();
 }
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,

@@ -23,11 +23,21 @@ struct RowArgs {
     uint64_t lcg_state;            // used when u == null: row b draws jump(state, b)
     uint32_t *tokens;
     int32_t *status;
+    int32_t *fb;                   // per row: 1 = binned path failed, use the sort path
     uint32_t *scratch;             // full-vocabulary path: 4*V u32 per row
     size_t scratch_stride;         // u32 elements per row
 };
 
-hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st);
+// Per-row scratch (u32 units) of the full-vocabulary paths: the sort path
+// needs 4V; the binned path needs its element list (V + 4352 u64), the
+// deferred ids (65536 u32) and the walk array (65536 f32 + 65536 u32).
+inline size_t scratch_u32_per_row(size_t V)
+{
+    const size_t bins = 2 * (V + 4352) + 65536 + 2 * 65536;
+    return (4 * V > bins ? 4 * V : bins);
+}
+
+hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st);
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st);
 hipError_t launch_synth(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0,
