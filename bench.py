@@ -110,6 +110,17 @@ def kernel_only_c1(gs, torch, reps=200):
     return e0.elapsed_time(e1) / reps * 1e3
 
 
+def calib_copy(torch, nbytes=1 << 30, reps=5):
+    """Plain device-to-device copy of a known size: its FETCH_SIZE and
+    WRITE_SIZE per dispatch give the scale factor of those counters."""
+    x = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log("calib copy: %d bytes read + %d bytes written per dispatch" % (nbytes, nbytes))
+
+
 def cpu_baseline(c3):
     """The oracle (C restatement of src/sampler.rs, full sort per row) over
     the whole c3 batch, once with all host threads (<= 16) and once on one
@@ -147,6 +158,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--c3-only", action="store_true",
+                    help="time only the c3 batch (for counter runs)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run a plain 1 GiB device copy 5x (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the sampler's rows are independent and this "
@@ -156,8 +171,13 @@ def main():
     import gs_sampler as gs
     gs.load_library()
     torch.cuda.init()
+    if args.calib_copy:
+        calib_copy(torch)
+        return
     c3 = bench_c3(gs, torch, args.steps, args.warmup)
     log("c3: %.3f ms/step" % c3["ms"])
+    if args.c3_only:
+        return
     c1 = bench_c1_latency(gs, torch)
     log("c1: p50 %.1f us" % c1["p50_us"])
     c1k = kernel_only_c1(gs, torch)
