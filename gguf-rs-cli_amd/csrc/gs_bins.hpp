@@ -40,21 +40,28 @@ constexpr float kDUp = 3.0f;
 constexpr float kDLo = 18.5f;
 constexpr float kInvW = (float)kBins / (kDUp + kDLo);
 constexpr float kDelta = 1.0f / 4096.0f;          // relative margin of the plan
-constexpr float kDeltaS = 1.0f / 4096.0f;         // accepted |S / Spred - 1|
 constexpr float kExpErr = 1.0f / 2097152.0f;      // bound on |fast_exp / expf - 1| (2^-21)
 constexpr float kTieThr = 1.0f / 256.0f;          // expected ties that force collection
 constexpr int kNoRun = 0x7fffffff;
 constexpr int kMaxSeg = 512;                      // largest collected bin (wave sort)
-constexpr uint32_t kNow = 0x80000000u;            // cnt[] flag: collect in pass 3
+constexpr uint32_t kNow = 0x80000000u;            // cnt[] flag: collect in the next pass
+constexpr uint32_t kMetaCol = 1u, kMetaNow = 0x80u;  // meta flags: collected / collect in the next pass
 constexpr uint32_t kDeferCapG = 65536;            // deferred elements per row
 constexpr uint32_t kWalkCap = 65536;              // items of the walk array per row
-// deferred entry: id | bit 31 penalized value | bit 30 seq-2 done | bit 29 seq-3 done
-constexpr uint32_t kDone2 = 0x40000000u, kDone3 = 0x20000000u, kIdMask = 0x1fffffffu;
+// deferred entry: id | bit 31 penalized value | bit 30 seq-2 done
+constexpr uint32_t kDone2 = 0x40000000u, kIdMask = 0x1fffffffu;
 
 __device__ __forceinline__ int bin_of(float dp)
 {
     int b = (int)((kDUp - dp) * kInvW);
     return b > kBins - 1 ? kBins - 1 : b;
+}
+
+// bin_of for any dp (out-of-range values land in the end bins).
+__device__ __forceinline__ int bin_clamp(float dp)
+{
+    const int b = (int)((kDUp - dp) * kInvW);
+    return min(max(b, 0), kBins - 1);
 }
 
 // exp(d) via v_exp_f32 with the rounding error of d*log2(e) compensated:
@@ -75,7 +82,8 @@ __device__ __forceinline__ float fast_exp(float d)
 }
 
 // meta: bit0 collected, bit1 seq-2 increments needed, bit2 seq-3 increments
-// needed, bit3 nonempty, bits 4..7 seq-1 ties; bytes 1..3 = b1, b2, b3 + 128.
+// needed, bit3 nonempty, bits 4..6 seq-1 ties, bit7 collect in the next pass;
+// bytes 1..3 = b1, b2, b3 + 128.
 __device__ __forceinline__ int meta_b(uint32_t mt, int which) { return (int)((mt >> (8 * which)) & 255u) - 128; }
 
 // Integer increment of a summand already scaled by 2^(23-b), known to
@@ -99,52 +107,6 @@ __device__ __forceinline__ int inc_exact(float a, int b, uint32_t *k)
     float fr = m - fl;
     *k = (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
     return fr != 0.5f ? 1 : 0;
-}
-
-// Increment of every float in [lo, hi] (at most 8 of them): true if all give
-// the same increment and none is a tie.
-__device__ __forceinline__ bool inc_range(float lo, float hi, int b, uint32_t *k)
-{
-    uint32_t k0;
-    if (inc_exact(lo, b, &k0) != 1) return false;
-    float v = lo;
-    for (int i = 0; i < 8 && v < hi; i++) {
-        v = __uint_as_float(__float_as_uint(v) + 1u);   // next float (v > 0)
-        uint32_t kk;
-        if (inc_exact(v, b, &kk) != 1 || kk != k0) return false;
-    }
-    if (v < hi) return false;
-    *k = k0;
-    return true;
-}
-
-__device__ __forceinline__ float next_up(float v) { return __uint_as_float(__float_as_uint(v) + 1u); }
-
-// Increment over every reachable value of a summand: p = e / S for every f32
-// S in [Slo, Shi], and (with s2) q = p / s2 for every f32 s2 in [s2lo, s2hi].
-// Returns 2 if some reachable value is a rounding tie (or the sets are too
-// large to enumerate), 0 if all give the same increment (*k), 1 otherwise.
-__device__ int inc_combos(float e, float Slo, float Shi, bool with_s2, float s2lo, float s2hi, int b, uint32_t *k)
-{
-    int n = 0;
-    uint32_t k0 = 0;
-    bool same = true;
-    int ns = 0;
-    for (float S = Slo; S <= Shi; S = next_up(S)) {
-        if (++ns > 8) return 2;
-        const float p = e / S;
-        int nq = 0;
-        for (float s2 = s2lo; s2 <= s2hi; s2 = next_up(s2)) {
-            if (++nq > 96) return 2;
-            uint32_t kk;
-            if (inc_exact(with_s2 ? p / s2 : p, b, &kk) != 1) return 2;
-            if (n++ == 0) k0 = kk;
-            else same &= kk == k0;
-            if (!with_s2) break;
-        }
-    }
-    *k = k0;
-    return same ? 0 : 1;
 }
 
 // Failure exit of the binned path (development builds record the line).
@@ -228,7 +190,7 @@ __device__ void wave_sort_c(uint64_t *g, int n)
 #pragma unroll
     for (int c = 0; c < C; c++) {
         const int j = c * 64 + lane;
-        mine[c] = j < n ? g[j] : 0ull;
+        mine[c] = j < n ? ldg(g + j) : 0ull;
         rank[c] = 0;
     }
 #pragma unroll
@@ -247,7 +209,7 @@ __device__ void wave_sort_c(uint64_t *g, int n)
 #pragma unroll
     for (int c = 0; c < C; c++) {
         const int j = c * 64 + lane;
-        if (j < n) g[rank[c]] = mine[c];
+        if (j < n) stg(g + rank[c], mine[c]);
     }
 }
 
@@ -261,29 +223,6 @@ __device__ bool wave_sort_segment(uint64_t *g, int n)
     else if (n <= kMaxSeg) wave_sort_c<8>(g, n);
     else return false;
     return true;
-}
-
-// ---------------------------------------------------------------------------
-// Pass-2 classification of one element (shared with the penalty fix-ups).
-// Returns 0 negligible/overflow, 1 collected, 2 deferred, 3 bulk.
-__device__ __forceinline__ int classify2(const BinsSmem &bn, float y, int *bin, uint32_t *k1, uint64_t *k23)
-{
-    const float dp = y - bn.m0;
-    if (!(dp <= kDUp) || dp < -kDLo) return 0;
-    const int b = bin_of(dp);
-    *bin = b;
-    const uint32_t mt = bn.meta[b];
-    if (mt & 1u) return 1;
-    const float e = fast_exp(y - bn.m);
-    uint32_t a1, a2 = 0, a3 = 0;
-    bool ok = inc_of(ldexpf(e, 23 - meta_b(mt, 1)), 2.0f * kExpErr, &a1);
-    const float p = e * bn.inv_spred;
-    if (mt & 2u) ok &= inc_of(ldexpf(p, 23 - meta_b(mt, 2)), bn.hw2, &a2);
-    if (mt & 4u) ok &= inc_of(ldexpf(p * bn.inv_s2c, 23 - meta_b(mt, 3)), bn.hw3, &a3);
-    if (!ok) return 2;
-    *k1 = a1;
-    *k23 = (uint64_t)a2 | ((uint64_t)a3 << 32);
-    return 3;
 }
 
 __device__ __forceinline__ uint64_t list_entry(float y, uint32_t i)
@@ -338,7 +277,7 @@ __device__ bool build_groups(RowSmem &sm)
             const int packed = (int)(((mt >> 8) & 0xffffffu) | ((mt & 2u) << 23) | ((mt & 4u) << 23));
             const int old = atomicCAS(&bn.runb[gb + 1], kNoRun, packed);
             if (old != kNoRun && old != packed) bn.fail = 1;
-            const uint32_t ties = (mt >> 4) & 15u;
+            const uint32_t ties = (mt >> 4) & 7u;
             if (ties) atomicAdd(&bn.runt[gb + 1], ties);
         }
     }
@@ -358,13 +297,11 @@ __device__ void gather_runs(RowSmem &sm, int which)
     const int t = threadIdx.x;
     for (int i = t; i <= bn.ngroups; i += kThreads) bn.run[i] = 0ull;
     __syncthreads();
+    const uint32_t *src = which == 2 ? bn.k2 : bn.esum;     // seq 3 reuses esum
     for (int b = t; b < kBins; b += kThreads) {
         const uint32_t mt = bn.meta[b];
         if ((mt & 1u) || bn.off[b + 1] == bn.off[b]) continue;     // nonempty bulk bins only
-        uint64_t v;
-        if (which == 1) v = bn.esum[b];
-        else if (which == 2) v = bn.k23[b] & 0xffffffffull;
-        else v = bn.k23[b] >> 32;
+        const uint32_t v = src[b];
         if (v) atomicAdd((unsigned long long *)&bn.run[bn.cnt[b]], (unsigned long long)v);
     }
     __syncthreads();
@@ -384,8 +321,16 @@ __device__ __forceinline__ int marker_run(float v) { return (int)(__float_as_uin
 __device__ __forceinline__ float make_marker(int r) { return __uint_as_float(0x7fc00000u | (uint32_t)r); }
 
 // Exact replay of one accumulation over the walk array by a single wave,
-// 64 items per step, DPP scans (see block_walk for the item encoding and the
-// return values).  Wave-uniform: every lane returns the same result.
+// kWalkK consecutive items per lane (kWalkK * 64 items per step): each lane
+// composes the increment functions of its items, a DPP scan composes the
+// lanes, and each lane then checks its items in order for an event (binade
+// crossing, the predicate, or a run that does not apply).  The first event
+// is evaluated with the reference's own f32 add and the step restarts after
+// it.  Items: f32 summands, or run markers (a NaN whose payload is the run
+// index); runfn(r, e, &f) gives run r's increment function at grid exponent
+// e, or false.  Returns the first item after which pred holds, n if none, or
+// -1 when an event falls on a run.  Wave-uniform result.
+constexpr int kWalkK = 4;
 template <class RunFn, class Pred>
 __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s_out)
 {
@@ -393,7 +338,7 @@ __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s
     float s = 0.0f;
     int pos = 0;
     while (pos < n && s == 0.0f) {               // 0 + a == a exactly
-        const float v = W[pos];
+        const float v = ldg(W + pos);
         if (is_marker(v)) {
             ParFn f;
             if (!runfn(marker_run(v), -126, &f) || f.f0 != 0u) { *s_out = s; return -1; }
@@ -403,40 +348,77 @@ __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s
         }
         pos++;
     }
-    float vnext = (pos + lane < n) ? W[pos + lane] : 0.0f;
-    for (; pos < n; pos += 64) {
-        const float v = vnext;
-        vnext = (pos + 64 + lane < n) ? W[pos + 64 + lane] : 0.0f;   // prefetch
-        const int lim = min(64, n - pos);
-        const bool mk = is_marker(v);
+    constexpr int kStep = 64 * kWalkK;
+    float vn[kWalkK];
+#pragma unroll
+    for (int q = 0; q < kWalkK; q++) {
+        const int i = pos + kWalkK * lane + q;
+        vn[q] = i < n ? ldg(W + i) : 0.0f;
+    }
+    for (; pos < n; pos += kStep) {
+        float v[kWalkK];
+#pragma unroll
+        for (int q = 0; q < kWalkK; q++) {
+            v[q] = vn[q];
+            const int i = pos + kStep + kWalkK * lane + q;   // prefetch the next window
+            vn[q] = i < n ? ldg(W + i) : 0.0f;
+        }
+        const int lim = min(kStep, n - pos);
         int start = 0;
         while (start < lim) {
             const int e = grid_exp(s);
             const uint32_t M = (uint32_t)ldexpf(s, 23 - e);
-            ParFn f = {0u, 0u};
-            bool bad = false;
-            const bool valid = lane >= start && lane < lim;
-            if (valid) {
-                if (mk) bad = !runfn(marker_run(v), e, &f);
-                else f = elem_fn(v, e);
+            ParFn f[kWalkK];
+            bool bad[kWalkK], valid[kWalkK];
+#pragma unroll
+            for (int q = 0; q < kWalkK; q++) {
+                const int idx = kWalkK * lane + q;
+                valid[q] = idx >= start && idx < lim;
+                f[q].f0 = f[q].f1 = 0u;
+                bad[q] = false;
+                if (valid[q]) {
+                    if (is_marker(v[q])) bad[q] = !runfn(marker_run(v[q]), e, &f[q]);
+                    else f[q] = elem_fn(v[q], e);
+                }
             }
-            const ParFn incl = wave_scan_incl(f);
-            const uint32_t after = par_apply(incl, M & 1u);
-            const bool cross = (M + after) >= (1u << 24);
-            const float sa = ldexpf((float)(M + after), e - 23);
-            const bool ev = valid && (cross || bad || pred(sa));
-            const uint64_t mask = __ballot(ev);
+            ParFn loc = f[0];
+#pragma unroll
+            for (int q = 1; q < kWalkK; q++) loc = par_compose(loc, f[q]);
+            const ParFn incl = wave_scan_incl(loc);
+            ParFn ex;
+            ex.f0 = __shfl_up(incl.f0, 1, 64);
+            ex.f1 = __shfl_up(incl.f1, 1, 64);
+            if (lane == 0) ex.f0 = ex.f1 = 0u;
+            uint32_t b = par_apply(ex, M & 1u);          // increments before this lane's items
+            int qev = kWalkK;
+#pragma unroll
+            for (int q = 0; q < kWalkK; q++) {
+                if (qev == kWalkK) {
+                    const uint32_t a = sat_add(b, par_apply(f[q], (M + b) & 1u));
+                    const bool cross = (M + a) >= (1u << 24);
+                    const bool ev = valid[q] && (cross || bad[q] || pred(ldexpf((float)(M + a), e - 23)));
+                    if (ev) qev = q;
+                    else b = a;
+                }
+            }
+            const uint64_t mask = __ballot(qev < kWalkK);
             if (mask == 0) {
-                s = rdl(sa, lim - 1);
+                s = ldexpf((float)(M + (uint32_t)__builtin_amdgcn_readlane((int)b, (lim - 1) / kWalkK)), e - 23);
                 break;
             }
-            const int first = __ffsll((unsigned long long)mask) - 1;
-            if (__builtin_amdgcn_readlane((int)mk, first)) { *s_out = s; return -1; }   // event on a run
-            const float prev = (first == start) ? s : rdl(sa, first - 1);
-            const float na = prev + rdl(v, first);   // the reference's f32 add
+            const int L = __ffsll((unsigned long long)mask) - 1;
+            const int q = __builtin_amdgcn_readlane(qev, L);
+            float vq = v[0];
+#pragma unroll
+            for (int k = 1; k < kWalkK; k++) if (q == k) vq = v[k];
+            const float vL = rdl(vq, L);
+            if (is_marker(vL)) { *s_out = s; return -1; }   // event on a run
+            const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)b, L);
+            const float na = ldexpf((float)(M + before), e - 23) + vL;   // the reference's f32 add
             s = na;
-            if (pred(na)) { *s_out = s; return pos + first; }
-            start = first + 1;
+            const int idx = kWalkK * L + q;
+            if (pred(na)) { *s_out = s; return pos + idx; }
+            start = idx + 1;
         }
     }
     *s_out = s;
@@ -450,6 +432,7 @@ __device__ int walk(RowSmem &sm, const float *W, int n, RunFn runfn, Pred pred, 
     if (wave_id() == 0) {
         float sv;
         const int r = wave_walk(W, n, runfn, pred, &sv);
+
         if (lane_id() == 0) { sm.seq.first = r; sm.seq.s = sv; }
     }
     __syncthreads();
@@ -457,181 +440,6 @@ __device__ int walk(RowSmem &sm, const float *W, int n, RunFn runfn, Pred pred, 
     *s_out = sm.seq.s;
     __syncthreads();
     return r;
-}
-
-template <class RunFn, class Pred>
-__device__ int block_walk(const float *W, int n, RunFn runfn, Pred pred, float *s_out, SeqSmem &sm)
-{
-    const int t = threadIdx.x;
-    float s = 0.0f;
-    int pos = 0;
-    // leading steps from s == 0: one at a time (0 + a == a exactly)
-#ifdef GS_TIMING
-    if (threadIdx.x == 0 && blockIdx.x == g_row) { g_fails[601] += n; g_fails[602]++; }
-#endif
-    while (pos < n && s == 0.0f) {
-#ifdef GS_TIMING
-        if (threadIdx.x == 0 && blockIdx.x == g_row) g_fails[603]++;
-#endif
-        const float v = W[pos];
-        if (is_marker(v)) {
-            ParFn f;
-            if (!runfn(marker_run(v), -126, &f)) { *s_out = s; return -1; }
-            if (f.f0 != 0u) { *s_out = s; return -1; }   // a run cannot open the sum
-        } else {
-            s = s + v;
-            if (pred(s)) { *s_out = s; return pos; }
-        }
-        pos++;
-    }
-    const int tile = kThreads * kSeqPer;
-    while (pos < n) {
-        const int tend = min(pos + tile, n);
-        float av[kSeqPer];
-#pragma unroll
-        for (int q = 0; q < kSeqPer; q++) {
-            const int j = pos + t * kSeqPer + q;
-            av[q] = (j < tend) ? W[j] : 0.0f;
-        }
-        int start = pos;
-        for (;;) {
-#ifdef GS_TIMING
-            if (threadIdx.x == 0 && blockIdx.x == g_row) {
-                int it = g_fails[600]++;
-                if (it < 64) { g_fails[700 + 2 * it] = (int)__builtin_amdgcn_s_memrealtime(); g_fails[701 + 2 * it] = start - pos; }
-            }
-#endif
-            const int e = grid_exp(s);
-            const uint32_t M = (uint32_t)ldexpf(s, 23 - e);
-            ParFn fn[kSeqPer];
-            bool badq[kSeqPer];
-            ParFn loc = {0u, 0u};
-#pragma unroll
-            for (int q = 0; q < kSeqPer; q++) {
-                const int j = pos + t * kSeqPer + q;
-                badq[q] = false;
-                fn[q].f0 = 0u;
-                fn[q].f1 = 0u;
-                if (j >= start && j < tend) {
-                    if (is_marker(av[q])) badq[q] = !runfn(marker_run(av[q]), e, &fn[q]);
-                    else fn[q] = elem_fn(av[q], e);
-                }
-                loc = par_compose(loc, fn[q]);
-            }
-            if (t == 0) sm.first = 0x7fffffff;
-            const ParFn ex = block_scan_excl(loc, sm);   // contains a barrier
-            const uint32_t pM = M & 1u;
-            uint32_t before = par_apply(ex, pM);
-            int my_first = 0x7fffffff;
-#pragma unroll
-            for (int q = 0; q < kSeqPer; q++) {
-                const int j = pos + t * kSeqPer + q;
-                const uint32_t inc = par_apply(fn[q], (pM + before) & 1u);
-                const uint32_t after = sat_add(before, inc);
-                if (j >= start && j < tend && my_first == 0x7fffffff) {
-                    const bool cross = (M + after) >= (1u << 24);
-                    const bool stop = !cross && pred(ldexpf((float)(M + after), e - 23));
-                    if (cross || stop || badq[q]) my_first = j;
-                }
-                before = after;
-            }
-            if (my_first != 0x7fffffff) atomicMin(&sm.first, my_first);
-            __syncthreads();
-            const int first = sm.first;
-            if (first == 0x7fffffff) {
-                const int last = tend - 1;
-                const int owner = (last - pos) / kSeqPer;
-                if (t == owner) {
-                    uint32_t b2 = par_apply(ex, pM);
-#pragma unroll
-                    for (int q = 0; q < kSeqPer; q++) {
-                        const int j = pos + t * kSeqPer + q;
-                        if (j <= last) b2 = sat_add(b2, par_apply(fn[q], (pM + b2) & 1u));
-                    }
-                    sm.s = ldexpf((float)(M + b2), e - 23);
-                }
-                __syncthreads();
-                s = sm.s;
-                __syncthreads();
-                break;
-            }
-            const int owner = (first - pos) / kSeqPer;
-            if (t == owner) {
-                uint32_t b2 = par_apply(ex, pM);
-                float sa = s;
-                int nxt = first + 1;
-#pragma unroll
-                for (int q = 0; q < kSeqPer; q++) {
-                    const int j = pos + t * kSeqPer + q;
-                    if (j >= start && j < first) b2 = sat_add(b2, par_apply(fn[q], (pM + b2) & 1u));
-                    if (j == first) {
-                        if (is_marker(av[q])) nxt = -1;            // event on a run
-                        else {
-                            const float sb = ldexpf((float)(M + b2), e - 23);
-                            sa = sb + av[q];                        // the reference's f32 add
-                            if (pred(sa)) nxt = -2 - first;
-                        }
-                    }
-                }
-                sm.s = sa;
-                sm.start = nxt;
-            }
-            __syncthreads();
-            s = sm.s;
-            const int nxt = sm.start;
-            __syncthreads();
-            if (nxt == -1) { *s_out = s; return -1; }
-            if (nxt < -1) { *s_out = s; return -2 - nxt; }
-            start = nxt;
-            if (start >= tend) break;
-        }
-        pos = tend;
-    }
-    *s_out = s;
-    return n;
-}
-
-// One accumulation over runs and groups (all threads call).  With last_g >= 0
-// it stops after the first last_n elements of group last_g.  tie_up adds the
-// run's seq-1 tie count (ties rounded up instead of down).  Returns false on
-// a failed check; *stop_g = -1 if the predicate never held.
-template <class A, class P>
-__device__ bool walk_seq(RowSmem &sm, const uint64_t *gl, int which, bool tie_up, int last_g, int last_n,
-                         A a_of, P pred, float *s_out, int *stop_g, int *stop_j)
-{
-    BinsSmem &bn = sm.x.bn;
-    const int G = bn.ngroups;
-    float s = 0.0f;
-    *stop_g = -1;
-    *stop_j = -1;
-    for (int g = 0; g <= G; g++) {
-        if (last_g >= 0 && g > last_g) break;
-        if (g > 0 && bn.runb[g] != kNoRun) {
-            const int packed = bn.runb[g];
-            if (which == 2 && !(packed & (1 << 24))) return false;
-            if (which == 3 && !(packed & (1 << 25))) return false;
-            const uint64_t R = bn.run[g] + (tie_up ? bn.runt[g] : 0u);
-            if (R) {
-                if (!(s > 0.0f)) return false;
-                const int eb = ((packed >> (8 * (which - 1))) & 255) - 128;
-                const int e = grid_exp(s);
-                if (e != eb) return false;
-                const uint64_t M = (uint64_t)ldexpf(s, 23 - e);
-                if (M + R >= (1ull << 24)) return false;
-                s = ldexpf((float)(M + R), e - 23);
-                if (pred(s)) return false;   // the event lies inside the run
-            }
-        }
-        if (g == G) break;
-        const uint32_t b0 = bn.gbeg[g];
-        const int n = (g == last_g) ? last_n : (int)(bn.gend[g] - b0);
-        float so;
-        const int stop = block_seqsum([&](int j) { return a_of(gl[b0 + j]); }, n, s, pred, &so, sm.seq);
-        s = so;
-        if (stop < n) { *stop_g = g; *stop_j = stop; break; }
-    }
-    *s_out = s;
-    return true;
 }
 
 // Clear the unused tail of the collected segments selected by `sel` and sort
@@ -643,7 +451,7 @@ __device__ bool finish_segments(RowSmem &sm, uint64_t *gl, Sel sel)
     const int t = threadIdx.x;
     for (int b = t; b < kBins; b += kThreads) {
         if (!sel(b)) continue;
-        for (uint32_t j = bn.cnt[b] & ~kNow; j < bn.off[b + 1]; j++) gl[j] = 0ull;
+        for (uint32_t j = bn.cnt[b] & ~kNow; j < bn.off[b + 1]; j++) stg(gl + j, (uint64_t)0);
     }
     __threadfence_block();
     __syncthreads();
@@ -683,7 +491,7 @@ __device__ __forceinline__ RunFn run_fn(const BinsSmem &bn, int which, bool tie_
 // sorted entries as exact summands expf(y - m) (0 for removed entries);
 // a final marker for the run after the last group.  WT holds token ids.
 // Returns the item count, or -1 if it does not fit.
-__device__ int build_walk(RowSmem &sm, const uint64_t *gl, float *W, uint32_t *WT, float m)
+__device__ int build_walk(RowSmem &sm, const uint64_t *gl, float *W, uint32_t *WT, float m, float m0, bool mass)
 {
     BinsSmem &bn = sm.x.bn;
     const int t = threadIdx.x;
@@ -696,51 +504,315 @@ __device__ int build_walk(RowSmem &sm, const uint64_t *gl, float *W, uint32_t *W
     __syncthreads();
     const uint32_t N = tot + 1;
     if (N > kWalkCap) return -1;
-    for (int g = t; g <= G; g += kThreads) { W[bn.wbase[g]] = make_marker(g); WT[bn.wbase[g]] = 0xffffffffu; }
-    for (int g = 0; g < G; g++) {
-        const uint32_t b0 = bn.gbeg[g], n = bn.gend[g] - b0, w0 = bn.wbase[g] + 1;
-        for (uint32_t p = t; p < n; p += kThreads) {
-            const uint64_t en = gl[b0 + p];
-            W[w0 + p] = en ? glibc_expf(key2f((uint32_t)(en >> 32)) - m) : 0.0f;
-            WT[w0 + p] = ~(uint32_t)en;
+    // one item per thread: group by binary search over the marker positions
+    for (uint32_t w = t; w < N; w += kThreads) {
+        int lo = 0, hi = G;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (bn.wbase[mid] <= w) lo = mid;
+            else hi = mid - 1;
         }
+        const uint32_t w0 = bn.wbase[lo];
+        if (w == w0) {
+            stg(W + w, make_marker(lo));
+            stg(WT + w, 0xffffffffu);
+            continue;
+        }
+        const uint64_t en = ldg(gl + bn.gbeg[lo] + (w - w0 - 1));
+        const float y = key2f((uint32_t)(en >> 32));
+        const float e = en ? glibc_expf(y - m) : 0.0f;
+        stg(W + w, e);
+        stg(WT + w, ~(uint32_t)en);
+        // masses of collected bins (plan B); overflow entries are summed there
+        if (mass && en && y - m0 <= kDUp) atomicAdd(reinterpret_cast<float *>(&bn.k2[bin_clamp(y - m0)]), e);
     }
     __threadfence_block();
     __syncthreads();
     return (int)N;
 }
 
+__device__ __forceinline__ float next_up(float v) { return __uint_as_float(__float_as_uint(v) + 1u); }
+
+// Increment of p = e / S (src/sampler.rs:56) over every f32 S in [Slo, Shi]
+// (at most 8 values).  Returns 2 if some value is a rounding tie, out of
+// range, or the range is too wide; 0 if all give the same increment (*k);
+// 1 if they differ (the increment waits for the exact S).
+__device__ __forceinline__ int inc_s_range(float e, float Slo, float Shi, int b, uint32_t *k)
+{
+    int n = 0;
+    uint32_t k0 = 0;
+    bool same = true;
+    for (float S = Slo; S <= Shi; S = next_up(S)) {
+        if (++n > 8) return 2;
+        uint32_t kk;
+        if (inc_exact(e / S, b, &kk) != 1) return 2;
+        if (n == 1) k0 = kk;
+        else same &= kk == k0;
+    }
+    *k = k0;
+    return same ? 0 : 1;
+}
+
+// Pass constants, kept in registers by the pass loops.
+struct PassK {
+    float m0, m, inv_s, inv_s2, hw2;
+};
+// Classification of one element: cl 0 nothing to do, 1 list it, 2 defer it,
+// 3 add increment k to bin b.  Branch-free; one LDS read (meta).
+struct Cls {
+    int b, cl;
+    uint32_t k;
+};
+// Pass 2: accumulation 1 (src/sampler.rs:54).
+__device__ __forceinline__ Cls classify1(const BinsSmem &bn, const PassK &K, float y)
+{
+    const float dp = y - K.m0;
+    const bool inr = (dp <= kDUp) && (dp >= -kDLo);
+    Cls c;
+    c.b = bin_clamp(dp);
+    const uint32_t mt = bn.meta[c.b];
+    const bool ok = inc_of(ldexpf(fast_exp(y - K.m), 23 - meta_b(mt, 1)), 2.0f * kExpErr, &c.k);
+    c.cl = !inr ? 0 : ((mt & kMetaCol) ? 1 : (ok ? 3 : 2));
+    return c;
+}
+// Pass 3: accumulation 2, p = e / S (src/sampler.rs:56, :61-63).
+__device__ __forceinline__ Cls classify3(const BinsSmem &bn, const PassK &K, float y)
+{
+    const float dp = y - K.m0;
+    const bool inr = (dp <= kDUp) && (dp >= -kDLo);
+    Cls c;
+    c.b = bin_clamp(dp);
+    const uint32_t mt = bn.meta[c.b];
+    const float p = fast_exp(y - K.m) * K.inv_s;
+    const bool ok = inc_of(ldexpf(p, 23 - meta_b(mt, 2)), K.hw2, &c.k);
+    c.cl = !inr ? 0 : ((mt & kMetaNow) ? 1 : (((mt & kMetaCol) || !(mt & 2u)) ? 0 : (ok ? 3 : 2)));
+    return c;
+}
+// Pass 4: accumulation 3, q = p / s2 (src/sampler.rs:68, :74-75).
+__device__ __forceinline__ Cls classify4(const BinsSmem &bn, const PassK &K, float y)
+{
+    const float dp = y - K.m0;
+    const bool inr = (dp <= kDUp) && (dp >= -kDLo);
+    Cls c;
+    c.b = bin_clamp(dp);
+    const uint32_t mt = bn.meta[c.b];
+    const float q = fast_exp(y - K.m) * K.inv_s * K.inv_s2;
+    const bool ok = inc_of(ldexpf(q, 23 - meta_b(mt, 3)), 2.0f * kExpErr + 0x1p-21f, &c.k);
+    c.cl = !inr ? 0 : ((mt & kMetaNow) ? 1 : (((mt & kMetaCol) || !(mt & 4u)) ? 0 : (ok ? 3 : 2)));
+    return c;
+}
+
+// One cached pass over the row, then over the penalized values: each element
+// is listed (bins flagged kNow), deferred, or adds its increment to acc[b],
+// as cls says.  Raw contributions of penalized ids are undone first.
+template <class ClsF>
+__device__ void bins_pass(RowSmem &sm, const float *row, int V, bool t_one, float T, bool has_pen,
+                          uint64_t *gl, uint32_t *defer, uint32_t dcap, uint32_t *acc, ClsF cls)
+{
+    BinsSmem &bn = sm.x.bn;
+    const int t = threadIdx.x;
+    auto act = [&](int i, float y, const Cls &c, uint32_t flag) {
+        if (c.cl == 1) {
+            const uint32_t slot = atomicAdd(&bn.cnt[c.b], 1u) & ~kNow;
+            stg(gl + slot, list_entry(y, (uint32_t)i));
+        } else if (c.cl == 2) {
+            const int slot = atomicAdd(&bn.ndefer, 1);
+            if ((uint32_t)slot < dcap) stg(defer + slot, (uint32_t)i | flag);
+        } else if (c.cl == 3 && c.k) {
+            atomicAdd(&acc[c.b], c.k);
+        }
+    };
+    auto act0 = [&](int i, float y, const Cls &c) { act(i, y, c, 0u); };
+    if (t_one) row_for_each_cls(row, V, [](float x) { return x; }, cls, act0);
+    else row_for_each_cls(row, V, [T](float x) { return x / T; }, cls, act0);
+    __syncthreads();
+    if (!has_pen) return;
+    for (int s = t; s < kHashSlots; s += kThreads) {
+        const uint32_t id = sm.hkey[s];
+        if (id == kEmpty) continue;
+        const float x = ldg(row + id);
+        const Cls c = cls(t_one ? x : x / T);
+        if (c.cl == 3 && c.k) atomicAdd(&acc[c.b], 0u - c.k);
+    }
+    for (int b = t; b < kBins; b += kThreads) {
+        if (!(bn.cnt[b] & kNow)) continue;
+        for (uint32_t j = bn.off[b]; j < (bn.cnt[b] & ~kNow); j++)
+            if (hash_find(sm, ~(uint32_t)ldg(gl + j)) >= 0) stg(gl + j, (uint64_t)0);
+    }
+    const int nd = min((uint32_t)bn.ndefer, dcap);
+    for (int j = t; j < nd; j += kThreads)
+        if (hash_find(sm, ldg(defer + j) & kIdMask) >= 0) stg(defer + j, 0xffffffffu);
+    __threadfence_block();
+    __syncthreads();
+    for (int s = t; s < kHashSlots; s += kThreads) {
+        const uint32_t id = sm.hkey[s];
+        if (id == kEmpty) continue;
+        const float yp = __uint_as_float(sm.hval[s]);
+        const float y = t_one ? yp : yp / T;
+        act((int)id, y, cls(y), 0x80000000u);
+    }
+    __syncthreads();
+}
+
+// List the elements of the bins flagged kNow (one pass over the row, then the
+// penalized values), sort those segments and clear the flag.
+__device__ bool collect_now(RowSmem &sm, const float *row, int V, bool t_one, float T, bool has_pen, uint64_t *gl)
+{
+    BinsSmem &bn = sm.x.bn;
+    const int t = threadIdx.x;
+    auto visit = [&](int i, float y) {
+        const float dp = y - bn.m0;
+        if (!(dp <= kDUp) || dp < -kDLo) return;
+        const int b = bin_of(dp);
+        if (bn.cnt[b] & kNow) {
+            const uint32_t slot = atomicAdd(&bn.cnt[b], 1u) & ~kNow;
+            stg(gl + slot, list_entry(y, (uint32_t)i));
+        }
+    };
+    if (t_one) row_for_each(row, V, true, visit);
+    else row_for_each(row, V, true, [&](int i, float x) { visit(i, x / T); });
+    __syncthreads();
+    if (has_pen) {
+        for (int b = t; b < kBins; b += kThreads) {
+            if (!(bn.cnt[b] & kNow)) continue;
+            for (uint32_t j = bn.off[b]; j < (bn.cnt[b] & ~kNow); j++)
+                if (hash_find(sm, ~(uint32_t)gl[j]) >= 0) gl[j] = 0ull;
+        }
+        __threadfence_block();
+        __syncthreads();
+        for (int s = t; s < kHashSlots; s += kThreads) {
+            const uint32_t id = sm.hkey[s];
+            if (id == kEmpty) continue;
+            const float yp = __uint_as_float(sm.hval[s]);
+            visit((int)id, t_one ? yp : yp / T);
+        }
+        __syncthreads();
+    }
+    return true;
+}
+
+// Sort the segments of the kNow bins descending (entries are distinct; removed
+// entries are 0 and go last), zero their unused tails and clear the flag.
+// Work items are 64-entry chunks of the segments, spread over all waves: each
+// lane ranks one entry against its whole segment and writes it to tmp (room
+// for kWalkCap entries); a second phase copies back.  False if a segment
+// exceeds kMaxSeg or tmp is too small.
+__device__ bool finish_now(RowSmem &sm, uint64_t *gl, uint64_t *tmp)
+{
+    BinsSmem &bn = sm.x.bn;
+    const int t = threadIdx.x, lane = lane_id();
+    constexpr int kPer = kBins / kThreads;
+    uint32_t nit[kPer], loc = 0;
+#pragma unroll
+    for (int c = 0; c < kPer; c++) {
+        const int b = kPer * t + c;
+        const uint32_t cb = bn.cnt[b];
+        uint32_t n = 0;
+        if (cb & kNow) {
+            const uint32_t cur = cb & ~kNow;
+            n = cur - bn.off[b];
+            for (uint32_t j = cur; j < bn.off[b + 1]; j++) stg(gl + j, (uint64_t)0);
+        }
+        if (n > (uint32_t)kMaxSeg) bn.fail = 1;
+        nit[c] = (n + 63u) >> 6;
+        loc += nit[c];
+    }
+    uint32_t tot;
+    uint32_t ex = block_excl_u32(loc, &tot, sm);
+#pragma unroll
+    for (int c = 0; c < kPer; c++) {
+        bn.sbase[kPer * t + c] = ex;
+        ex += nit[c];
+    }
+    __threadfence_block();
+    __syncthreads();
+    if (bn.fail || tot * 64u > kWalkCap) return false;
+    auto item_bin = [&](uint32_t it) {
+        int lo = 0, hi = kBins - 1;                 // largest b with sbase[b] <= it
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (bn.sbase[mid] <= it) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
+    for (uint32_t it = wave_id(); it < tot; it += kWaves) {
+        const int b = __builtin_amdgcn_readfirstlane(item_bin(it));
+        const uint32_t o = __builtin_amdgcn_readfirstlane(bn.off[b]);
+        const uint32_t n = __builtin_amdgcn_readfirstlane((bn.cnt[b] & ~kNow) - o);
+        const uint32_t j = 64u * (it - bn.sbase[b]) + lane;
+        // the segment in registers (lane l holds entries l, l + 64, ...), then
+        // v_readlane broadcasts
+        uint64_t seg[kMaxSeg / 64];
+#pragma unroll
+        for (int k = 0; k < kMaxSeg / 64; k++) {
+            const uint32_t idx = 64u * k + lane;
+            seg[k] = idx < n ? ldg(gl + o + idx) : 0ull;
+        }
+        const uint64_t mine = j < n ? ldg(gl + o + j) : 0ull;
+        uint32_t rank = 0;
+#pragma unroll
+        for (int k = 0; k < kMaxSeg / 64; k++) {
+            if (64u * k >= n) break;
+            const uint32_t lim = min(64u, n - 64u * k);
+            const uint32_t lo32 = (uint32_t)seg[k], hi32 = (uint32_t)(seg[k] >> 32);
+            for (uint32_t l = 0; l < lim; l++) {
+                const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi32, l) << 32) |
+                                       (uint32_t)__builtin_amdgcn_readlane((int)lo32, l);
+                const uint32_t i = 64u * k + l;
+                rank += (other > mine) | ((other == mine) & (i < j));
+            }
+        }
+        if (j < n) stg(tmp + 64u * bn.sbase[b] + rank, mine);
+    }
+    __threadfence_block();
+    __syncthreads();
+    for (uint32_t it = wave_id(); it < tot; it += kWaves) {
+        const int b = item_bin(it);
+        const uint32_t o = bn.off[b], n = (bn.cnt[b] & ~kNow) - o;
+        const uint32_t j = 64u * (it - bn.sbase[b]) + lane;
+        if (j < n) stg(gl + o + j, ldg(tmp + 64u * bn.sbase[b] + j));
+    }
+    __threadfence_block();
+    __syncthreads();
+    for (int b = t; b < kBins; b += kThreads)
+        if (bn.cnt[b] & kNow) { bn.cnt[b] = bn.off[b + 1]; bn.meta[b] &= ~kMetaNow; }
+    __syncthreads();
+    return true;
+}
+
 // ---------------------------------------------------------------------------
 // The binned path.  Returns true with *tok / *status set, or false to ask for
 // the sort-based path.  Needs a 16-byte aligned row and `gl`, a per-row list
-// of lcap >= V + kOverCap + 2*kHashSlots u64 entries in global memory.
+// of lcap u64 entries in global memory.
 __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, float top_p,
                               bool has_pen, float r, uint64_t *gl, uint32_t lcap, int *tok,
                               int *status)
 {
-    // deferred ids live in the upper part of the scratch row
+    // deferred ids and the walk arrays live after the list
     const uint32_t lneed = (uint32_t)V + (uint32_t)(kOverCap + 2 * kHashSlots);
     if (lcap < lneed + kDeferCapG / 2 + kWalkCap) BINS_FAIL();
     uint32_t *defer = reinterpret_cast<uint32_t *>(gl + lneed);
     const uint32_t dcap = kDeferCapG;
     float *W = reinterpret_cast<float *>(gl + lneed + kDeferCapG / 2);
     uint32_t *WT = reinterpret_cast<uint32_t *>(W + kWalkCap);
+    uint64_t *tmp = reinterpret_cast<uint64_t *>(W);       // segment sort staging (W is dead then)
     BinsSmem &bn = sm.x.bn;
     const int t = threadIdx.x;
     const bool t_one = (T == 1.0f);
+    const bool nucleus = top_p < 1.0f;
     const float4 *r4 = reinterpret_cast<const float4 *>(row);
     const int n4 = V >> 2;
     if (n4 == 0) BINS_FAIL();
 
     for (int b = t; b < kBins; b += kThreads) bn.cnt[b] = 0;
-    if (t == 0) { bn.nover = 0; bn.ndefer = 0; bn.fail = 0; bn.ncollect = 0; }
+    if (t == 0) { bn.nover = 0; bn.ndefer = 0; bn.fail = 0; bn.ncollect = 0; bn.nties = 0; }
 
-    // ---- pass 1: counts, max, NaN ------------------------------------------
+    // ---- pass 1 (HBM): counts, max, NaN -------------------------------------
     float tmax = -INFINITY;
     int nan = 0;
     float m0 = 0.0f;
-    auto visit = [&](int i, float x) {
-        const float y = t_one ? x : x / T;
+    auto visit = [&](int i, float y) {
         nan |= (int)isnan(y);
         if (y > tmax && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) tmax = y;
         const float dp = y - m0;
@@ -754,10 +826,8 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     for (int base = 0; base < n4; base += kThreads * kUnroll) {
         float4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int q = base + u * kThreads + t;
-            if (q < n4) v[u] = r4[q];
-        }
+        for (int u = 0; u < kUnroll; u++)
+            v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));   // unconditional: no wait between loads
         if (base == 0) {
             float lm = -INFINITY;
 #pragma unroll
@@ -769,18 +839,31 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
             m0 = t_one ? bm : bm / T;
             if (!isfinite(m0)) BINS_FAIL();
         }
+        if (t_one) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int q = base + u * kThreads + t;
-            if (q < n4) {
-                visit(4 * q + 0, v[u].x);
-                visit(4 * q + 1, v[u].y);
-                visit(4 * q + 2, v[u].z);
-                visit(4 * q + 3, v[u].w);
+            for (int u = 0; u < kUnroll; u++) {
+                const int q = base + u * kThreads + t;
+                if (q < n4) {
+                    visit(4 * q + 0, v[u].x);
+                    visit(4 * q + 1, v[u].y);
+                    visit(4 * q + 2, v[u].z);
+                    visit(4 * q + 3, v[u].w);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                const int q = base + u * kThreads + t;
+                if (q < n4) {
+                    visit(4 * q + 0, v[u].x / T);
+                    visit(4 * q + 1, v[u].y / T);
+                    visit(4 * q + 2, v[u].z / T);
+                    visit(4 * q + 3, v[u].w / T);
+                }
             }
         }
     }
-    for (int i = (n4 << 2) + t; i < V; i += kThreads) visit(i, row[i]);
+    for (int i = (n4 << 2) + t; i < V; i += kThreads) visit(i, t_one ? row[i] : row[i] / T);
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {
             if (sm.hkey[s] == kEmpty) continue;
@@ -798,7 +881,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     if (!isfinite(m)) BINS_FAIL();
     // bins must cover [m - 18.5, m]; a first-round max above m (penalized) breaks that
     if (bn.nover > kOverCap || m0 > m) BINS_FAIL();
-    GS_STAMP(10);
+    GS_STAMP(9);
 
     // ---- penalty: penalized values join the counts and the overflow --------
     if (has_pen) {
@@ -822,125 +905,217 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     }
     const int nover = bn.nover;
 
-    // ---- plan ---------------------------------------------------------------
+    // ---- plan A: accumulation 1 ----------------------------------------------
+    // The running sum before bin b is predicted from counts times the bin's
+    // central value; its binade gives the bin's grid.  Collected: the bin that
+    // opens the sum, bins where it may change binade, bins with likely
+    // rounding ties, and bins whose increment sum might not fit 32 bits.
     constexpr int kPer = kBins / kThreads;
     static_assert(kPer * kThreads == kBins, "bins per thread");
     const float wbin = (kDUp + kDLo) / (float)kBins;
     const float shift = m0 - m;            // e = exp(d' + shift)
     auto e_at = [&](float bpos) { return (double)fast_exp(kDUp - bpos * wbin + shift); };
-    double osum = 0.0;
-    for (int j = t; j < nover; j += kThreads) {
-        const uint64_t en = bn.over[j];
-        if (en) osum += (double)fast_exp(key2f((uint32_t)(en >> 32)) - m);
-    }
-    osum = block_sum_f64(osum, sm);
-    uint32_t cntv[kPer];
-    double eb[kPer];
-    double loc = 0.0;
-    uint32_t ctot = 0;
-#pragma unroll
-    for (int c = 0; c < kPer; c++) {
-        const int b = kPer * t + c;
-        cntv[c] = bn.cnt[b];
-        eb[c] = (double)cntv[c] * e_at((float)b + 0.5f);
-        loc += eb[c];
-        ctot += cntv[c];
-    }
-    double stot;
-    const double pre = block_excl_f64(loc, &stot, sm) + osum;
-    stot += osum;
-    uint32_t call;
-    const uint32_t cpre = block_excl_u32(ctot, &call, sm);
-    if ((uint32_t)nover + call > lcap) BINS_FAIL();
-    double plo[kPer + 1];
-    plo[0] = pre;
-#pragma unroll
-    for (int c = 0; c < kPer; c++) plo[c + 1] = plo[c] + eb[c];
-    // Predicted seq-1 result: in a bulk bin every summand is rounded to the
-    // grid of the running sum (src/sampler.rs:54); with the bin's summands
-    // between its edge values, a bin inside one rounding cell contributes
-    // count * k exactly, a bin across one cell boundary is split by the
-    // position of the boundary (summands uniform in d), and wide bins
-    // contribute their mean.
-    double spred = 0.0;
-#pragma unroll
-    for (int c = 0; c < kPer; c++) {
-        const int b = kPer * t + c;
-        if (cntv[c] == 0) continue;
-        if (plo[c] <= 0.0) { spred += eb[c]; continue; }
-        const double g = ldexp(1.0, grid_exp((float)plo[c]) - 23);
-        const double mlo = e_at((float)b + 1.0f) / g, mhi = e_at((float)b) / g;
-        const double klo = floor(mlo + 0.5), khi = floor(mhi + 0.5);
-        double k;
-        if (klo == khi) k = klo;
-        else if (khi == klo + 1.0) {
-            const double h = klo + 0.5;
-            const double f = (log(mhi) - log(h)) / (log(mhi) - log(mlo));
-            k = klo + f;
-        } else k = eb[c] / ((double)cntv[c] * g);
-        spred += (double)cntv[c] * k * g;
-    }
-    spred = block_sum_f64(spred, sm) + osum;
-    const double lost = stot - spred;
-    const double Spred = stot - lost;
-    const bool nucleus = top_p < 1.0f;
-    if (t == 0) { bn.cut_g = kBins; bn.Spred = (float)Spred; }
-    __syncthreads();
-    double s2lo = 1.0, s2hi = 1.0;
-    if (nucleus) {
-        if (stot / Spred < (double)top_p * (1.0 + 2.0 * kDelta)) BINS_FAIL();   // the cut may not happen
-#pragma unroll
-        for (int c = 0; c < kPer; c++) {
-            if (cntv[c] == 0) continue;
-            if (plo[c + 1] / Spred * (1.0 + kDelta) >= (double)top_p) { atomicMin(&bn.cut_g, kPer * t + c); break; }
-        }
-        __syncthreads();
-        const int cb = bn.cut_g;
-        if (cb >= kBins) BINS_FAIL();
-        // the cut element lies in bin cb, or anywhere from the max (e = 1) on
-        // if the overflow segment may already reach top_p
-        const double ehc = (osum / Spred * (1.0 + kDelta) >= (double)top_p) ? 1.0 : e_at((float)cb) * 1.001;
-        s2lo = (double)top_p;
-        s2hi = (double)top_p + ehc / Spred * (1.0 + 4.0 * kDelta);
-    }
-    const double s2c = 0.5 * (s2lo + s2hi);
-    const float hw2 = kDeltaS + 2.0f * kExpErr + 4.0f / 16777216.0f;
-    const float hw3 = hw2 + (float)((s2hi - s2lo) / (2.0 * s2c)) + 4.0f / 16777216.0f;
-    if (t == 0) {
-        bn.inv_spred = (float)(1.0 / Spred);
-        bn.inv_s2c = nucleus ? (float)(1.0 / s2c) : 1.0f;
-        bn.hw2 = hw2;
-        bn.hw3 = hw3;
-        bn.s2lo = (float)s2lo;
-        bn.s2hi = (float)s2hi;
-        bn.off[kBins] = (uint32_t)nover + call;
-    }
+    const double dl = 1.0 - kDelta, dh = 1.0 + kDelta;
     {
-        uint32_t o = (uint32_t)nover + cpre;
+        double osum = 0.0;
+        for (int j = t; j < nover; j += kThreads) {
+            const uint64_t en = bn.over[j];
+            if (en) osum += (double)fast_exp(key2f((uint32_t)(en >> 32)) - m);
+        }
+        osum = block_sum_f64(osum, sm);
+        uint32_t cntv[kPer];
+        double eb[kPer];
+        double loc = 0.0;
+        uint32_t ctot = 0;
 #pragma unroll
         for (int c = 0; c < kPer; c++) {
             const int b = kPer * t + c;
-            const double lo = plo[c], hi = plo[c + 1];
+            cntv[c] = bn.cnt[b];
+            eb[c] = (double)cntv[c] * e_at((float)b + 0.5f);
+            loc += eb[c];
+            ctot += cntv[c];
+        }
+        double stot;
+        const double pre = block_excl_f64(loc, &stot, sm) + osum;
+        uint32_t call;
+        const uint32_t cpre = block_excl_u32(ctot, &call, sm);
+        if ((uint32_t)nover + call > lneed) BINS_FAIL();
+        if (t == 0) bn.off[kBins] = (uint32_t)nover + call;
+        uint32_t o = (uint32_t)nover + cpre;
+        double lo = pre;
+#pragma unroll
+        for (int c = 0; c < kPer; c++) {
+            const int b = kPer * t + c;
+            const double hi = lo + eb[c];
             const double ehi = e_at((float)b) * 1.001;
-            const double dl = 1.0 - kDelta, dh = 1.0 + kDelta;
             const double cn = (double)cntv[c];
             bool col = !(lo > 0.0);
-            int b1 = 0, b2 = 0, b3 = 0;
-            bool k2 = false, k3 = false;
+            int b1 = 0;
             if (cntv[c] && !col) {
                 b1 = grid_exp((float)lo);
                 col |= grid_exp((float)(lo * dl)) != grid_exp((float)(hi * dh));
                 const int c1 = ilogb(ehi);
                 if (c1 < b1) col |= cn * ldexp(1.0, c1 - b1) > kTieThr;
                 col |= cn * (ldexp(ehi, 23 - b1) + 1.0) >= 4.0e9;
-                const double plo_ = lo / Spred, phi_ = hi / Spred;
-                const double pe = ehi / Spred;
-                bool reach3 = true;
+            }
+            if (cntv[c] == 0) col = false;
+            bn.meta[b] = (col ? kMetaCol | kMetaNow : 0u) | (cntv[c] ? 8u : 0u) | ((uint32_t)(b1 + 128) << 8) |
+                         (128u << 16) | (128u << 24);
+            bn.off[b] = o;
+            bn.cnt[b] = col ? o | kNow : o;  // list cursor of collected bins
+            bn.esum[b] = 0u;
+            bn.k2[b] = 0u;                  // collected masses accumulate here (f32)
+            o += cntv[c];
+            lo = hi;
+        }
+    }
+    for (int j = t; j < nover; j += kThreads) stg(gl + j, bn.over[j]);
+    __syncthreads();
+    GS_STAMP(10);
+
+    // ---- pass 2 (cache): accumulation-1 increments, collected bins listed ----
+    PassK K;
+    K.m0 = m0;
+    K.m = m;
+    K.inv_s = 1.0f;
+    K.inv_s2 = 1.0f;
+    K.hw2 = 0.0f;
+    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.esum,
+              [&bn, K](float y) { return classify1(bn, K, y); });
+    GS_STAMP(11);
+    if ((uint32_t)bn.ndefer > dcap) BINS_FAIL();
+    if (!finish_now(sm, gl, tmp)) BINS_FAIL();
+    if (wave_id() == 0 && !wave_sort_segment(gl, nover)) bn.fail = 1;
+    __threadfence_block();
+    __syncthreads();
+    if (bn.fail) BINS_FAIL();
+    GS_STAMP(12);
+
+    // ---- exact accumulation-1 increments of the deferred elements ------------
+    auto def_y = [&](uint32_t en) {
+        const uint32_t id = en & kIdMask;
+        float x = ldg(row + id);
+        if (en & 0x80000000u) {
+            const int s = hash_find(sm, id);
+            if (s >= 0) x = __uint_as_float(sm.hval[s]);
+        }
+        return t_one ? x : x / T;
+    };
+    {
+        const int nd = bn.ndefer;
+        for (int j = t; j < nd; j += kThreads) {
+            const uint32_t en = ldg(defer + j);
+            if (en == 0xffffffffu) continue;
+            const float y = def_y(en);
+            const int b = bin_of(y - m0);
+            uint32_t k;
+            const int rc = inc_exact(glibc_expf(y - m), meta_b(bn.meta[b], 1), &k);
+            if (rc < 0) { bn.fail = 1; continue; }
+            if (k) atomicAdd(&bn.esum[b], k);
+            if (rc == 0) {                  // tie: the lower choice is added, the tie counted
+                const uint32_t old = atomicAdd(&bn.meta[b], 16u);
+                if (((old >> 4) & 7u) == 7u) bn.fail = 1;
+                atomicAdd(&bn.nties, 1);
+            }
+        }
+    }
+    __syncthreads();
+    if (bn.fail) BINS_FAIL();
+
+    // ---- S, bracketed by the ties rounded down / up --------------------------
+    if (!build_groups(sm)) BINS_FAIL();
+    gather_runs(sm, 1);
+    int N = build_walk(sm, gl, W, WT, m, m0, true);
+    if (N < 0) BINS_FAIL();
+    GS_STAMP(13);
+    GS_DIAG(26, N);
+    GS_DIAG(28, bn.ndefer);
+    GS_DIAG(30, bn.nties);
+    float Slo, Shi;
+    if (walk(sm, W, N, run_fn(bn, 1, false), [](float) { return false; }, &Slo) != N) BINS_FAIL();
+    Shi = Slo;
+    const bool s_exact = bn.nties == 0;
+    if (!s_exact && walk(sm, W, N, run_fn(bn, 1, true), [](float) { return false; }, &Shi) != N) BINS_FAIL();
+    if (!(Slo > 0.0f) || !(Shi >= Slo) || !isfinite(Shi)) BINS_FAIL();
+    GS_STAMP(14);
+
+    // ---- plan B: accumulations 2 and 3 ---------------------------------------
+    // Masses: bulk bins from their exact seq-1 increments, collected bins and
+    // the overflow from their exact summands.  With S bracketed, the seq-2
+    // running sum before each bin is known to the rounding of the increments:
+    // bulk bins before the cut get seq-2 increments in pass 3; bins where it
+    // may change binade or reach top_p are collected.
+    double osum = 0.0;
+    for (int j = t; j < nover; j += kThreads) {
+        const uint64_t en = ldg(gl + j);
+        if (en) osum += (double)glibc_expf(key2f((uint32_t)(en >> 32)) - m);
+    }
+    osum = block_sum_f64(osum, sm);          // contains barriers
+    const double Sc = 0.5 * ((double)Slo + (double)Shi);
+    const double iSc = 1.0 / Sc;
+    {
+        uint32_t mtv[kPer];
+        double mass[kPer];
+        double loc = 0.0;
+#pragma unroll
+        for (int c = 0; c < kPer; c++) {
+            const int b = kPer * t + c;
+            mtv[c] = bn.meta[b];
+            if (mtv[c] & 1u) mass[c] = (double)__uint_as_float(bn.k2[b]);
+            else mass[c] = ldexp((double)bn.esum[b] + 0.5 * (double)((mtv[c] >> 4) & 7u), meta_b(mtv[c], 1) - 23);
+            if (!(mtv[c] & 8u)) mass[c] = 0.0;
+            loc += mass[c];
+        }
+        double stot;
+        const double pre = block_excl_f64(loc, &stot, sm) + osum;
+        stot += osum;
+        double s2lo = 1.0, s2hi = 1.0;
+        if (t == 0) bn.cut_g = kBins;
+        __syncthreads();
+        if (nucleus) {
+            if (stot / Sc < (double)top_p * (1.0 + 2.0 * kDelta)) BINS_FAIL();   // the cut may not happen
+            double lo = pre;
+#pragma unroll
+            for (int c = 0; c < kPer; c++) {
+                const double hi = lo + mass[c];
+                if (mass[c] > 0.0 && hi * iSc * dh >= (double)top_p) { atomicMin(&bn.cut_g, kPer * t + c); break; }
+                lo = hi;
+            }
+            __syncthreads();
+            const int cb = bn.cut_g;
+            if (cb >= kBins) BINS_FAIL();
+            // the cut element lies in bin cb, or anywhere from the max (e = 1)
+            // on if the overflow segment may already reach top_p
+            const double ehc = (osum / Sc * dh >= (double)top_p) ? 1.0 : e_at((float)cb) * 1.001;
+            s2lo = (double)top_p;
+            s2hi = (double)top_p + ehc / Sc * (1.0 + 4.0 * kDelta) + 0x1p-24;
+        }
+        if (t == 0) {
+            bn.Slo = Slo;
+            bn.Shi = Shi;
+            bn.inv_s = (float)(1.0 / Sc);
+            bn.hw2 = 2.0f * kExpErr + (float)(((double)Shi - (double)Slo) / (double)Slo) + 0x1p-21f;
+            bn.s2lo = (float)s2lo;
+            bn.s2hi = (float)s2hi;
+        }
+        double lo = pre;
+#pragma unroll
+        for (int c = 0; c < kPer; c++) {
+            const int b = kPer * t + c;
+            const double hi = lo + mass[c];
+            const uint32_t mt = mtv[c];
+            if ((mt & 8u) && !(mt & 1u)) {
+                const double cn = (double)(bn.off[b + 1] - bn.off[b]);
+                bool col = ((mt >> 4) & 7u) != 0u;            // seq-1 ties need the order for S
+                const double ehi = e_at((float)b) * 1.001;
+                const double plo_ = lo * iSc, phi_ = hi * iSc, pe = ehi * iSc;
+                bool k2 = false;
+                int b2 = 0;
                 if (nucleus) {
                     k2 = plo_ * dl < (double)top_p;
-                    reach3 = k2;
                     if (k2) {
                         b2 = grid_exp((float)plo_);
+                        col |= !(plo_ > 0.0);
                         col |= grid_exp((float)(plo_ * dl)) != grid_exp((float)(phi_ * dh));
                         col |= phi_ * dh >= (double)top_p;
                         const int c2 = ilogb(pe);
@@ -948,247 +1123,85 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
                         col |= cn * (ldexp(pe, 23 - b2) + 1.0) >= 4.0e9;
                     }
                 }
-                if (reach3) {
-                    const double qlo = plo_ / s2c, qhi = phi_ / s2c;
-                    k3 = qlo * dl <= (double)r;
-                    if (k3) {
-                        b3 = grid_exp((float)qlo);
-                        col |= grid_exp((float)(qlo * dl)) != grid_exp((float)(qhi * dh));
-                        col |= qhi * dh > (double)r;
-                        const int c3 = ilogb(pe / s2c);
-                        if (c3 < b3) col |= cn * ldexp(1.0, c3 - b3) > kTieThr;
-                        col |= cn * (ldexp(pe / s2c, 23 - b3) + 1.0) >= 4.0e9;
-                    }
+                bn.meta[b] = (mt & 0xff00u) | (mt & 0x78u) | (col ? 0x81u : 0u) | (k2 ? 2u : 0u) |
+                             ((uint32_t)(b2 + 128) << 16) | (128u << 24);
+                if (col) {
+                    bn.cnt[b] = bn.off[b] | kNow;
+                    atomicAdd(&bn.ncollect, 1);
                 }
             }
-            if (cntv[c] == 0) col = false;
-            bn.meta[b] = (col ? 1u : 0u) | (k2 ? 2u : 0u) | (k3 ? 4u : 0u) | (cntv[c] ? 8u : 0u) |
-                         ((uint32_t)(b1 + 128) << 8) | ((uint32_t)(b2 + 128) << 16) |
-                         ((uint32_t)(b3 + 128) << 24);
-            bn.off[b] = o;
-            bn.cnt[b] = o;                  // cursor of collected bins
-            bn.esum[b] = 0ull;
-            bn.k23[b] = 0ull;
-            o += cntv[c];
+            bn.k2[b] = 0u;
+            bn.pre_e[b] = (float)lo;
+            lo = hi;
         }
+        if (t == kThreads - 1) bn.pre_e[kBins] = (float)lo;
     }
-    for (int j = t; j < nover; j += kThreads) gl[j] = bn.over[j];
+    if (t == 0) bn.ndefer = 0;
     __syncthreads();
-    GS_STAMP(11);
-
-    // ---- pass 2 -------------------------------------------------------------
-    auto visit2 = [&](int i, float x) {
-        const float y = t_one ? x : x / T;
-        int b;
-        uint32_t k1;
-        uint64_t k23;
-        const int cl = classify2(bn, y, &b, &k1, &k23);
-        if (cl == 1) {
-            const uint32_t slot = atomicAdd(&bn.cnt[b], 1u);
-            gl[slot] = list_entry(y, (uint32_t)i);
-        } else if (cl == 2) {
-            const int slot = atomicAdd(&bn.ndefer, 1);
-            if ((uint32_t)slot < dcap) defer[slot] = (uint32_t)i;
-        } else if (cl == 3) {
-            if (k1) atomicAdd((unsigned long long *)&bn.esum[b], (unsigned long long)k1);
-            if (k23) atomicAdd((unsigned long long *)&bn.k23[b], (unsigned long long)k23);
-        }
-    };
-    row_for_each(row, V, true, visit2);
-    __syncthreads();
-    GS_STAMP(12);
-    if (has_pen) {
-        // undo raw contributions of penalized ids, then add the penalized values
-        for (int s = t; s < kHashSlots; s += kThreads) {
-            const uint32_t id = sm.hkey[s];
-            if (id == kEmpty) continue;
-            const float yr = t_one ? row[id] : row[id] / T;
-            int b;
-            uint32_t k1;
-            uint64_t k23;
-            if (classify2(bn, yr, &b, &k1, &k23) == 3) {
-                if (k1) atomicAdd((unsigned long long *)&bn.esum[b], (unsigned long long)(0ull - (uint64_t)k1));
-                if (k23) atomicAdd((unsigned long long *)&bn.k23[b], (unsigned long long)(0ull - k23));
-            }
-        }
-        for (int b = t; b < kBins; b += kThreads) {
-            if (!(bn.meta[b] & 1u)) continue;
-            for (uint32_t j = bn.off[b]; j < bn.cnt[b]; j++)
-                if (hash_find(sm, ~(uint32_t)gl[j]) >= 0) gl[j] = 0ull;
-        }
-        const int nd = min((uint32_t)bn.ndefer, dcap);
-        for (int j = t; j < nd; j += kThreads)
-            if (hash_find(sm, defer[j] & kIdMask) >= 0) defer[j] = 0xffffffffu;
-        __threadfence_block();
-        __syncthreads();
-        for (int s = t; s < kHashSlots; s += kThreads) {
-            const uint32_t id = sm.hkey[s];
-            if (id == kEmpty) continue;
-            const float yp = t_one ? __uint_as_float(sm.hval[s]) : __uint_as_float(sm.hval[s]) / T;
-            int b;
-            uint32_t k1;
-            uint64_t k23;
-            const int cl = classify2(bn, yp, &b, &k1, &k23);
-            if (cl == 1) {
-                const uint32_t slot = atomicAdd(&bn.cnt[b], 1u);
-                gl[slot] = list_entry(yp, id);
-            } else if (cl == 2) {
-                const int slot = atomicAdd(&bn.ndefer, 1);
-                if ((uint32_t)slot < dcap) defer[slot] = id | 0x80000000u;
-            } else if (cl == 3) {
-                if (k1) atomicAdd((unsigned long long *)&bn.esum[b], (unsigned long long)k1);
-                if (k23) atomicAdd((unsigned long long *)&bn.k23[b], (unsigned long long)k23);
-            }
-        }
-        __syncthreads();
-    }
-#ifdef GS_TIMING
-    if (t == 0 && blockIdx.x == g_row) g_stamp[28] = (uint64_t)bn.ndefer;
-#endif
-    if ((uint32_t)bn.ndefer > dcap) BINS_FAIL();
-    if (!finish_segments(sm, gl, [&](int b) { return (bn.meta[b] & 1u) != 0u; })) BINS_FAIL();
-    if (wave_id() == 0 && !wave_sort_segment(gl, nover)) bn.fail = 1;
-    __threadfence_block();
-    __syncthreads();
-    if (bn.fail) BINS_FAIL();
-    GS_STAMP(13);
-
-    // ---- resolve deferred elements -------------------------------------------
-    const int nd = bn.ndefer;
-    auto def_y = [&](uint32_t en) {
-        const uint32_t id = en & kIdMask;
-        float x = row[id];
-        if (en & 0x80000000u) {
-            const int s = hash_find(sm, id);
-            if (s >= 0) x = __uint_as_float(sm.hval[s]);
-        }
-        return t_one ? x : x / T;
-    };
-    auto mark = [&](int b) {
-        const uint32_t old = atomicOr(&bn.meta[b], 1u);
-        if (!(old & 1u)) { bn.cnt[b] = bn.off[b] | kNow; atomicAdd(&bn.ncollect, 1); }
-    };
-    // seq 1: exact increments; a tie adds its lower choice and is counted
-    for (int j = t; j < nd; j += kThreads) {
-        const uint32_t en = defer[j];
-        if (en == 0xffffffffu) continue;
-        const float y = def_y(en);
-        const int b = bin_of(y - m0);
-        uint32_t k;
-        const int rc = inc_exact(glibc_expf(y - m), meta_b(bn.meta[b], 1), &k);
-        if (rc < 0) { bn.fail = 1; continue; }
-        if (k) atomicAdd((unsigned long long *)&bn.esum[b], (unsigned long long)k);
-        if (rc == 0) {
-            const uint32_t old = atomicAdd(&bn.meta[b], 16u);
-            if (((old >> 4) & 15u) == 15u) bn.fail = 1;
-        }
-    }
-    __syncthreads();
-    if (bn.fail) BINS_FAIL();
     GS_STAMP(16);
-    if (!build_groups(sm)) BINS_FAIL();
-    gather_runs(sm, 1);
-    int N = build_walk(sm, gl, W, WT, m);
-    if (N < 0) BINS_FAIL();
+
+    // ---- pass 3 (cache): accumulation-2 increments, new bins listed ----------
+    K.inv_s = bn.inv_s;
+    K.hw2 = bn.hw2;
+    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.k2,
+              [&bn, K](float y) { return classify3(bn, K, y); });
     GS_STAMP(17);
-    float Slo, Shi;
-    if (walk(sm, W, N, run_fn(bn, 1, false), [](float) { return false; }, &Slo) != N) BINS_FAIL();
-    GS_STAMP(18);
-    if (walk(sm, W, N, run_fn(bn, 1, true), [](float) { return false; }, &Shi) != N) BINS_FAIL();
-    GS_STAMP(19);
-#ifdef GS_TIMING
-    if (t == 0 && blockIdx.x == g_row) { g_stamp[30] = __float_as_uint(Slo); g_stamp[31] = ((uint64_t)__float_as_uint(Shi) << 32) | __float_as_uint(bn.Spred); }
-#endif
-    if (!(Slo >= bn.Spred * (1.0f - kDeltaS) && Shi <= bn.Spred * (1.0f + kDeltaS))) BINS_FAIL();
-    GS_STAMP(14);
-    // bins with a seq-1 tie need the exact order
-    for (int b = t; b < kBins; b += kThreads)
-        if (!(bn.meta[b] & 1u) && ((bn.meta[b] >> 4) & 15u)) mark(b);
-    __syncthreads();
-    // seq 2 and seq 3 over the reachable values of S and s2: a possible tie
-    // needs the exact order (collect the bin); a unique increment is added
-    // now; otherwise the increment waits for the exact S or s2 (kDone bits).
+    GS_DIAG(29, bn.ndefer | ((uint64_t)bn.ncollect << 32));
+    if ((uint32_t)bn.ndefer > dcap) BINS_FAIL();
+    if (!finish_now(sm, gl, tmp)) BINS_FAIL();
+
+    // ---- deferred accumulation-2 elements over the reachable S ---------------
+    // A possible tie needs the exact order (the bin is collected in pass 4); a
+    // unique increment is added now; otherwise it waits for the exact S.
+    auto mark = [&](int b) {
+        const uint32_t old = atomicOr(&bn.meta[b], kMetaCol | kMetaNow);
+        if (!(old & 1u)) { bn.cnt[b] = bn.off[b] | kNow; atomicAdd(&bn.ncollect, 0x10000); }
+    };
+    const int nd = bn.ndefer;
     for (int j = t; j < nd; j += kThreads) {
-        const uint32_t en = defer[j];
+        const uint32_t en = ldg(defer + j);
         if (en == 0xffffffffu) continue;
         const float y = def_y(en);
         const int b = bin_of(y - m0);
         const uint32_t mt = bn.meta[b];
         if (mt & 1u) continue;
-        const float e = glibc_expf(y - m);
-        uint32_t k, st = 0;
-        if (mt & 2u) {
-            const int rc = inc_combos(e, Slo, Shi, false, 1.0f, 1.0f, meta_b(mt, 2), &k);
-            if (rc == 2) { mark(b); continue; }
-            if (rc == 0) { st |= kDone2; if (k) atomicAdd((unsigned long long *)&bn.k23[b], (unsigned long long)k); }
-        } else st |= kDone2;
-        if (mt & 4u) {
-            const int rc = inc_combos(e, Slo, Shi, nucleus, bn.s2lo, bn.s2hi, meta_b(mt, 3), &k);
-            if (rc == 2) { mark(b); continue; }
-            if (rc == 0) { st |= kDone3; if (k) atomicAdd((unsigned long long *)&bn.k23[b], (unsigned long long)k << 32); }
-        } else st |= kDone3;
-        defer[j] = en | st;
+        uint32_t k;
+        const int rc = inc_s_range(glibc_expf(y - m), Slo, Shi, meta_b(mt, 2), &k);
+        if (rc == 2) { mark(b); continue; }
+        if (rc == 0) {
+            if (k) atomicAdd(&bn.k2[b], k);
+            defer[j] = en | kDone2;
+        }
     }
     __syncthreads();
-#ifdef GS_TIMING
-    if (t == 0 && blockIdx.x == g_row) g_stamp[29] = (uint64_t)bn.ncollect;
-#endif
+    GS_STAMP(18);
 
-    // ---- pass 3: collect the marked bins ------------------------------------
-    if (bn.ncollect > 0) {
-        auto visit3 = [&](int i, float x) {
-            const float y = t_one ? x : x / T;
-            const float dp = y - m0;
-            if (!(dp <= kDUp) || dp < -kDLo) return;
-            const int b = bin_of(dp);
-            if (bn.cnt[b] & kNow) {
-                const uint32_t slot = atomicAdd(&bn.cnt[b], 1u) & ~kNow;
-                gl[slot] = list_entry(y, (uint32_t)i);
-            }
-        };
-        row_for_each(row, V, true, visit3);
-        __syncthreads();
-        GS_STAMP(20);
-        if (has_pen) {
-            for (int b = t; b < kBins; b += kThreads) {
-                if (!(bn.cnt[b] & kNow)) continue;
-                for (uint32_t j = bn.off[b]; j < (bn.cnt[b] & ~kNow); j++)
-                    if (hash_find(sm, ~(uint32_t)gl[j]) >= 0) gl[j] = 0ull;
-            }
-            __threadfence_block();
-            __syncthreads();
-            for (int s = t; s < kHashSlots; s += kThreads) {
-                const uint32_t id = sm.hkey[s];
-                if (id == kEmpty) continue;
-                const float yp = t_one ? __uint_as_float(sm.hval[s]) : __uint_as_float(sm.hval[s]) / T;
-                const float dq = yp - m0;
-                if (!(dq <= kDUp) || dq < -kDLo) continue;
-                const int b = bin_of(dq);
-                if (bn.cnt[b] & kNow) {
-                    const uint32_t slot = atomicAdd(&bn.cnt[b], 1u) & ~kNow;
-                    gl[slot] = list_entry(yp, id);
-                }
-            }
-            __syncthreads();
-        }
-        if (!finish_segments(sm, gl, [&](int b) { return (bn.cnt[b] & kNow) != 0u; })) BINS_FAIL();
-        if (!build_groups(sm)) BINS_FAIL();
-        N = build_walk(sm, gl, W, WT, m);
-        if (N < 0) BINS_FAIL();
-        GS_STAMP(21);
+    // ---- pass 4 (cache, rare): collect the bins of possible ties -------------
+    if (bn.ncollect >> 16) {
+        collect_now(sm, row, V, t_one, T, has_pen, gl);
+        if (!finish_now(sm, gl, tmp)) BINS_FAIL();
     }
+    // runs carry the accumulation-2 grids now: always regroup; the walk array
+    // changes only if bins were collected
+    if (!build_groups(sm)) BINS_FAIL();
+    if (bn.ncollect) {
+        N = build_walk(sm, gl, W, WT, m, m0, false);
+        if (N < 0) BINS_FAIL();
+    }
+    GS_STAMP(19);
+    GS_DIAG(27, N | ((uint64_t)bn.ncollect << 32));
 
-    // ---- exact walks --------------------------------------------------------
+    // ---- exact walks ----------------------------------------------------------
     float S = Slo;
-    if (bn.ncollect > 0) {
+    if (!s_exact) {
         gather_runs(sm, 1);
         if (walk(sm, W, N, run_fn(bn, 1, false), [](float) { return false; }, &S) != N) BINS_FAIL();
         if (!(S >= Slo && S <= Shi)) BINS_FAIL();
-    } else if (Slo != Shi) BINS_FAIL();
-    GS_STAMP(22);
-    // late seq-2 increments, now that S is exact
+    }
+    GS_STAMP(20);
+    // late seq-2 increments, now that S is exact (no reachable value was a tie)
     for (int j = t; j < nd; j += kThreads) {
-        const uint32_t en = defer[j];
+        const uint32_t en = ldg(defer + j);
         if (en == 0xffffffffu || (en & kDone2)) continue;
         const float y = def_y(en);
         const int b = bin_of(y - m0);
@@ -1196,48 +1209,116 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
         if (mt & 1u) continue;
         uint32_t k;
         if (inc_exact(glibc_expf(y - m) / S, meta_b(mt, 2), &k) != 1) { bn.fail = 1; continue; }
-        if (k) atomicAdd((unsigned long long *)&bn.k23[b], (unsigned long long)k);
+        if (k) atomicAdd(&bn.k2[b], k);
     }
-    __syncthreads();
-    if (bn.fail) BINS_FAIL();
     // summands of seq 2: p = e / S (src/sampler.rs:56)
     for (int j = t; j < N; j += kThreads) { const float v = W[j]; if (!is_marker(v)) W[j] = v / S; }
     __threadfence_block();
     __syncthreads();
-    int n3 = N, js = -1;
+    if (bn.fail) BINS_FAIL();
+    int js = -1;
     float s2 = 1.0f;
+    uint32_t cut_tok = 0;
     if (nucleus) {
         gather_runs(sm, 2);
         js = walk(sm, W, N, run_fn(bn, 2, false), [top_p](float c) { return c >= top_p; }, &s2);
         if (js < 0 || js >= N || !(s2 >= bn.s2lo && s2 <= bn.s2hi)) BINS_FAIL();
-        // summands of seq 3: q = p / s2 (src/sampler.rs:68)
-        for (int j = t; j <= js; j += kThreads) { const float v = W[j]; if (!is_marker(v)) W[j] = v / s2; }
-        __threadfence_block();
-        __syncthreads();
-        n3 = js + 1;
+        cut_tok = WT[js];
     }
-    // late seq-3 increments, now that S and s2 are exact
-    for (int j = t; j < nd; j += kThreads) {
-        const uint32_t en = defer[j];
-        if (en == 0xffffffffu || (en & kDone3)) continue;
-        const float y = def_y(en);
-        const int b = bin_of(y - m0);
-        const uint32_t mt = bn.meta[b];
-        if ((mt & 1u) || !(mt & 4u)) continue;
-        const float p = glibc_expf(y - m) / S;
-        uint32_t k;
-        if (inc_exact(nucleus ? p / s2 : p, meta_b(mt, 3), &k) != 1) { bn.fail = 1; continue; }
-        if (k) atomicAdd((unsigned long long *)&bn.k23[b], (unsigned long long)k << 32);
+    GS_STAMP(21);
+
+    // ---- plan C: accumulation 3, with S and s2 exact -------------------------
+    // q = p / s2 (src/sampler.rs:68); the seq-3 running sum before bin b is
+    // the bin's mass prefix / (S s2) to the rounding of the increments.  Bulk
+    // bins before the draw get seq-3 increments in pass 4 (in esum, free now);
+    // bins where it may change binade or pass r are collected.
+    {
+        const double inv_ss = 1.0 / ((double)S * (double)s2);
+#pragma unroll
+        for (int c = 0; c < kPer; c++) {
+            const int b = kPer * t + c;
+            const uint32_t mt = bn.meta[b];
+            bn.esum[b] = 0u;
+            if (!(mt & 8u) || (mt & 1u) || (nucleus && !(mt & 2u))) continue;
+            const double qlo = (double)bn.pre_e[b] * inv_ss, qhi = (double)bn.pre_e[b + 1] * inv_ss;
+            if (!(qlo * dl <= (double)r)) continue;
+            const double cn = (double)(bn.off[b + 1] - bn.off[b]);
+            const double qe = e_at((float)b) * 1.001 * inv_ss;
+            const int b3 = grid_exp((float)qlo);
+            bool col = !(qlo > 0.0);
+            col |= grid_exp((float)(qlo * dl)) != grid_exp((float)(qhi * dh));
+            col |= qhi * dh > (double)r;
+            const int c3 = ilogb(qe);
+            if (c3 < b3) col |= cn * ldexp(1.0, c3 - b3) > kTieThr;
+            col |= cn * (ldexp(qe, 23 - b3) + 1.0) >= 4.0e9;
+            bn.meta[b] = (mt & 0x00ffffffu) | 4u | (col ? kMetaCol | kMetaNow : 0u) | ((uint32_t)(b3 + 128) << 24);
+            if (col) bn.cnt[b] = bn.off[b] | kNow;
+        }
+        if (t == 0) {
+            bn.ndefer = 0;
+            bn.ncollect = 0;
+            bn.inv_s = 1.0f / S;
+            bn.inv_s2 = 1.0f / s2;
+        }
+        __syncthreads();
+    }
+
+    // ---- pass 4 (cache): accumulation-3 increments, new bins listed ----------
+    K.inv_s = bn.inv_s;
+    K.inv_s2 = bn.inv_s2;
+    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.esum,
+              [&bn, K](float y) { return classify4(bn, K, y); });
+    GS_STAMP(22);
+    if ((uint32_t)bn.ndefer > dcap) BINS_FAIL();
+    if (!finish_now(sm, gl, tmp)) BINS_FAIL();
+    // deferred seq-3 elements: exact increments; a tie needs the bin's order
+    {
+        const int nd4 = bn.ndefer;
+        for (int j = t; j < nd4; j += kThreads) {
+            const uint32_t en = ldg(defer + j);
+            if (en == 0xffffffffu) continue;
+            const float y = def_y(en);
+            const int b = bin_of(y - m0);
+            const uint32_t mt = bn.meta[b];
+            if (mt & 1u) continue;
+            const float p = glibc_expf(y - m) / S;
+            uint32_t k;
+            const int rc = inc_exact(nucleus ? p / s2 : p, meta_b(mt, 3), &k);
+            if (rc < 0) { bn.fail = 1; continue; }
+            if (rc == 0) { mark(b); continue; }
+            if (k) atomicAdd(&bn.esum[b], k);
+        }
     }
     __syncthreads();
     if (bn.fail) BINS_FAIL();
+    if (bn.ncollect) {
+        collect_now(sm, row, V, t_one, T, has_pen, gl);
+        if (!finish_now(sm, gl, tmp)) BINS_FAIL();
+    }
+    if (!build_groups(sm)) BINS_FAIL();
+    N = build_walk(sm, gl, W, WT, m, m0, false);
+    if (N < 0) BINS_FAIL();
+    // summands of seq 3 (src/sampler.rs:56, :68); the walk ends at the cut
+    if (t == 0) bn.cut_g = N;
+    __syncthreads();
+    for (int j = t; j < N; j += kThreads) {
+        const float v = W[j];
+        if (is_marker(v)) continue;
+        const float p = v / S;
+        W[j] = nucleus ? p / s2 : p;
+        if (nucleus && WT[j] == cut_tok) atomicMin(&bn.cut_g, j);
+    }
+    __threadfence_block();
+    __syncthreads();
+    const int n3 = nucleus ? bn.cut_g + 1 : N;
+    if (n3 > N) BINS_FAIL();
     GS_STAMP(23);
     gather_runs(sm, 3);
     float c3;
     const int jd = walk(sm, W, n3, run_fn(bn, 3, false), [r](float c) { return r < c; }, &c3);
     if (jd < 0) BINS_FAIL();
     if (jd < n3) *tok = (int)WT[jd];
-    else if (nucleus) *tok = (int)WT[js];
+    else if (nucleus) *tok = (int)WT[n3 - 1];
     else BINS_FAIL();   // the last element of the whole order: sort path
     return true;
 }

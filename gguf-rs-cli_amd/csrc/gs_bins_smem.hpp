@@ -11,9 +11,11 @@ constexpr int kMaxGroups = 256;    // runs of consecutive collected bins
 struct BinsSmem {
     uint32_t cnt[kBins];           // pass 1: count; then collected bin -> cursor, bulk bin -> run index
     uint32_t off[kBins + 1];       // list segment of bin b: [off[b], off[b+1])
-    uint64_t esum[kBins];          // bulk bin: sum of seq-1 increments
-    uint64_t k23[kBins];           // bulk bin: seq-2 increments (low 32) | seq-3 increments (high 32)
+    uint32_t esum[kBins];          // bulk bin: sum of seq-1 increments
+    uint32_t k2[kBins];            // bulk bin: sum of seq-2 increments (collected bin: f32 mass, transiently)
     uint32_t meta[kBins];          // flags, tie count and grid exponents
+    float pre_e[kBins + 1];        // summand mass before bin b (plan B), for plan C
+    uint32_t sbase[kBins];         // segment sort: first work item of bin b
     uint64_t over[kOverCap];       // (key << 32) | ~idx of d' > kDUp
     uint32_t gbeg[kMaxGroups];     // group g: list range [gbeg, gend)
     uint32_t gend[kMaxGroups];
@@ -21,10 +23,10 @@ struct BinsSmem {
     uint32_t runt[kMaxGroups + 1]; // seq-1 rounding ties inside run g
     int runb[kMaxGroups + 1];      // packed grid exponents and flags of run g
     uint32_t wbase[kMaxGroups + 1];// walk array: position of run g's marker
-    float m0, m, S, s2, Spred, s2lo, s2hi, Slo, Shi;
-    float hw2, hw3, inv_spred, inv_s2c;
-    int ngroups, ndefer, nover, fail, ncollect;
-    int cut_g, cut_j, tok;
+    float m0, m, s2lo, s2hi, Slo, Shi;
+    float hw2, inv_s, inv_s2;
+    int ngroups, ndefer, nover, fail, ncollect, nties;
+    int cut_g;
 };
 
 } // namespace gs

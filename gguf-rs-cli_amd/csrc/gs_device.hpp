@@ -108,4 +108,25 @@ __host__ __device__ __forceinline__ float synth_logit(uint64_t seed, uint64_t co
     return z * sigma;
 }
 
+// Global-memory accessors.  The address space is stated so that the backend
+// emits global_* instructions: a flat access also counts against the LDS
+// wait counter, so in loops that mix row loads with LDS atomics every LDS
+// wait would also wait for the outstanding row loads.
+template <class T>
+__device__ __forceinline__ T ldg(const T *p)
+{
+    return *(const __attribute__((address_space(1))) T *)p;
+}
+typedef float gs_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ldg(const float4 *p)
+{
+    const gs_f4 v = *(const __attribute__((address_space(1))) gs_f4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <class T>
+__device__ __forceinline__ void stg(T *p, T v)
+{
+    *(__attribute__((address_space(1))) T *)p = v;
+}
+
 } // namespace gs

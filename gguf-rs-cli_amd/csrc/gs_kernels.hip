@@ -24,8 +24,12 @@ __device__ uint64_t g_stamp[32];
 __device__ int g_fails[1024];
 __device__ unsigned g_row;
 #define GS_STAMP(i) do { if (blockIdx.x == g_row && threadIdx.x == 0) g_stamp[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#define GS_DIAG(i, v) do { if (blockIdx.x == g_row && threadIdx.x == 0) g_stamp[i] = (uint64_t)(v); } while (0)
+#define GS_SUB(i) do { if (blockIdx.x == g_row && threadIdx.x == 0 && g_fails[899] < 1) g_fails[900 + (i)] = (int)__builtin_amdgcn_s_memrealtime(); } while (0)
 #else
 #define GS_STAMP(i) do { } while (0)
+#define GS_DIAG(i, v) do { } while (0)
+#define GS_SUB(i) do { } while (0)
 #endif
 
 constexpr int kHashSlots = 2 * kMaxWindow;     // open addressing, load <= 1/2
@@ -152,10 +156,8 @@ __device__ __forceinline__ void row_for_each(const float *row, int V, bool align
         for (int base = 0; base < n4; base += kThreads * kUnroll) {
             float4 v[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; u++) {
-                int q = base + u * kThreads + t;
-                if (q < n4) v[u] = r4[q];
-            }
+            for (int u = 0; u < kUnroll; u++)
+                v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));   // unconditional: no wait between loads
 #pragma unroll
             for (int u = 0; u < kUnroll; u++) {
                 int q = base + u * kThreads + t;
@@ -167,21 +169,52 @@ __device__ __forceinline__ void row_for_each(const float *row, int V, bool align
                 }
             }
         }
-        for (int i = (n4 << 2) + t; i < V; i += kThreads) f(i, row[i]);
+        for (int i = (n4 << 2) + t; i < V; i += kThreads) f(i, ldg(row + i));
     } else {
         for (int base = 0; base < V; base += kThreads * kUnroll) {
             float v[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; u++) {
-                int i = base + u * kThreads + t;
-                if (i < V) v[u] = row[i];
-            }
+            for (int u = 0; u < kUnroll; u++) v[u] = ldg(row + min(base + u * kThreads + t, V - 1));
 #pragma unroll
             for (int u = 0; u < kUnroll; u++) {
                 int i = base + u * kThreads + t;
                 if (i < V) f(i, v[u]);
             }
         }
+    }
+}
+
+// Two-phase visit of a 16-byte aligned row: for each float4, cls(y) is
+// evaluated for the four values first (pure, so their LDS reads issue
+// together), then act(i, y, c) performs the side effects in index order.
+// xf maps the raw logit to the value that is classified.
+template <class X, class C, class A>
+__device__ __forceinline__ void row_for_each_cls(const float *row, int V, X xf, C cls, A act)
+{
+    const int t = threadIdx.x;
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+    const int n4 = V >> 2;
+    for (int base = 0; base < n4; base += kThreads * kUnroll) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++)
+            v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));   // unconditional: no wait between loads
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int q = base + u * kThreads + t;
+            if (q < n4) {
+                const float y0 = xf(v[u].x), y1 = xf(v[u].y), y2 = xf(v[u].z), y3 = xf(v[u].w);
+                const auto c0 = cls(y0), c1 = cls(y1), c2 = cls(y2), c3 = cls(y3);
+                act(4 * q + 0, y0, c0);
+                act(4 * q + 1, y1, c1);
+                act(4 * q + 2, y2, c2);
+                act(4 * q + 3, y3, c3);
+            }
+        }
+    }
+    for (int i = (n4 << 2) + t; i < V; i += kThreads) {
+        const float y = xf(ldg(row + i));
+        act(i, y, cls(y));
     }
 }
 
