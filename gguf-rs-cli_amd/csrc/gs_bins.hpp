@@ -39,9 +39,14 @@
 constexpr float kDUp = 3.0f;
 constexpr float kDLo = 18.5f;
 constexpr float kInvW = (float)kBins / (kDUp + kDLo);
+// Bins b < kMassBins (d' > 3 - kMassBins/kInvW, about -3) get exact masses
+// in pass 1: their elements are few and large, so count times the bin's
+// central value is too coarse for the running-sum plan there.
+constexpr int kMassBins = 1143;
+constexpr float kMassScale = 4294967296.0f;       // fixed point 2^32
 constexpr float kDelta = 1.0f / 4096.0f;          // relative margin of the plan
-constexpr float kExpErr = 1.0f / 2097152.0f;      // bound on |fast_exp / expf - 1| (2^-21)
-constexpr float kTieThr = 1.0f / 256.0f;          // expected ties that force collection
+constexpr float kExpErr = 1.0f / 4194304.0f;      // bound on |fast_exp / expf - 1| (2^-22)
+constexpr float kTieThr = 1.0f / 8.0f;            // expected ties that force collection
 constexpr int kNoRun = 0x7fffffff;
 constexpr int kMaxSeg = 512;                      // largest collected bin (wave sort)
 constexpr uint32_t kNow = 0x80000000u;            // cnt[] flag: collect in the next pass
@@ -67,7 +72,7 @@ __device__ __forceinline__ int bin_clamp(float dp)
 // exp(d) via v_exp_f32 with the rounding error of d*log2(e) compensated:
 // t = RN(d*L), err = d*L - t (exact by fma) + d*(log2(e) - L), then
 // exp2(t) * (1 + err*ln2).  Measured on gfx950 against glibc expf over every
-// f32 d in [-30, 0]: max relative error 1.19e-7 (2^-23); kExpErr allows 4x.
+// f32 d in [-30, 0]: max relative error 1.19e-7 (2^-23); kExpErr allows 2x.
 // (Summands with d < -30 are below 1e-13: their increments are 0, far from
 // any rounding boundary.)
 __device__ __forceinline__ float fast_exp(float d)
@@ -597,7 +602,7 @@ __device__ __forceinline__ Cls classify4(const BinsSmem &bn, const PassK &K, flo
     c.b = bin_clamp(dp);
     const uint32_t mt = bn.meta[c.b];
     const float q = fast_exp(y - K.m) * K.inv_s * K.inv_s2;
-    const bool ok = inc_of(ldexpf(q, 23 - meta_b(mt, 3)), 2.0f * kExpErr + 0x1p-21f, &c.k);
+    const bool ok = inc_of(ldexpf(q, 23 - meta_b(mt, 3)), 2.0f * kExpErr + 0x1p-22f, &c.k);
     c.cl = !inr ? 0 : ((mt & kMetaNow) ? 1 : (((mt & kMetaCol) || !(mt & 4u)) ? 0 : (ok ? 3 : 2)));
     return c;
 }
@@ -692,86 +697,139 @@ __device__ bool collect_now(RowSmem &sm, const float *row, int V, bool t_one, fl
 }
 
 // Sort the segments of the kNow bins descending (entries are distinct; removed
-// entries are 0 and go last), zero their unused tails and clear the flag.
-// Work items are 64-entry chunks of the segments, spread over all waves: each
-// lane ranks one entry against its whole segment and writes it to tmp (room
-// for kWalkCap entries); a second phase copies back.  False if a segment
-// exceeds kMaxSeg or tmp is too small.
+// entries are 0), zero their unused tails and clear the flag.  Bins are
+// monotone in the key, so a run of consecutive kNow bins (empty bins between
+// them included) sorts as one range, and the position of a nonzero entry in
+// its run is the number of nonzero entries of the run's earlier bins plus its
+// rank inside its own bin; zeros take the slots after the last nonzero
+// entry.  Work items are 64-entry chunks of the runs, spread over all waves;
+// entries go to tmp (room for kWalkCap entries), then back.  False if a run
+// exceeds kMaxRun entries or tmp is too small.  Uses gbeg/gend/wbase/runt/run
+// as run tables (build_groups and build_walk rebuild them).
+constexpr uint32_t kMaxRun = 16384;
 __device__ bool finish_now(RowSmem &sm, uint64_t *gl, uint64_t *tmp)
 {
     BinsSmem &bn = sm.x.bn;
     const int t = threadIdx.x, lane = lane_id();
+    const float m0 = bn.m0;
     constexpr int kPer = kBins / kThreads;
-    uint32_t nit[kPer], loc = 0;
+    // kind: 0 empty (transparent), 1 other nonempty, 2 kNow
+    int kind[kPer], lastk = 0;
 #pragma unroll
     for (int c = 0; c < kPer; c++) {
         const int b = kPer * t + c;
         const uint32_t cb = bn.cnt[b];
-        uint32_t n = 0;
-        if (cb & kNow) {
-            const uint32_t cur = cb & ~kNow;
-            n = cur - bn.off[b];
-            for (uint32_t j = cur; j < bn.off[b + 1]; j++) stg(gl + j, (uint64_t)0);
-        }
-        if (n > (uint32_t)kMaxSeg) bn.fail = 1;
-        nit[c] = (n + 63u) >> 6;
-        loc += nit[c];
+        const bool ne = bn.off[b + 1] > bn.off[b];
+        kind[c] = !ne ? 0 : ((cb & kNow) ? 2 : 1);
+        if (cb & kNow)
+            for (uint32_t j = cb & ~kNow; j < bn.off[b + 1]; j++) stg(gl + j, (uint64_t)0);
+        if (kind[c]) lastk = kind[c];
+        bn.nzc[b] = 0u;
     }
-    uint32_t tot;
-    uint32_t ex = block_excl_u32(loc, &tot, sm);
+    int prevk = block_excl_last(lastk, 1, sm);
+    uint32_t nst = 0;
+    int starts[kPer];
 #pragma unroll
     for (int c = 0; c < kPer; c++) {
-        bn.sbase[kPer * t + c] = ex;
-        ex += nit[c];
+        starts[c] = (kind[c] == 2 && prevk != 2) ? 1 : 0;
+        if (kind[c]) prevk = kind[c];
+        nst += starts[c];
+    }
+    uint32_t nruns;
+    uint32_t r = block_excl_u32(nst, &nruns, sm);
+    if (nruns > (uint32_t)kMaxGroups) return false;
+    for (int g = t; g < kMaxGroups; g += kThreads) { bn.gbeg[g] = 0xffffffffu; bn.gend[g] = 0u; bn.run[g] = 0ull; }
+    __syncthreads();
+    r -= 1;                                   // run index of the current kNow bin
+#pragma unroll
+    for (int c = 0; c < kPer; c++) {
+        const int b = kPer * t + c;
+        r += starts[c];
+        if (kind[c] == 2) {
+            atomicMin(&bn.gbeg[r], bn.off[b]);
+            atomicMax(&bn.gend[r], bn.off[b + 1]);
+        }
     }
     __threadfence_block();
     __syncthreads();
+    // items per run and their prefix (wbase[r] = first item of run r)
+    const uint32_t nit = (t < (int)nruns) ? (bn.gend[t] - bn.gbeg[t] + 63u) >> 6 : 0u;
+    if (t < (int)nruns && bn.gend[t] - bn.gbeg[t] > kMaxRun) bn.fail = 1;
+    uint32_t tot;
+    const uint32_t ib = block_excl_u32(nit, &tot, sm);
+    if (t < (int)nruns) bn.wbase[t] = ib;
+    __syncthreads();
     if (bn.fail || tot * 64u > kWalkCap) return false;
-    auto item_bin = [&](uint32_t it) {
-        int lo = 0, hi = kBins - 1;                 // largest b with sbase[b] <= it
+    auto item_run = [&](uint32_t it) {
+        int lo = 0, hi = (int)nruns - 1;            // largest r with wbase[r] <= it
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (bn.sbase[mid] <= it) lo = mid;
+            if (bn.wbase[mid] <= it) lo = mid;
             else hi = mid - 1;
         }
         return lo;
     };
+    auto bin_of_entry = [&](uint64_t en) { return bin_clamp(key2f((uint32_t)(en >> 32)) - m0); };
+    // nonzero entries per bin
     for (uint32_t it = wave_id(); it < tot; it += kWaves) {
-        const int b = __builtin_amdgcn_readfirstlane(item_bin(it));
-        const uint32_t o = __builtin_amdgcn_readfirstlane(bn.off[b]);
-        const uint32_t n = __builtin_amdgcn_readfirstlane((bn.cnt[b] & ~kNow) - o);
-        const uint32_t j = 64u * (it - bn.sbase[b]) + lane;
-        // the segment in registers (lane l holds entries l, l + 64, ...), then
-        // v_readlane broadcasts
-        uint64_t seg[kMaxSeg / 64];
+        const int rr = item_run(it);
+        const uint32_t o = bn.gbeg[rr], n = bn.gend[rr] - o;
+        const uint32_t j = 64u * (it - bn.wbase[rr]) + lane;
+        const uint64_t en = j < n ? ldg(gl + o + j) : 0ull;
+        if (en) atomicAdd(&bn.nzc[bin_of_entry(en)], 1u);
+    }
+    __syncthreads();
+    // exclusive prefix of the nonzero counts in bin order
+    {
+        uint32_t v[kPer], loc = 0;
 #pragma unroll
-        for (int k = 0; k < kMaxSeg / 64; k++) {
-            const uint32_t idx = 64u * k + lane;
-            seg[k] = idx < n ? ldg(gl + o + idx) : 0ull;
-        }
-        const uint64_t mine = j < n ? ldg(gl + o + j) : 0ull;
-        uint32_t rank = 0;
+        for (int c = 0; c < kPer; c++) { v[c] = bn.nzc[kPer * t + c]; loc += v[c]; }
+        uint32_t all;
+        uint32_t ex = block_excl_u32(loc, &all, sm);
 #pragma unroll
-        for (int k = 0; k < kMaxSeg / 64; k++) {
-            if (64u * k >= n) break;
-            const uint32_t lim = min(64u, n - 64u * k);
-            const uint32_t lo32 = (uint32_t)seg[k], hi32 = (uint32_t)(seg[k] >> 32);
-            for (uint32_t l = 0; l < lim; l++) {
-                const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi32, l) << 32) |
-                                       (uint32_t)__builtin_amdgcn_readlane((int)lo32, l);
-                const uint32_t i = 64u * k + l;
-                rank += (other > mine) | ((other == mine) & (i < j));
+        for (int c = 0; c < kPer; c++) { bn.nzc[kPer * t + c] = ex; ex += v[c]; }
+    }
+    __syncthreads();
+    // run r: nonzero prefix at its first bin (runt[r])
+    if (t < (int)nruns) {
+        const uint64_t en0 = ldg(gl + bn.gbeg[t]);       // the first entry of a run is its largest
+        bn.runt[t] = en0 ? bn.nzc[bin_of_entry(en0)] : 0u;
+    }
+    __syncthreads();
+    for (uint32_t it = wave_id(); it < tot; it += kWaves) {
+        const int rr = item_run(it);
+        const uint32_t o = bn.gbeg[rr], n = bn.gend[rr] - o, base = bn.wbase[rr];
+        const uint32_t j = 64u * (it - base) + lane;
+        if (j >= n) continue;
+        const uint64_t mine = ldg(gl + o + j);
+        uint32_t pos;
+        if (mine) {
+            const int b = bin_of_entry(mine);
+            const uint32_t bo = bn.off[b], bc = bn.cnt[b] & ~kNow;
+            uint32_t rank = 0;
+            uint32_t i = bo;
+            for (; i + 4 <= bc; i += 4) {
+                const uint64_t a0 = ldg(gl + i), a1 = ldg(gl + i + 1), a2 = ldg(gl + i + 2), a3 = ldg(gl + i + 3);
+                rank += (a0 > mine) + (a1 > mine) + (a2 > mine) + (a3 > mine);
             }
+            for (; i < bc; i++) rank += ldg(gl + i) > mine;
+            pos = bn.nzc[b] - bn.runt[rr] + rank;
+        } else {
+            // zeros after the run's nonzero entries; the run's nonzero total is
+            // its size minus its zeros, which the zero counter reaches last
+            pos = 0xffffffffu;
+            const uint32_t zi = (uint32_t)atomicAdd((unsigned long long *)&bn.run[rr], 1ull);
+            pos = n - 1u - zi;
         }
-        if (j < n) stg(tmp + 64u * bn.sbase[b] + rank, mine);
+        stg(tmp + 64u * base + pos, mine);
     }
     __threadfence_block();
     __syncthreads();
     for (uint32_t it = wave_id(); it < tot; it += kWaves) {
-        const int b = item_bin(it);
-        const uint32_t o = bn.off[b], n = (bn.cnt[b] & ~kNow) - o;
-        const uint32_t j = 64u * (it - bn.sbase[b]) + lane;
-        if (j < n) stg(gl + o + j, ldg(tmp + 64u * bn.sbase[b] + j));
+        const int rr = item_run(it);
+        const uint32_t o = bn.gbeg[rr], n = bn.gend[rr] - o, base = bn.wbase[rr];
+        const uint32_t j = 64u * (it - base) + lane;
+        if (j < n) stg(gl + o + j, ldg(tmp + 64u * base + j));
     }
     __threadfence_block();
     __syncthreads();
@@ -805,7 +863,8 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     const int n4 = V >> 2;
     if (n4 == 0) BINS_FAIL();
 
-    for (int b = t; b < kBins; b += kThreads) bn.cnt[b] = 0;
+    uint64_t *mass64 = reinterpret_cast<uint64_t *>(bn.esum);   // aliases esum + k2 until plan A
+    for (int b = t; b < kBins; b += kThreads) { bn.cnt[b] = 0; mass64[b] = 0ull; }
     if (t == 0) { bn.nover = 0; bn.ndefer = 0; bn.fail = 0; bn.ncollect = 0; bn.nties = 0; }
 
     // ---- pass 1 (HBM): counts, max, NaN -------------------------------------
@@ -820,7 +879,9 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
             const int slot = atomicAdd(&bn.nover, 1);
             if (slot < kOverCap) bn.over[slot] = list_entry(y, (uint32_t)i);
         } else if (dp >= -kDLo) {
-            atomicAdd(&bn.cnt[bin_of(dp)], 1u);
+            const int b = bin_of(dp);
+            atomicAdd(&bn.cnt[b], 1u);
+            if (b < kMassBins) atomicAdd((unsigned long long *)&mass64[b], (unsigned long long)(fast_exp(dp) * kMassScale));
         }
     };
     for (int base = 0; base < n4; base += kThreads * kUnroll) {
@@ -897,7 +958,10 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
                 const int slot = atomicAdd(&bn.nover, 1);
                 if (slot < kOverCap) bn.over[slot] = list_entry(yp, id);
             } else if (dq >= -kDLo) {
-                atomicAdd(&bn.cnt[bin_of(dq)], 1u);   // raw counts stay: segment sizes are upper bounds
+                // raw counts stay (segment sizes are upper bounds); masses are a plan only
+                const int b = bin_of(dq);
+                atomicAdd(&bn.cnt[b], 1u);
+                if (b < kMassBins) atomicAdd((unsigned long long *)&mass64[b], (unsigned long long)(fast_exp(dq) * kMassScale));
             }
         }
         __syncthreads();
@@ -927,11 +991,12 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
         double eb[kPer];
         double loc = 0.0;
         uint32_t ctot = 0;
+        const double mscale = (double)fast_exp(shift) / (double)kMassScale;   // mass rel. m0 -> rel. m
 #pragma unroll
         for (int c = 0; c < kPer; c++) {
             const int b = kPer * t + c;
             cntv[c] = bn.cnt[b];
-            eb[c] = (double)cntv[c] * e_at((float)b + 0.5f);
+            eb[c] = b < kMassBins ? (double)mass64[b] * mscale : (double)cntv[c] * e_at((float)b + 0.5f);
             loc += eb[c];
             ctot += cntv[c];
         }
@@ -953,10 +1018,16 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
             int b1 = 0;
             if (cntv[c] && !col) {
                 b1 = grid_exp((float)lo);
-                col |= grid_exp((float)(lo * dl)) != grid_exp((float)(hi * dh));
+                const bool cx = grid_exp((float)(lo * dl)) != grid_exp((float)(hi * dh));
+                col |= cx;
                 const int c1 = ilogb(ehi);
-                if (c1 < b1) col |= cn * ldexp(1.0, c1 - b1) > kTieThr;
-                col |= cn * (ldexp(ehi, 23 - b1) + 1.0) >= 4.0e9;
+                const bool ct = (c1 < b1) && cn * ldexp(1.0, c1 - b1) > kTieThr;
+                col |= ct;
+                const bool co = cn * (ldexp(ehi, 23 - b1) + 1.0) >= 4.0e9;
+                col |= co;
+#ifdef GS_TIMING
+                if (blockIdx.x == g_row) { if (cx) atomicAdd(&g_fails[1010], (int)cntv[c]); if (ct) atomicAdd(&g_fails[1011], (int)cntv[c]); if (co) atomicAdd(&g_fails[1012], (int)cntv[c]); g_fails[1013] = __float_as_int((float)lo); }
+#endif
             }
             if (cntv[c] == 0) col = false;
             bn.meta[b] = (col ? kMetaCol | kMetaNow : 0u) | (cntv[c] ? 8u : 0u) | ((uint32_t)(b1 + 128) << 8) |
@@ -1031,11 +1102,29 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     GS_DIAG(26, N);
     GS_DIAG(28, bn.ndefer);
     GS_DIAG(30, bn.nties);
+    // ties rounded down (wave 0) and, if there are ties, rounded up (wave 1),
+    // concurrently
     float Slo, Shi;
-    if (walk(sm, W, N, run_fn(bn, 1, false), [](float) { return false; }, &Slo) != N) BINS_FAIL();
-    Shi = Slo;
     const bool s_exact = bn.nties == 0;
-    if (!s_exact && walk(sm, W, N, run_fn(bn, 1, true), [](float) { return false; }, &Shi) != N) BINS_FAIL();
+    {
+        const int w = wave_id();
+        if (w == 0 || (w == 1 && !s_exact)) {
+            float sv;
+            const int rr = wave_walk(W, N, run_fn(bn, 1, w == 1), [](float) { return false; }, &sv);
+            if (lane_id() == 0) {
+                if (w == 0) { sm.seq.first = rr; sm.seq.s = sv; }
+                else { sm.seq.start = rr; bn.Shi = sv; }
+            }
+        }
+        __syncthreads();
+#ifdef GS_TIMING
+        if (t == 0 && (sm.seq.first != N || (!s_exact && sm.seq.start != N))) { g_fails[1000] = blockIdx.x; g_fails[1001] = sm.seq.first; g_fails[1002] = sm.seq.start; g_fails[1003] = N; g_fails[1004] = bn.nties; }
+#endif
+        if (sm.seq.first != N || (!s_exact && sm.seq.start != N)) BINS_FAIL();
+        Slo = sm.seq.s;
+        Shi = s_exact ? Slo : bn.Shi;
+        __syncthreads();
+    }
     if (!(Slo > 0.0f) || !(Shi >= Slo) || !isfinite(Shi)) BINS_FAIL();
     GS_STAMP(14);
 
@@ -1094,7 +1183,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
             bn.Slo = Slo;
             bn.Shi = Shi;
             bn.inv_s = (float)(1.0 / Sc);
-            bn.hw2 = 2.0f * kExpErr + (float)(((double)Shi - (double)Slo) / (double)Slo) + 0x1p-21f;
+            bn.hw2 = 2.0f * kExpErr + (float)(((double)Shi - (double)Slo) / (double)Slo) + 0x1p-22f;
             bn.s2lo = (float)s2lo;
             bn.s2hi = (float)s2hi;
         }
@@ -1177,6 +1266,9 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     GS_STAMP(18);
 
     // ---- pass 4 (cache, rare): collect the bins of possible ties -------------
+#ifdef GS_TIMING
+    if (t == 0 && blockIdx.x < 256) g_fails[512 + blockIdx.x] = ((bn.ncollect >> 16) ? 1 : 0) | (s_exact ? 0 : 4);
+#endif
     if (bn.ncollect >> 16) {
         collect_now(sm, row, V, t_one, T, has_pen, gl);
         if (!finish_now(sm, gl, tmp)) BINS_FAIL();
@@ -1291,6 +1383,9 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     }
     __syncthreads();
     if (bn.fail) BINS_FAIL();
+#ifdef GS_TIMING
+    if (t == 0 && blockIdx.x < 256 && bn.ncollect) g_fails[512 + blockIdx.x] |= 2;
+#endif
     if (bn.ncollect) {
         collect_now(sm, row, V, t_one, T, has_pen, gl);
         if (!finish_now(sm, gl, tmp)) BINS_FAIL();

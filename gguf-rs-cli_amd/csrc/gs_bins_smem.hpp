@@ -11,11 +11,12 @@ constexpr int kMaxGroups = 256;    // runs of consecutive collected bins
 struct BinsSmem {
     uint32_t cnt[kBins];           // pass 1: count; then collected bin -> cursor, bulk bin -> run index
     uint32_t off[kBins + 1];       // list segment of bin b: [off[b], off[b+1])
-    uint32_t esum[kBins];          // bulk bin: sum of seq-1 increments
+    // esum and k2 together double as a u64 mass array during pass 1 and plan A
+    alignas(8) uint32_t esum[kBins];  // bulk bin: sum of seq-1 increments (later seq 3)
     uint32_t k2[kBins];            // bulk bin: sum of seq-2 increments (collected bin: f32 mass, transiently)
     uint32_t meta[kBins];          // flags, tie count and grid exponents
     float pre_e[kBins + 1];        // summand mass before bin b (plan B), for plan C
-    uint32_t sbase[kBins];         // segment sort: first work item of bin b
+    uint32_t nzc[kBins];           // segment sort: nonzero entries of bin b, then their prefix
     uint64_t over[kOverCap];       // (key << 32) | ~idx of d' > kDUp
     uint32_t gbeg[kMaxGroups];     // group g: list range [gbeg, gend)
     uint32_t gend[kMaxGroups];
