@@ -561,12 +561,14 @@ __device__ __forceinline__ int inc_s_range(float e, float Slo, float Shi, int b,
 // Pass constants, kept in registers by the pass loops.
 struct PassK {
     float m0, m, inv_s, inv_s2, hw2;
+    int ixlim;                     // pass 3: record indices of bins <= ixlim
 };
 // Classification of one element: cl 0 nothing to do, 1 list it, 2 defer it,
 // 3 add increment k to bin b.  Branch-free; one LDS read (meta).
 struct Cls {
     int b, cl;
     uint32_t k;
+    bool wix;                      // record the element index in its bin's segment
 };
 // Pass 2: accumulation 1 (src/sampler.rs:54).
 __device__ __forceinline__ Cls classify1(const BinsSmem &bn, const PassK &K, float y)
@@ -578,6 +580,7 @@ __device__ __forceinline__ Cls classify1(const BinsSmem &bn, const PassK &K, flo
     const uint32_t mt = bn.meta[c.b];
     const bool ok = inc_of(ldexpf(fast_exp(y - K.m), 23 - meta_b(mt, 1)), 2.0f * kExpErr, &c.k);
     c.cl = !inr ? 0 : ((mt & kMetaCol) ? 1 : (ok ? 3 : 2));
+    c.wix = false;
     return c;
 }
 // Pass 3: accumulation 2, p = e / S (src/sampler.rs:56, :61-63).
@@ -591,6 +594,7 @@ __device__ __forceinline__ Cls classify3(const BinsSmem &bn, const PassK &K, flo
     const float p = fast_exp(y - K.m) * K.inv_s;
     const bool ok = inc_of(ldexpf(p, 23 - meta_b(mt, 2)), K.hw2, &c.k);
     c.cl = !inr ? 0 : ((mt & kMetaNow) ? 1 : (((mt & kMetaCol) || !(mt & 2u)) ? 0 : (ok ? 3 : 2)));
+    c.wix = inr && c.b <= K.ixlim;
     return c;
 }
 // Pass 4: accumulation 3, q = p / s2 (src/sampler.rs:68, :74-75).
@@ -604,6 +608,7 @@ __device__ __forceinline__ Cls classify4(const BinsSmem &bn, const PassK &K, flo
     const float q = fast_exp(y - K.m) * K.inv_s * K.inv_s2;
     const bool ok = inc_of(ldexpf(q, 23 - meta_b(mt, 3)), 2.0f * kExpErr + 0x1p-22f, &c.k);
     c.cl = !inr ? 0 : ((mt & kMetaNow) ? 1 : (((mt & kMetaCol) || !(mt & 4u)) ? 0 : (ok ? 3 : 2)));
+    c.wix = false;
     return c;
 }
 
@@ -612,11 +617,12 @@ __device__ __forceinline__ Cls classify4(const BinsSmem &bn, const PassK &K, flo
 // as cls says.  Raw contributions of penalized ids are undone first.
 template <class ClsF>
 __device__ void bins_pass(RowSmem &sm, const float *row, int V, bool t_one, float T, bool has_pen,
-                          uint64_t *gl, uint32_t *defer, uint32_t dcap, uint32_t *acc, ClsF cls)
+                          uint64_t *gl, uint32_t *defer, uint32_t dcap, uint32_t *acc, uint32_t *ix, ClsF cls)
 {
     BinsSmem &bn = sm.x.bn;
     const int t = threadIdx.x;
     auto act = [&](int i, float y, const Cls &c, uint32_t flag) {
+        if (c.wix) stg(ix + atomicAdd(&bn.icur[c.b], 1u), (uint32_t)i);
         if (c.cl == 1) {
             const uint32_t slot = atomicAdd(&bn.cnt[c.b], 1u) & ~kNow;
             stg(gl + slot, list_entry(y, (uint32_t)i));
@@ -693,6 +699,50 @@ __device__ bool collect_now(RowSmem &sm, const float *row, int V, bool t_one, fl
         }
         __syncthreads();
     }
+    return true;
+}
+
+// collect_now for rows whose bins were indexed in pass 3 (ix[off[b],
+// icur[b]) holds every element of bin b <= ixlim): the flagged bins are
+// listed from their index segments, one wave per bin, without a pass over
+// the row.  Returns false if a flagged bin was not indexed.
+__device__ bool collect_now_ix(RowSmem &sm, const float *row, bool t_one, float T, uint64_t *gl,
+                               const uint32_t *ix)
+{
+    BinsSmem &bn = sm.x.bn;
+    const int t = threadIdx.x, lane = lane_id();
+    constexpr int kPer = kBins / kThreads;
+    uint32_t nk = 0;
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < kPer; c++) {
+        const int b = kPer * t + c;
+        if (bn.cnt[b] & kNow) {
+            nk++;
+            bad |= b > bn.ixlim || bn.icur[b] != bn.off[b + 1];
+        }
+    }
+    if (block_or((int)bad, sm)) return false;
+    uint32_t tot;
+    uint32_t ex = block_excl_u32(nk, &tot, sm);
+#pragma unroll
+    for (int c = 0; c < kPer; c++) {
+        const int b = kPer * t + c;
+        if (bn.cnt[b] & kNow) bn.nzc[ex++] = (uint32_t)b;
+    }
+    __syncthreads();
+    for (uint32_t k = wave_id(); k < tot; k += kWaves) {
+        const int b = (int)bn.nzc[k];
+        for (uint32_t p = bn.off[b] + lane; p < bn.off[b + 1]; p += 64) {
+            const uint32_t id = ldg(ix + p);
+            const float x = ldg(row + id);
+            const float y = t_one ? x : x / T;
+            const uint32_t slot = atomicAdd(&bn.cnt[b], 1u) & ~kNow;
+            stg(gl + slot, list_entry(y, id));
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
     return true;
 }
 
@@ -855,6 +905,13 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     float *W = reinterpret_cast<float *>(gl + lneed + kDeferCapG / 2);
     uint32_t *WT = reinterpret_cast<uint32_t *>(W + kWalkCap);
     uint64_t *tmp = reinterpret_cast<uint64_t *>(W);       // segment sort staging (W is dead then)
+    // element indices by bin (same positions as the list), recorded in pass 3
+    // for bins up to the cut when the row has no penalty and a nucleus cut;
+    // later stages read the elements of a few bins from them instead of
+    // passing over the row again
+    uint32_t *ix = reinterpret_cast<uint32_t *>(gl + lneed + kDeferCapG / 2 + kWalkCap);
+    if (lcap < lneed + kDeferCapG / 2 + kWalkCap + (lneed + 1) / 2) BINS_FAIL();
+    const bool use_ix = (top_p < 1.0f) && !has_pen;
     BinsSmem &bn = sm.x.bn;
     const int t = threadIdx.x;
     const bool t_one = (T == 1.0f);
@@ -1051,7 +1108,8 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     K.inv_s = 1.0f;
     K.inv_s2 = 1.0f;
     K.hw2 = 0.0f;
-    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.esum,
+    K.ixlim = -1;
+    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.esum, nullptr,
               [&bn, K](float y) { return classify1(bn, K, y); });
     GS_STAMP(11);
     if ((uint32_t)bn.ndefer > dcap) BINS_FAIL();
@@ -1159,7 +1217,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
         const double pre = block_excl_f64(loc, &stot, sm) + osum;
         stot += osum;
         double s2lo = 1.0, s2hi = 1.0;
-        if (t == 0) bn.cut_g = kBins;
+        if (t == 0) { bn.cut_g = kBins; bn.ixlim = -1; }
         __syncthreads();
         if (nucleus) {
             if (stot / Sc < (double)top_p * (1.0 + 2.0 * kDelta)) BINS_FAIL();   // the cut may not happen
@@ -1214,25 +1272,28 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
                 }
                 bn.meta[b] = (mt & 0xff00u) | (mt & 0x78u) | (col ? 0x81u : 0u) | (k2 ? 2u : 0u) |
                              ((uint32_t)(b2 + 128) << 16) | (128u << 24);
+                if (k2) atomicMax(&bn.ixlim, b);
                 if (col) {
                     bn.cnt[b] = bn.off[b] | kNow;
                     atomicAdd(&bn.ncollect, 1);
                 }
             }
             bn.k2[b] = 0u;
+            bn.icur[b] = bn.off[b];
             bn.pre_e[b] = (float)lo;
             lo = hi;
         }
         if (t == kThreads - 1) bn.pre_e[kBins] = (float)lo;
     }
-    if (t == 0) bn.ndefer = 0;
+    if (t == 0) { bn.ndefer = 0; bn.ixlast = -1; }
     __syncthreads();
     GS_STAMP(16);
 
     // ---- pass 3 (cache): accumulation-2 increments, new bins listed ----------
     K.inv_s = bn.inv_s;
     K.hw2 = bn.hw2;
-    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.k2,
+    K.ixlim = use_ix ? bn.ixlim : -1;
+    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.k2, ix,
               [&bn, K](float y) { return classify3(bn, K, y); });
     GS_STAMP(17);
     GS_DIAG(29, bn.ndefer | ((uint64_t)bn.ncollect << 32));
@@ -1270,7 +1331,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     if (t == 0 && blockIdx.x < 256) g_fails[512 + blockIdx.x] = ((bn.ncollect >> 16) ? 1 : 0) | (s_exact ? 0 : 4);
 #endif
     if (bn.ncollect >> 16) {
-        collect_now(sm, row, V, t_one, T, has_pen, gl);
+        if (!use_ix || !collect_now_ix(sm, row, t_one, T, gl, ix)) collect_now(sm, row, V, t_one, T, has_pen, gl);
         if (!finish_now(sm, gl, tmp)) BINS_FAIL();
     }
     // runs carry the accumulation-2 grids now: always regroup; the walk array
@@ -1345,6 +1406,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
             col |= cn * (ldexp(qe, 23 - b3) + 1.0) >= 4.0e9;
             bn.meta[b] = (mt & 0x00ffffffu) | 4u | (col ? kMetaCol | kMetaNow : 0u) | ((uint32_t)(b3 + 128) << 24);
             if (col) bn.cnt[b] = bn.off[b] | kNow;
+            atomicMax(&bn.ixlast, b);
         }
         if (t == 0) {
             bn.ndefer = 0;
@@ -1358,8 +1420,51 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     // ---- pass 4 (cache): accumulation-3 increments, new bins listed ----------
     K.inv_s = bn.inv_s;
     K.inv_s2 = bn.inv_s2;
-    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.esum,
-              [&bn, K](float y) { return classify4(bn, K, y); });
+    K.ixlim = -1;
+    {
+        // with indexed bins, only the elements of bins up to the last seq-3
+        // bin are visited, through their indices; otherwise a pass over the row
+        bool gather = use_ix && bn.ixlast <= bn.ixlim;
+        if (gather) {
+            bool bad = false;
+            for (int b = t; b <= bn.ixlim; b += kThreads) bad |= bn.icur[b] != bn.off[b + 1];
+            gather = !block_or((int)bad, sm);
+        }
+        if (gather) {
+            const uint32_t p0 = bn.off[0], p1 = bn.ixlast >= 0 ? bn.off[bn.ixlast + 1] : p0;
+            auto act = [&](uint32_t i, float y, const Cls &c) {
+                if (c.cl == 1) {
+                    const uint32_t slot = atomicAdd(&bn.cnt[c.b], 1u) & ~kNow;
+                    stg(gl + slot, list_entry(y, i));
+                } else if (c.cl == 2) {
+                    const int slot = atomicAdd(&bn.ndefer, 1);
+                    if ((uint32_t)slot < dcap) stg(defer + slot, i);
+                } else if (c.cl == 3 && c.k) {
+                    atomicAdd(&bn.esum[c.b], c.k);
+                }
+            };
+            constexpr int kG = 4;
+            for (uint32_t p = p0 + t; p < p1; p += kThreads * kG) {
+                uint32_t id[kG];
+                float x[kG];
+#pragma unroll
+                for (int g = 0; g < kG; g++) id[g] = ldg(ix + min(p + (uint32_t)(g * kThreads), p1 - 1));
+#pragma unroll
+                for (int g = 0; g < kG; g++) x[g] = ldg(row + id[g]);
+#pragma unroll
+                for (int g = 0; g < kG; g++) {
+                    if (p + (uint32_t)(g * kThreads) < p1) {
+                        const float y = t_one ? x[g] : x[g] / T;
+                        act(id[g], y, classify4(bn, K, y));
+                    }
+                }
+            }
+            __syncthreads();
+        } else {
+            bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.esum, ix,
+                      [&bn, K](float y) { return classify4(bn, K, y); });
+        }
+    }
     GS_STAMP(22);
     if ((uint32_t)bn.ndefer > dcap) BINS_FAIL();
     if (!finish_now(sm, gl, tmp)) BINS_FAIL();
@@ -1387,7 +1492,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     if (t == 0 && blockIdx.x < 256 && bn.ncollect) g_fails[512 + blockIdx.x] |= 2;
 #endif
     if (bn.ncollect) {
-        collect_now(sm, row, V, t_one, T, has_pen, gl);
+        if (!use_ix || !collect_now_ix(sm, row, t_one, T, gl, ix)) collect_now(sm, row, V, t_one, T, has_pen, gl);
         if (!finish_now(sm, gl, tmp)) BINS_FAIL();
     }
     if (!build_groups(sm)) BINS_FAIL();

@@ -17,6 +17,7 @@ struct BinsSmem {
     uint32_t meta[kBins];          // flags, tie count and grid exponents
     float pre_e[kBins + 1];        // summand mass before bin b (plan B), for plan C
     uint32_t nzc[kBins];           // segment sort: nonzero entries of bin b, then their prefix
+    uint32_t icur[kBins];          // pass 3: cursor of bin b's element indices
     uint64_t over[kOverCap];       // (key << 32) | ~idx of d' > kDUp
     uint32_t gbeg[kMaxGroups];     // group g: list range [gbeg, gend)
     uint32_t gend[kMaxGroups];
@@ -27,7 +28,7 @@ struct BinsSmem {
     float m0, m, s2lo, s2hi, Slo, Shi;
     float hw2, inv_s, inv_s2;
     int ngroups, ndefer, nover, fail, ncollect, nties;
-    int cut_g;
+    int cut_g, ixlim, ixlast;
 };
 
 } // namespace gs

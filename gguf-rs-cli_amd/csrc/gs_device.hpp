@@ -123,6 +123,12 @@ __device__ __forceinline__ float4 ldg(const float4 *p)
     const gs_f4 v = *(const __attribute__((address_space(1))) gs_f4 *)p;
     return make_float4(v.x, v.y, v.z, v.w);
 }
+typedef uint32_t gs_u4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg(const uint4 *p)
+{
+    const gs_u4 v = *(const __attribute__((address_space(1))) gs_u4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 template <class T>
 __device__ __forceinline__ void stg(T *p, T v)
 {

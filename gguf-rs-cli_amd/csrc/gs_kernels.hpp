@@ -30,10 +30,11 @@ struct RowArgs {
 
 // Per-row scratch (u32 units) of the full-vocabulary paths: the sort path
 // needs 4V; the binned path needs its element list (V + 4352 u64), the
-// deferred ids (65536 u32) and the walk array (65536 f32 + 65536 u32).
+// deferred ids (65536 u32), the walk array (65536 f32 + 65536 u32) and the
+// per-bin element indices (V + 4352 u32).
 inline size_t scratch_u32_per_row(size_t V)
 {
-    const size_t bins = 2 * (V + 4352) + 65536 + 2 * 65536;
+    const size_t bins = 2 * (V + 4352) + 65536 + 2 * 65536 + (V + 4352 + 1);
     return (4 * V > bins ? 4 * V : bins);
 }
 
