@@ -21,10 +21,14 @@ struct gs_sampler {
     size_t row_cap;
     uint32_t *d_rec;             // staging for host recent ids
     size_t rec_cap;
-    uint32_t *h_tok;             // pinned, mapped: kernel writes the token here
+    uint32_t *h_tok;             // pinned, mapped, coherent: kernel writes the token here
     int32_t *h_status;
-    uint32_t *d_tok_map;         // device aliases of h_tok / h_status
+    uint32_t *h_done;            // completion flag of single-row calls (sequence number)
+    uint32_t *d_tok_map;         // device aliases of h_tok / h_status / h_done
     int32_t *d_status_map;
+    uint32_t *d_done_map;
+    uint32_t seq;
+    const char *dev_lo, *dev_hi; // last device allocation seen by is_device_ptr
     uint32_t *scratch;           // full-vocabulary path
     size_t scratch_elems;
     int32_t *fb;                 // per-row fallback flags of the full-vocabulary path
@@ -33,11 +37,26 @@ struct gs_sampler {
 
 namespace {
 
-bool is_device_ptr(const void *p)
+// Device pointer test with a one-allocation cache: consecutive rows of one
+// device tensor skip the runtime query.
+bool is_device_ptr(gs_sampler *s, const void *p)
 {
+    const char *c = (const char *)p;
+    if (c >= s->dev_lo && c < s->dev_hi) return true;
     hipPointerAttribute_t at;
     if (hipPointerGetAttributes(&at, p) != hipSuccess) { (void)hipGetLastError(); return false; }
-    return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged;
+    const bool dev = at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged;
+    if (dev) {
+        hipDeviceptr_t base = nullptr;
+        size_t size = 0;
+        if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) == hipSuccess && base) {
+            s->dev_lo = (const char *)base;
+            s->dev_hi = (const char *)base + size;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
+    return dev;
 }
 
 int grow(void **buf, size_t *cap, size_t need_bytes)
@@ -86,13 +105,16 @@ int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out)
     s->state = seed;
     if (hipGetDevice(&s->device) != hipSuccess) { delete s; return GS_ERR_HIP; }
     if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) { delete s; return GS_ERR_HIP; }
-    if (hipHostMalloc((void **)&s->h_tok, 64, hipHostMallocMapped) != hipSuccess ||
+    if (hipHostMalloc((void **)&s->h_tok, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
         hipHostGetDevicePointer((void **)&s->d_tok_map, s->h_tok, 0) != hipSuccess) {
         gs_sampler_destroy(s);
         return GS_ERR_HIP;
     }
     s->h_status = (int32_t *)(s->h_tok + 4);
     s->d_status_map = (int32_t *)(s->d_tok_map + 4);
+    s->h_done = s->h_tok + 8;
+    s->d_done_map = s->d_tok_map + 8;
+    *(volatile uint32_t *)s->h_done = 0u;
     *out = s;
     return GS_OK;
 }
@@ -157,7 +179,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     if (W > (size_t)gs::kMaxWindow) return GS_ERR_UNSUPPORTED;
     int rc;
     const float *d_logits = logits;
-    if (V > 0 && !is_device_ptr(logits)) {
+    if (V > 0 && !is_device_ptr(s, logits)) {
         void *p = s->d_row;
         rc = grow(&p, &s->row_cap, V * sizeof(float));
         s->d_row = (float *)p;
@@ -167,7 +189,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
         d_logits = s->d_row;
     }
     const uint32_t *d_rec = recent;
-    if (W > 0 && !is_device_ptr(recent)) {
+    if (W > 0 && !is_device_ptr(s, recent)) {
         void *p = s->d_rec;
         rc = grow(&p, &s->rec_cap, W * sizeof(uint32_t));
         s->d_rec = (uint32_t *)p;
@@ -196,8 +218,24 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     a.scratch_stride = gs::scratch_u32_per_row(V);
     a.fb = s->fb;
     const bool full = needs_full_path(s->params, V);
+    // A single small-path kernel signals completion through the mapped flag,
+    // so the host polls it instead of a stream synchronisation; the
+    // full-vocabulary path (several kernels) synchronises the stream.
+    const uint32_t seq = ++s->seq;
+    if (!full) {
+        a.done = s->d_done_map;
+        a.done_val = seq;
+    }
     if (gs::launch_sample_rows(a, 1, !full, full, s->stream) != hipSuccess) return GS_ERR_HIP;
-    if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
+    bool synced = full;
+    if (!full) {
+        volatile uint32_t *f = s->h_done;
+        for (uint32_t spins = 0; *f != seq; spins++) {
+            if (spins > (1u << 22)) { synced = true; break; }   // slow call: fall back to the runtime
+            __builtin_ia32_pause();
+        }
+    }
+    if (synced && hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
     if (s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, 1);   // one draw iff T > 0
     int st = *(volatile int32_t *)s->h_status;
     if (st != GS_OK) return st;

@@ -685,6 +685,98 @@ __device__ int topk_row_tmax(RowSmem &sm, const float *row, int V, int k, float 
     return finish_sorted(sm, k, yv, ix, top_p, r);
 }
 
+// topk_row_tmax for rows held in registers (V <= kThreads * 4 * kRegF4, V a
+// multiple of 4, 16-byte aligned): the caller loads the row once, before
+// the penalty table is built, and the candidates come from the registers
+// instead of a second read of the row.
+constexpr int kRegF4 = 8;
+__device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int k, float T, float top_p,
+                            bool has_pen, int nuniq, float r, int *status, bool *ok)
+{
+    const int t = threadIdx.x;
+    const int n4 = V >> 2;
+    *ok = false;
+    const uint32_t need = (uint32_t)k + (uint32_t)nuniq;
+    if (need > (uint32_t)kThreads) return 0;
+    float tmax = -INFINITY;
+    bool any = false;
+    int nan = 0;
+#pragma unroll
+    for (int u = 0; u < kRegF4; u++) {
+        if (u * kThreads + t < n4) {
+            const float xs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                nan |= (int)isnan(xs[c]) | ((int)isinf(xs[c]) & (int)isinf(T));
+                tmax = fmaxf(tmax, xs[c]);
+            }
+            any = true;
+        }
+    }
+    if (block_or(nan, sm)) { *ok = true; *status = GS_ERR_NAN; return 0; }
+    GS_STAMP(2);
+    const uint32_t tk = any ? f2key(tmax) : 0u;
+    uint32_t prefix = 0, above = 0;
+    for (int level = 0; level < 2; level++) {
+        const int sh = level == 0 ? 20 : 8;
+        for (int i = t; i < 4096; i += kThreads) sm.x.tk.u.hist[i] = 0;
+        __syncthreads();
+        if (level == 0 || (tk >> 20) == prefix) atomicAdd(&sm.x.tk.u.hist[(tk >> sh) & 4095u], 1u);
+        __syncthreads();
+        uint32_t b, ab;
+        select_bin(sm, 4096, need - above, &b, &ab);
+        above += ab;
+        prefix = level == 0 ? b : ((prefix << 12) | b);
+    }
+    const uint32_t tau = prefix << 8;   // >= need thread maxima have key >= tau
+    GS_STAMP(3);
+    if (t == 0) sm.ncand = 0;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kRegF4; u++) {
+        const int q = u * kThreads + t;
+        if (q < n4) {
+            const float xs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int i = 4 * q + c;
+                if (f2key(xs[c]) >= tau && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) {
+                    const int slot = atomicAdd(&sm.ncand, 1);
+                    if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(xs[c] / T), (uint32_t)i);
+                }
+            }
+        }
+    }
+    if (has_pen) {
+        for (int s = t; s < kHashSlots; s += kThreads) {
+            const uint32_t id = sm.hkey[s];
+            if (id == kEmpty) continue;
+            const float x = __uint_as_float(sm.hval[s]);
+            if (f2key(x) >= tau) {
+                const int slot = atomicAdd(&sm.ncand, 1);
+                if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(x / T), id);
+            }
+        }
+    }
+    __syncthreads();
+    GS_STAMP(4);
+    const int nc = sm.ncand;
+    __syncthreads();
+    if (nc > kCandCap || nc < k) return 0;
+    sort_cand_desc(sm, nc);
+    GS_STAMP(5);
+    if (tau > 0x007fffffu) {
+        const float y_out = key2f(tau - 1u) / T;
+        const uint32_t yk = (uint32_t)(sm.x.tk.cand[k - 1] >> 32);
+        if (!(f2key(y_out) < yk)) return 0;
+    }
+    *ok = true;
+    auto yv = [&](int j) { return key2f((uint32_t)(sm.x.tk.cand[j] >> 32)); };
+    auto ix = [&](int j) { return ~(uint32_t)sm.x.tk.cand[j]; };
+    *status = GS_OK;
+    return finish_sorted(sm, k, yv, ix, top_p, r);
+}
+
 #include "gs_bins.hpp"
 
 // --------------------------------------------------------------------------
@@ -825,6 +917,19 @@ sample_rows_kernel(RowArgs a)
         W = a.recent_len ? (int)a.recent_len[b] : a.W;
         if (W > a.W) W = a.W;
     }
+    // Small top-k rows that fit in registers: issue the row loads before the
+    // penalty table is built, so the two overlap.
+    const int keep0 = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
+    const bool regpath = MODE == kModeSmall && p.temperature > 0.0f && V > 1 && (V & 3) == 0 &&
+                         V <= kThreads * 4 * kRegF4 && keep0 < V &&
+                         ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+    float4 rv[kRegF4];
+    if (regpath) {
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        const int n4 = V >> 2;
+#pragma unroll
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+    }
     __syncthreads();
     if (has_pen) build_penalty(sm, row, V, a.recent + (size_t)b * a.ld_recent, W,
                                p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
@@ -854,8 +959,11 @@ sample_rows_kernel(RowArgs a)
             status = GS_ERR_NAN;
         } else {
             bool ok;
-            tok = topk_row_tmax(sm, row, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r,
-                                aligned, &status, &ok);
+            if (regpath)
+                tok = topk_row_reg(sm, rv, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r, &status, &ok);
+            else
+                tok = topk_row_tmax(sm, row, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r,
+                                    aligned, &status, &ok);
             if (!ok)
                 tok = topk_row<true>(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, aligned,
                                      &status, &ok);
@@ -889,6 +997,10 @@ sample_rows_kernel(RowArgs a)
     if (t == 0) {
         a.tokens[b] = (uint32_t)tok;
         if (a.status) a.status[b] = status;
+        if (a.done) {
+            __threadfence_system();           // token and status before the flag
+            __hip_atomic_store(a.done, a.done_val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 
