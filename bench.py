@@ -26,6 +26,20 @@ sys.path.insert(0, os.path.join(ROOT, "gguf-rs-cli_amd"))
 PEAK_HBM_GBS = 8000.0   # MI355X HBM3E
 
 
+def profiled_traffic():
+    """HBM bytes per c3 step from the committed rocprofv3 summary
+    (FETCH_SIZE and WRITE_SIZE runs, scaled by a plain-copy calibration), or
+    None if the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "sample_rows_c3_qwen_V152064_B256.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -200,7 +214,7 @@ def main():
         "config": {"workload": "c3 Qwen2.5 V=152064 B=256 top_k=0 top_p=0.95 T=1.0 rep=1.0",
                    "global_batch": c3["B"], "vocab": c3["V"], "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": profiled_traffic(),
                      "kernel": "gs::sample_rows_kernel", "bytes_per_launch": c3["bytes"]},
         "c1_latency": {"p50_us": c1["p50_us"], "p90_us": c1["p90_us"], "kernel_us": c1k,
                        "V": 32000, "B": 1, "steps": 256},
