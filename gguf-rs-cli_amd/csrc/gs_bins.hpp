@@ -325,19 +325,77 @@ __device__ __forceinline__ bool is_marker(float v) { return isnan(v); }
 __device__ __forceinline__ int marker_run(float v) { return (int)(__float_as_uint(v) & 0xffffu); }
 __device__ __forceinline__ float make_marker(int r) { return __uint_as_float(0x7fc00000u | (uint32_t)r); }
 
+// Run tables of one walk, built block-wide by make_walk_tab: per run r,
+// inc[r] = (increment with seq-1 ties rounded up << 32) | increment with ties
+// rounded down, each capped at kSat, or kBadInc if the run has no increments
+// for this accumulation; ex[r] = packed planned grid exponents (rounded down
+// | rounded up << 16, each + 512), kAnyEx where the increment is 0.
+constexpr uint32_t kBadInc = 0xffffffffu;
+constexpr int kAnyEx = 0xffff;
+struct WalkTab {
+    const uint64_t *inc;
+    const int *ex;
+    int G;
+    int hi;                        // 1: use the ties-rounded-up half
+};
+__device__ void make_walk_tab(RowSmem &sm, int which)
+{
+    BinsSmem &bn = sm.x.bn;
+    const int G = bn.ngroups;
+    for (int r = threadIdx.x; r <= G; r += kThreads) {
+        uint32_t lo = 0u, hi = 0u;
+        int exl = kAnyEx, exh = kAnyEx;
+        const int packed = bn.runb[r];
+        if (r > 0 && packed != kNoRun) {
+            const bool have = which == 1 || (which == 2 && (packed & (1 << 24))) || (which == 3 && (packed & (1 << 25)));
+            if (!have) {
+                lo = hi = kBadInc;
+            } else {
+                const uint64_t R = bn.run[r], Rh = R + (which == 1 ? bn.runt[r] : 0u);
+                const int eb = ((packed >> (8 * (which - 1))) & 255) - 128;
+                lo = R > kSat ? kSat : (uint32_t)R;
+                hi = Rh > kSat ? kSat : (uint32_t)Rh;
+                if (lo) exl = eb + 512;
+                if (hi) exh = eb + 512;
+            }
+        }
+        bn.run[r] = ((uint64_t)hi << 32) | lo;
+        bn.wbase[r] = (uint32_t)(exl | (exh << 16));
+    }
+    __syncthreads();
+}
+__device__ __forceinline__ WalkTab walk_tab(const BinsSmem &bn, bool hi)
+{
+    return WalkTab{bn.run, reinterpret_cast<const int *>(bn.wbase), bn.ngroups, hi ? 1 : 0};
+}
+// Increment of a marker item at grid exponent e; *bad if the run cannot be
+// applied there.  Reads the tables for any item (the index is clamped).
+__device__ __forceinline__ uint32_t tab_inc(const WalkTab &T, float v, int e, bool *bad)
+{
+    const int r = min(marker_run(v), T.G);
+    const uint64_t pk = T.inc[r];
+    const int exw = T.ex[r];
+    const uint32_t inc = T.hi ? (uint32_t)(pk >> 32) : (uint32_t)pk;
+    const int ex = T.hi ? (int)((uint32_t)exw >> 16) : (exw & 0xffff);
+    *bad = inc == kBadInc || (ex != kAnyEx && ex != e + 512);
+    return inc == kBadInc ? 0u : inc;
+}
+
 // Exact replay of one accumulation over the walk array by a single wave,
-// kWalkK consecutive items per lane (kWalkK * 64 items per step): each lane
-// composes the increment functions of its items, a DPP scan composes the
-// lanes, and each lane then checks its items in order for an event (binade
-// crossing, the predicate, or a run that does not apply).  The first event
-// is evaluated with the reference's own f32 add and the step restarts after
-// it.  Items: f32 summands, or run markers (a NaN whose payload is the run
-// index); runfn(r, e, &f) gives run r's increment function at grid exponent
-// e, or false.  Returns the first item after which pred holds, n if none, or
-// -1 when an event falls on a run.  Wave-uniform result.
+// kWalkK consecutive items per lane (kWalkK * 64 items per step).  Items are
+// f32 summands, or run markers (a NaN whose payload is the run index) that
+// stand for a run's integer increment (tables from make_walk_tab).  Each
+// step composes the lanes' increment functions with a DPP scan and checks
+// each item in order for an event: a binade crossing, the predicate, or a
+// run that does not apply.  Windows without rounding ties use plain integer
+// sums at grids e and e + 1 and take one crossing within the step; windows
+// with ties compose parity functions (ParFn) and restart after each event.
+// The event's element is added with the reference's own f32 add.  Returns
+// the first item after which pred holds, n if none, or -1 when an event
+// falls on a run.  Wave-uniform result.
 constexpr int kWalkK = 4;
-template <class RunFn, class Pred>
-__device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s_out)
+template <class Pred>
+__device__ int wave_walk(const float *W, int n, const WalkTab &T, Pred pred, float *s_out)
 {
     const int lane = lane_id();
     float s = 0.0f;
@@ -345,8 +403,8 @@ __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s
     while (pos < n && s == 0.0f) {               // 0 + a == a exactly
         const float v = ldg(W + pos);
         if (is_marker(v)) {
-            ParFn f;
-            if (!runfn(marker_run(v), -126, &f) || f.f0 != 0u) { *s_out = s; return -1; }
+            bool bad;
+            if (tab_inc(T, v, -126, &bad) != 0u || bad) { *s_out = s; return -1; }
         } else {
             s = s + v;
             if (pred(s)) { *s_out = s; return pos; }
@@ -373,18 +431,111 @@ __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s
         while (start < lim) {
             const int e = grid_exp(s);
             const uint32_t M = (uint32_t)ldexpf(s, 23 - e);
-            ParFn f[kWalkK];
-            bool bad[kWalkK], valid[kWalkK];
+            uint32_t k0[kWalkK], k1[kWalkK];
+            bool bad0[kWalkK], bad1[kWalkK], valid[kWalkK], t0[kWalkK];
+            bool anytie = false;
 #pragma unroll
             for (int q = 0; q < kWalkK; q++) {
                 const int idx = kWalkK * lane + q;
                 valid[q] = idx >= start && idx < lim;
-                f[q].f0 = f[q].f1 = 0u;
-                bad[q] = false;
-                if (valid[q]) {
-                    if (is_marker(v[q])) bad[q] = !runfn(marker_run(v[q]), e, &f[q]);
-                    else f[q] = elem_fn(v[q], e);
+                const bool mk = is_marker(v[q]);
+                bool rb0, rb1, et0, et1;
+                const uint32_t r0 = tab_inc(T, v[q], e, &rb0), r1 = tab_inc(T, v[q], e + 1, &rb1);
+                const uint32_t e0 = elem_inc(v[q], e, &et0), e1 = elem_inc(v[q], e + 1, &et1);
+                k0[q] = !valid[q] ? 0u : (mk ? r0 : e0);
+                k1[q] = !valid[q] ? 0u : (mk ? r1 : e1);
+                bad0[q] = valid[q] && mk && rb0;
+                bad1[q] = valid[q] && mk && rb1;
+                t0[q] = valid[q] && !mk && et0;
+                anytie |= valid[q] && !mk && (et0 || et1);
+            }
+            if (!__any(anytie)) {
+                // ---- fast step: integer sums at grids e and e + 1 ----
+                uint32_t l0 = 0, l1 = 0;
+#pragma unroll
+                for (int q = 0; q < kWalkK; q++) { l0 = sat_add(l0, k0[q]); l1 = sat_add(l1, k1[q]); }
+                const uint32_t i0 = wave_scan_add(l0), i1 = wave_scan_add(l1);
+                uint32_t b = i0 - l0;                        // grid-e increments before this lane's items
+                uint32_t c1[kWalkK];                         // inclusive grid-(e+1) sums
+                {
+                    uint32_t acc = i1 - l1;
+#pragma unroll
+                    for (int q = 0; q < kWalkK; q++) { acc += k1[q]; c1[q] = acc; }
                 }
+                int qev = kWalkK;
+#pragma unroll
+                for (int q = 0; q < kWalkK; q++) {
+                    if (qev == kWalkK) {
+                        const uint32_t a = b + k0[q];
+                        const bool ev = valid[q] && ((M + a) >= (1u << 24) || bad0[q] ||
+                                                     pred(ldexpf((float)(M + a), e - 23)));
+                        if (ev) qev = q;
+                        else b = a;
+                    }
+                }
+                const uint64_t mask = __ballot(qev < kWalkK);
+                if (mask == 0) {
+                    s = ldexpf((float)(M + (uint32_t)__builtin_amdgcn_readlane((int)b, (lim - 1) / kWalkK)), e - 23);
+                    break;
+                }
+                const int L = __ffsll((unsigned long long)mask) - 1;
+                const int q = __builtin_amdgcn_readlane(qev, L);
+                float vq = v[0];
+                uint32_t cq = c1[0];
+#pragma unroll
+                for (int k = 1; k < kWalkK; k++) if (q == k) { vq = v[k]; cq = c1[k]; }
+                const float vL = rdl(vq, L);
+                if (is_marker(vL)) { *s_out = s; return -1; }   // event on a run
+                const int idx = kWalkK * L + q;
+                const float sc = ldexpf((float)(M + (uint32_t)__builtin_amdgcn_readlane((int)b, L)), e - 23) + vL;
+                s = sc;
+                if (pred(sc)) { *s_out = s; return pos + idx; }
+                start = idx + 1;
+                if (grid_exp(sc) != e + 1) continue;         // not a one-binade crossing: restart
+                // the rest of the window on the grid-(e+1) sums
+                const uint32_t C = (uint32_t)__builtin_amdgcn_readlane((int)cq, L);
+                const uint32_t M1 = (uint32_t)ldexpf(sc, 22 - e);
+                int qev2 = kWalkK;
+                uint32_t prev = i1 - l1;
+#pragma unroll
+                for (int q2 = 0; q2 < kWalkK; q2++) {
+                    const int idx2 = kWalkK * lane + q2;
+                    if (qev2 == kWalkK && idx2 > idx && valid[q2]) {
+                        const uint32_t a = M1 + (c1[q2] - C);
+                        if (a >= (1u << 24) || bad1[q2] || pred(ldexpf((float)a, e + 1 - 23))) qev2 = q2;
+                    }
+                    if (qev2 == kWalkK) prev = c1[q2];
+                }
+                const uint64_t mask2 = __ballot(qev2 < kWalkK);
+                if (mask2 == 0) {
+                    const uint32_t last = (uint32_t)__builtin_amdgcn_readlane((int)c1[kWalkK - 1], (lim - 1) / kWalkK);
+                    s = ldexpf((float)(M1 + (last - C)), e + 1 - 23);
+                    break;
+                }
+                const int L2 = __ffsll((unsigned long long)mask2) - 1;
+                const int q2 = __builtin_amdgcn_readlane(qev2, L2);
+                float v2 = v[0];
+#pragma unroll
+                for (int k = 1; k < kWalkK; k++) if (q2 == k) v2 = v[k];
+                const float vL2 = rdl(v2, L2);
+                if (is_marker(vL2)) { *s_out = s; return -1; }
+                const int idx2 = kWalkK * L2 + q2;
+                // prev: grid-(e+1) sum up to the item before idx2 (C right after the crossing)
+                const uint32_t before2 = (uint32_t)__builtin_amdgcn_readlane((int)prev, L2);
+                const float sc2 = ldexpf((float)(M1 + (before2 - C)), e + 1 - 23) + vL2;
+                s = sc2;
+                if (pred(sc2)) { *s_out = s; return pos + idx2; }
+                start = idx2 + 1;
+                continue;
+            }
+            // ---- step with ties: parity functions at grid e ----
+            ParFn f[kWalkK];
+#pragma unroll
+            for (int q = 0; q < kWalkK; q++) {
+                // a tie element: K + ((p + K) & 1), K the lower choice (elem_inc's value)
+                const uint32_t K = k0[q];
+                f[q].f0 = t0[q] ? K + (K & 1u) : k0[q];
+                f[q].f1 = t0[q] ? K + ((K + 1u) & 1u) : k0[q];
             }
             ParFn loc = f[0];
 #pragma unroll
@@ -394,14 +545,14 @@ __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s
             ex.f0 = __shfl_up(incl.f0, 1, 64);
             ex.f1 = __shfl_up(incl.f1, 1, 64);
             if (lane == 0) ex.f0 = ex.f1 = 0u;
-            uint32_t b = par_apply(ex, M & 1u);          // increments before this lane's items
+            uint32_t b = par_apply(ex, M & 1u);
             int qev = kWalkK;
 #pragma unroll
             for (int q = 0; q < kWalkK; q++) {
                 if (qev == kWalkK) {
                     const uint32_t a = sat_add(b, par_apply(f[q], (M + b) & 1u));
                     const bool cross = (M + a) >= (1u << 24);
-                    const bool ev = valid[q] && (cross || bad[q] || pred(ldexpf((float)(M + a), e - 23)));
+                    const bool ev = valid[q] && (cross || bad0[q] || pred(ldexpf((float)(M + a), e - 23)));
                     if (ev) qev = q;
                     else b = a;
                 }
@@ -417,7 +568,7 @@ __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s
 #pragma unroll
             for (int k = 1; k < kWalkK; k++) if (q == k) vq = v[k];
             const float vL = rdl(vq, L);
-            if (is_marker(vL)) { *s_out = s; return -1; }   // event on a run
+            if (is_marker(vL)) { *s_out = s; return -1; }
             const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)b, L);
             const float na = ldexpf((float)(M + before), e - 23) + vL;   // the reference's f32 add
             s = na;
@@ -431,13 +582,13 @@ __device__ int wave_walk(const float *W, int n, RunFn runfn, Pred pred, float *s
 }
 
 // Run wave_walk on wave 0 and hand the result to the whole block.
-template <class RunFn, class Pred>
-__device__ int walk(RowSmem &sm, const float *W, int n, RunFn runfn, Pred pred, float *s_out)
+template <class Pred>
+__device__ int walk(RowSmem &sm, const float *W, int n, int which, Pred pred, float *s_out)
 {
+    make_walk_tab(sm, which);
     if (wave_id() == 0) {
         float sv;
-        const int r = wave_walk(W, n, runfn, pred, &sv);
-
+        const int r = wave_walk(W, n, walk_tab(sm.x.bn, false), pred, &sv);
         if (lane_id() == 0) { sm.seq.first = r; sm.seq.s = sv; }
     }
     __syncthreads();
@@ -469,28 +620,6 @@ __device__ bool finish_segments(RowSmem &sm, uint64_t *gl, Sel sel)
     return bn.fail == 0;
 }
 
-// Increment functor of the runs for accumulation `which` (tie_up: the run's
-// seq-1 ties round up).
-struct RunFn {
-    const BinsSmem *bn;
-    int which;
-    bool tie_up;
-    __device__ bool operator()(int r, int e, ParFn *f) const
-    {
-        f->f0 = f->f1 = 0u;
-        if (r == 0 || bn->runb[r] == kNoRun) return true;
-        const int packed = bn->runb[r];
-        if (which == 2 && !(packed & (1 << 24))) return false;
-        if (which == 3 && !(packed & (1 << 25))) return false;
-        const uint64_t R = bn->run[r] + (tie_up ? bn->runt[r] : 0u);
-        if (R == 0) return true;
-        if (e != ((packed >> (8 * (which - 1))) & 255) - 128) return false;
-        const uint32_t R32 = R > kSat ? kSat : (uint32_t)R;
-        f->f0 = f->f1 = R32;
-        return true;
-    }
-};
-__device__ __forceinline__ RunFn run_fn(const BinsSmem &bn, int which, bool tie_up) { return RunFn{&bn, which, tie_up}; }
 
 // The flat walk array: per group g, a marker of run g, then the group's
 // sorted entries as exact summands expf(y - m) (0 for removed entries);
@@ -1165,10 +1294,11 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     float Slo, Shi;
     const bool s_exact = bn.nties == 0;
     {
+        make_walk_tab(sm, 1);
         const int w = wave_id();
         if (w == 0 || (w == 1 && !s_exact)) {
             float sv;
-            const int rr = wave_walk(W, N, run_fn(bn, 1, w == 1), [](float) { return false; }, &sv);
+            const int rr = wave_walk(W, N, walk_tab(bn, w == 1), [](float) { return false; }, &sv);
             if (lane_id() == 0) {
                 if (w == 0) { sm.seq.first = rr; sm.seq.s = sv; }
                 else { sm.seq.start = rr; bn.Shi = sv; }
@@ -1348,7 +1478,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     float S = Slo;
     if (!s_exact) {
         gather_runs(sm, 1);
-        if (walk(sm, W, N, run_fn(bn, 1, false), [](float) { return false; }, &S) != N) BINS_FAIL();
+        if (walk(sm, W, N, 1, [](float) { return false; }, &S) != N) BINS_FAIL();
         if (!(S >= Slo && S <= Shi)) BINS_FAIL();
     }
     GS_STAMP(20);
@@ -1374,7 +1504,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     uint32_t cut_tok = 0;
     if (nucleus) {
         gather_runs(sm, 2);
-        js = walk(sm, W, N, run_fn(bn, 2, false), [top_p](float c) { return c >= top_p; }, &s2);
+        js = walk(sm, W, N, 2, [top_p](float c) { return c >= top_p; }, &s2);
         if (js < 0 || js >= N || !(s2 >= bn.s2lo && s2 <= bn.s2hi)) BINS_FAIL();
         cut_tok = WT[js];
     }
@@ -1515,7 +1645,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     GS_STAMP(23);
     gather_runs(sm, 3);
     float c3;
-    const int jd = walk(sm, W, n3, run_fn(bn, 3, false), [r](float c) { return r < c; }, &c3);
+    const int jd = walk(sm, W, n3, 3, [r](float c) { return r < c; }, &c3);
     if (jd < 0) BINS_FAIL();
     if (jd < n3) *tok = (int)WT[jd];
     else if (nucleus) *tok = (int)WT[n3 - 1];

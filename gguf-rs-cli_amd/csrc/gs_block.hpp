@@ -110,6 +110,32 @@ __device__ __forceinline__ ParFn wave_scan_incl(ParFn v)
     return v;
 }
 
+// Wave64 inclusive add-scan of u32 with DPP moves (same pattern as above).
+__device__ __forceinline__ uint32_t wave_scan_add(uint32_t v)
+{
+    const int lane = lane_id(), rl = lane & 15;
+    uint32_t o;
+    o = dpp_mov<0x111>(v); if (rl >= 1) v += o;
+    o = dpp_mov<0x112>(v); if (rl >= 2) v += o;
+    o = dpp_mov<0x114>(v); if (rl >= 4) v += o;
+    o = dpp_mov<0x118>(v); if (rl >= 8) v += o;
+    o = dpp_mov<0x142>(v); if ((lane & 31) >= 16) v += o;
+    o = dpp_mov<0x143>(v); if (lane >= 32) v += o;
+    return v;
+}
+
+// Integer increment of summand a at grid exponent e (capped at kSat), and
+// whether it is an exact rounding tie.
+__device__ __forceinline__ uint32_t elem_inc(float a, int e, bool *tie)
+{
+    const float m = ldexpf(a, 23 - e);
+    const bool big = !(m < (float)kSat);
+    const float fl = floorf(m);
+    const float fr = m - fl;
+    *tie = !big && fr == 0.5f;
+    return big ? kSat : (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+}
+
 struct SeqSmem {
     ParFn wave_tot[kWaves];
     int first;
