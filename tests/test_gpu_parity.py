@@ -240,3 +240,59 @@ def test_reference_free_function_api(gpu, oracle):
         a = gs_sampler.sample(x, T, 40, 0.9, 1.1, rec)
         b = oracle.sample(x, T, 40, 0.9, 1.1, rec)
         assert a == b
+
+
+# --- full-vocabulary path (binned exact sums) -------------------------------
+def test_c3_full_batch_256(gpu, torch, oracle):
+    """All 256 rows of the benchmark batch, bit-exact."""
+    import workloads
+    w = workloads.make("c3")
+    _say("c3 B=256 V", w["V"])
+    tok, st, _ = run_batch(gpu, torch, w["logits"], params=w["params"], u=w["u"])
+    want = oracle.sample_batch(w["logits"], w["params"], w["u"], nthreads=16)
+    check_tokens("c3 B=256", tok, want, st)
+
+
+def _sweep_rows(rng, B, V, shape):
+    """Rows of several shapes: normal of various widths, a dominant maximum,
+    values on a coarse grid (many exactly equal logits), heavy tails."""
+    if shape == "normal":
+        sig = rng.choice([0.3, 1.0, 2.0, 4.0, 8.0], size=(B, 1)).astype(np.float32)
+        return (rng.standard_normal((B, V), dtype=np.float32) * sig).astype(np.float32)
+    if shape == "spike":
+        x = rng.standard_normal((B, V), dtype=np.float32) * 2.0
+        x[np.arange(B), rng.integers(0, V, B)] += rng.uniform(6, 14, B).astype(np.float32)
+        return x.astype(np.float32)
+    if shape == "grid":
+        return (np.round(rng.standard_normal((B, V)) * 4.0) / 2.0).astype(np.float32)
+    # heavy tail: Student-like via normal / sqrt(chi2)
+    z = rng.standard_normal((B, V))
+    c = rng.chisquare(3, size=(B, V))
+    return (z / np.sqrt(c / 3.0)).astype(np.float32)
+
+
+@pytest.mark.parametrize("V,shape", [(100, "normal"), (4099, "grid"), (50000, "normal"),
+                                     (50000, "spike"), (152064, "normal"), (152064, "grid"),
+                                     (152064, "heavy"), (262144, "normal")])
+def test_full_vocab_sweep(gpu, torch, oracle, V, shape):
+    """Heterogeneous rows through the full-vocabulary path (top_k = 0):
+    temperatures, top_p (including >= 1 and tiny), penalties with windows and
+    draws over [0, 1), against the oracle bit for bit."""
+    import workloads
+    rng = np.random.default_rng(V * 7 + len(shape))
+    B = 16
+    x = _sweep_rows(rng, B, V, shape)
+    rows = []
+    for b in range(B):
+        T = float(rng.choice([0.5, 1.0, 1.7]))
+        p = float(rng.choice([0.3, 0.9, 0.95, 0.999, 1.0]))
+        rep = float(rng.choice([1.0, 1.0, 1.2]))
+        rows.append((T, 0, p, rep))
+    params = np.array(rows, dtype=workloads.PARAMS_DTYPE)
+    W = 64
+    recent = rng.integers(0, V, size=(B, W), dtype=np.uint32)
+    u = rng.random(B, dtype=np.float32)
+    _say("sweep V", V, shape)
+    tok, st, _ = run_batch(gpu, torch, x, params=params, u=u, recent=recent)
+    want = oracle.sample_batch(x, params, u, recent=recent, nthreads=16)
+    check_tokens("sweep V=%d %s" % (V, shape), tok, want, st)
