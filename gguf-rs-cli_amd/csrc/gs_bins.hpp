@@ -1554,7 +1554,10 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     {
         // with indexed bins, only the elements of bins up to the last seq-3
         // bin are visited, through their indices; otherwise a pass over the row
-        bool gather = use_ix && bn.ixlast <= bn.ixlim;
+        // gathers win only for small regions: about one fifth of the row
+        // costs as much as a streaming pass
+        bool gather = use_ix && bn.ixlast <= bn.ixlim &&
+                      (bn.ixlast < 0 || bn.off[bn.ixlast + 1] - bn.off[0] <= (uint32_t)V / 5u);
         if (gather) {
             bool bad = false;
             for (int b = t; b <= bn.ixlim; b += kThreads) bad |= bn.icur[b] != bn.off[b + 1];
@@ -1573,7 +1576,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
                     atomicAdd(&bn.esum[c.b], c.k);
                 }
             };
-            constexpr int kG = 4;
+            constexpr int kG = 8;
             for (uint32_t p = p0 + t; p < p1; p += kThreads * kG) {
                 uint32_t id[kG];
                 float x[kG];

@@ -23,7 +23,8 @@ namespace gs {
 __device__ uint64_t g_stamp[32];
 __device__ int g_fails[1024];
 __device__ unsigned g_row;
-#define GS_STAMP(i) do { if (blockIdx.x == g_row && threadIdx.x == 0) g_stamp[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+__device__ uint32_t g_stages[256 * 32];   // per row: realtime at each stamp (mode 1)
+#define GS_STAMP(i) do { if (threadIdx.x == 0) { const uint64_t _t = __builtin_amdgcn_s_memrealtime(); if (blockIdx.x == g_row) g_stamp[i] = _t; if (blockIdx.x < 256 && (i) >= 8 && (i) < 24) g_stages[blockIdx.x * 32 + (i)] = (uint32_t)_t; } } while (0)
 #define GS_DIAG(i, v) do { if (blockIdx.x == g_row && threadIdx.x == 0) g_stamp[i] = (uint64_t)(v); } while (0)
 #define GS_SUB(i) do { if (blockIdx.x == g_row && threadIdx.x == 0 && g_fails[899] < 1) g_fails[900 + (i)] = (int)__builtin_amdgcn_s_memrealtime(); } while (0)
 #else
@@ -1023,6 +1024,10 @@ __global__ void synth_kernel(float *out, int B, int V, size_t ld, uint64_t seed,
 } // namespace gs
 
 #ifdef GS_TIMING
+extern "C" int gs_debug_stages(uint32_t *out)
+{
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_stages), sizeof(uint32_t) * 256 * 32) == hipSuccess ? 0 : -5;
+}
 extern "C" int gs_debug_stamps(uint64_t *out)
 {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_stamp), sizeof(uint64_t) * 32) == hipSuccess ? 0 : -5;

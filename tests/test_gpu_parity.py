@@ -296,3 +296,38 @@ def test_full_vocab_sweep(gpu, torch, oracle, V, shape):
     tok, st, _ = run_batch(gpu, torch, x, params=params, u=u, recent=recent)
     want = oracle.sample_batch(x, params, u, recent=recent, nthreads=16)
     check_tokens("sweep V=%d %s" % (V, shape), tok, want, st)
+
+
+def test_c5_hip_graph(gpu, torch, oracle):
+    """Config C5 as a captured HIP graph: every step (on-device logits, batched
+    sample, window push) recorded once, then replayed; each replay's token
+    trace and final window must equal the oracle's.  The LCG states of the
+    steps are fixed at capture, as the eager loop would draw them."""
+    import workloads
+    w = workloads.make("c5", B=4, steps=6)
+    B, V, W, steps = w["B"], w["V"], w["W"], w["steps"]
+    _say("c5 graph B", B, "steps", steps)
+    d_lg = torch.empty((B, V), dtype=torch.float32, device="cuda")
+    win0 = torch.from_numpy(w["window"].view(np.int32)).cuda()
+    d_win = win0.clone()
+    d_toks = torch.zeros((steps, B), dtype=torch.int32, device="cuda")
+    s = gpu.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=st):
+        for t in range(steps):
+            gpu.synth_logits(d_lg, w["synth_seed"], t * B * V, w["sigma"], stream=st)
+            s.sample_batch(d_lg, d_toks[t], recent=d_win, stream=st)
+            gpu.window_push(d_win, d_toks[t], t, stream=st)
+    u, _ = workloads.lcg_stream(w["seed"], steps * B)
+    want, win = oracle.device_loop(B, V, steps, w["synth_seed"], w["sigma"],
+                                   (w["T"], w["k"], w["p"], w["rep"]), w["window"], u, nthreads=4)
+    for rep in range(3):
+        d_win.copy_(win0)          # eager work between replays
+        d_toks.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        check_tokens("c5 graph replay %d" % rep, d_toks.cpu().numpy().astype(np.int64), want)
+        assert (d_win.cpu().numpy().view(np.uint32) == win).all()
