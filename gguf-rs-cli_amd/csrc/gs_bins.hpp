@@ -1402,7 +1402,8 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
                 }
                 bn.meta[b] = (mt & 0xff00u) | (mt & 0x78u) | (col ? 0x81u : 0u) | (k2 ? 2u : 0u) |
                              ((uint32_t)(b2 + 128) << 16) | (128u << 24);
-                if (k2) atomicMax(&bn.ixlim, b);
+                // index the bins that may precede the draw (seq 3)
+                if (k2 && plo_ / (0.5 * (s2lo + s2hi)) * dl <= (double)r) atomicMax(&bn.ixlim, b);
                 if (col) {
                     bn.cnt[b] = bn.off[b] | kNow;
                     atomicAdd(&bn.ncollect, 1);
@@ -1415,7 +1416,13 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
         }
         if (t == kThreads - 1) bn.pre_e[kBins] = (float)lo;
     }
-    if (t == 0) { bn.ndefer = 0; bn.ixlast = -1; }
+    __syncthreads();
+    if (t == 0) {
+        bn.ndefer = 0;
+        bn.ixlast = -1;
+        // a large region is cheaper as passes over the row than as gathers
+        if (bn.ixlim >= 0 && bn.off[bn.ixlim + 1] - bn.off[0] > (uint32_t)V / 5u) bn.ixlim = -1;
+    }
     __syncthreads();
     GS_STAMP(16);
 
