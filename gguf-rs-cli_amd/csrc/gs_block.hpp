@@ -124,6 +124,24 @@ __device__ __forceinline__ uint32_t wave_scan_add(uint32_t v)
     return v;
 }
 
+// Wave64 maximum / minimum of a u32, returned in every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    const int lane = lane_id(), rl = lane & 15;
+    uint32_t o;
+    o = dpp_mov<0x111>(v); if (rl >= 1) v = max(v, o);
+    o = dpp_mov<0x112>(v); if (rl >= 2) v = max(v, o);
+    o = dpp_mov<0x114>(v); if (rl >= 4) v = max(v, o);
+    o = dpp_mov<0x118>(v); if (rl >= 8) v = max(v, o);
+    o = dpp_mov<0x142>(v); if ((lane & 31) >= 16) v = max(v, o);
+    o = dpp_mov<0x143>(v); if (lane >= 32) v = max(v, o);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
+{
+    return ~wave_max_u32(~v);
+}
+
 // Integer increment of summand a at grid exponent e (capped at kSat), and
 // whether it is an exact rounding tie.
 __device__ __forceinline__ uint32_t elem_inc(float a, int e, bool *tie)

@@ -22,7 +22,7 @@ namespace gs {
 // Stage timestamps of row 0 (development builds only).
 __device__ uint64_t g_stamp[32];
 __device__ int g_fails[1024];
-__device__ unsigned g_row;
+__constant__ unsigned g_row;   // scalar loads: a stamp adds no memory wait
 __device__ uint32_t g_stages[256 * 32];   // per row: realtime at each stamp (mode 1)
 #define GS_STAMP(i) do { if (threadIdx.x == 0) { const uint64_t _t = __builtin_amdgcn_s_memrealtime(); if (blockIdx.x == g_row) g_stamp[i] = _t; if (blockIdx.x < 256 && (i) >= 8 && (i) < 24) g_stages[blockIdx.x * 32 + (i)] = (uint32_t)_t; } } while (0)
 #define GS_DIAG(i, v) do { if (blockIdx.x == g_row && threadIdx.x == 0) g_stamp[i] = (uint64_t)(v); } while (0)
@@ -37,15 +37,18 @@ constexpr int kHashSlots = 2 * kMaxWindow;     // open addressing, load <= 1/2
 constexpr int kHistBins = 4096;                 // 12-bit radix digits
 constexpr int kCandCap = 2048;                  // LDS candidate capacity
 constexpr uint32_t kEmpty = 0xffffffffu;
+constexpr int kPenBitsWords = 1024;             // bitmap of ids < 32768 (the register-resident rows)
 
 struct TopkSmem {
-    union {
+    union alignas(16) {
         uint32_t hist[kHistBins];
         uint32_t wcnt[kWaves * 256];            // radix sort: per-wave digit counts
         float ev[kHistBins];
     } u;
-    uint64_t cand[kCandCap];                    // (key << 32) | ~idx, sorted descending
+    alignas(16) uint64_t cand[kCandCap];        // (key << 32) | ~idx, sorted descending
     uint32_t base[256];
+    uint32_t hraw[kHashSlots];                  // raw logit of each penalized id (table build only)
+    uint32_t pbits[kPenBitsWords];              // penalized-id bitmap, ids < 32 * kPenBitsWords
 };
 
 struct RowSmem {
@@ -85,33 +88,54 @@ __device__ __forceinline__ int hash_find(const RowSmem &sm, uint32_t id)
     return -1;
 }
 
-// Build the penalty table for this row.  Returns the number of unique ids.
-__device__ void build_penalty(RowSmem &sm, const float *row, int V, const uint32_t *rec, int W,
-                              float T, float pen)
+// The recent window's loads, issued before the penalty table is built so
+// that both dependent loads overlap the row loads: thread j takes recent[j]
+// (W <= kMaxWindow == kThreads) and the raw logit of that id.  Ids outside
+// [0, V) are skipped, as logits.get_mut does at src/sampler.rs:26.
+struct PenLoad { uint32_t id; float raw; };
+static_assert(kMaxWindow <= kThreads, "one window entry per thread");
+__device__ __forceinline__ PenLoad pen_load(const float *row, int V, const uint32_t *rec, int W)
+{
+    PenLoad p{kEmpty, 0.0f};
+    const int t = threadIdx.x;
+    if (t < W) {
+        const uint32_t id = ldg(rec + t);
+        if (id < (uint32_t)V) { p.id = id; p.raw = ldg(row + id); }
+    }
+    return p;
+}
+
+// Build the penalty table for this row (src/sampler.rs:23-30): an LDS hash of
+// id -> penalized logit, the occurrence count applied one op at a time, and
+// a bitmap of the penalized ids below 32 * kPenBitsWords.  sm.nuniq receives
+// the number of distinct ids.
+__device__ void build_penalty(RowSmem &sm, PenLoad pl, float T, float pen)
 {
     const int t = threadIdx.x;
     for (int i = t; i < kHashSlots; i += kThreads) { sm.hkey[i] = kEmpty; sm.hval[i] = 0; }
+    for (int i = t; i < kPenBitsWords; i += kThreads) sm.x.tk.pbits[i] = 0u;
     if (t == 0) sm.nuniq = 0;
     __syncthreads();
-    for (int j = t; j < W; j += kThreads) {
-        uint32_t id = rec[j];
-        if ((int)id >= V || id == kEmpty) continue;   // src/sampler.rs:26 logits.get_mut
+    if (pl.id != kEmpty) {
+        const uint32_t id = pl.id;
         uint32_t h = hash_slot(id);
         for (;;) {
-            uint32_t prev = atomicCAS(&sm.hkey[h], kEmpty, id);
+            const uint32_t prev = atomicCAS(&sm.hkey[h], kEmpty, id);
             if (prev == kEmpty || prev == id) {
                 if (prev == kEmpty) atomicAdd(&sm.nuniq, 1);
                 atomicAdd(&sm.hval[h], 1u);
+                sm.x.tk.hraw[h] = __float_as_uint(pl.raw);   // every writer stores the same value
                 break;
             }
             h = (h + 1) & (kHashSlots - 1);
         }
+        if (id < 32u * kPenBitsWords) atomicOr(&sm.x.tk.pbits[id >> 5], 1u << (id & 31u));
     }
     __syncthreads();
     for (int i = t; i < kHashSlots; i += kThreads) {
-        uint32_t id = sm.hkey[i];
+        const uint32_t id = sm.hkey[i];
         if (id != kEmpty) {
-            float l = penalize(row[id], sm.hval[i], pen);
+            const float l = penalize(__uint_as_float(sm.x.tk.hraw[i]), sm.hval[i], pen);
             sm.hval[i] = __float_as_uint(l);
             if (isnan(l / T)) sm.flag_nan = 1;
         }
@@ -686,94 +710,199 @@ __device__ int topk_row_tmax(RowSmem &sm, const float *row, int V, int k, float 
     return finish_sorted(sm, k, yv, ix, top_p, r);
 }
 
-// topk_row_tmax for rows held in registers (V <= kThreads * 4 * kRegF4, V a
-// multiple of 4, 16-byte aligned): the caller loads the row once, before
-// the penalty table is built, and the candidates come from the registers
-// instead of a second read of the row.
+// Top-k for rows held in registers (V <= kThreads * 4 * kRegF4, V a multiple
+// of 4, 16-byte aligned).  The caller loads the row once, before the penalty
+// table is built.  The bound is the one of topk_row_tmax (the (k + U)-th
+// largest of the 1024 thread maxima), found with one histogram level over
+// the spread of the thread maxima: bin = (max key - key) >> shift, with the
+// shift that maps that spread onto kSelBins bins.  Every wave scans the
+// histogram itself, so the bound costs one barrier.  The candidates are
+// compacted per wave (one LDS atomic per wave), the penalized ids are left
+// out through the id bitmap and come back from the penalty table with their
+// penalized value, and a rank sort places only the first k.
 constexpr int kRegF4 = 8;
+constexpr int kSelBins = 2048;
+__device__ __forceinline__ float f4c(const float4 &v, int c)
+{
+    return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
+}
 __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int k, float T, float top_p,
                             bool has_pen, int nuniq, float r, int *status, bool *ok)
 {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int n4 = V >> 2;
     *ok = false;
     const uint32_t need = (uint32_t)k + (uint32_t)nuniq;
-    if (need > (uint32_t)kThreads) return 0;
-    float tmax = -INFINITY;
-    bool any = false;
-    int nan = 0;
-#pragma unroll
-    for (int u = 0; u < kRegF4; u++) {
-        if (u * kThreads + t < n4) {
-            const float xs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                nan |= (int)isnan(xs[c]) | ((int)isinf(xs[c]) & (int)isinf(T));
-                tmax = fmaxf(tmax, xs[c]);
-            }
-            any = true;
-        }
-    }
-    if (block_or(nan, sm)) { *ok = true; *status = GS_ERR_NAN; return 0; }
-    GS_STAMP(2);
-    const uint32_t tk = any ? f2key(tmax) : 0u;
-    uint32_t prefix = 0, above = 0;
-    for (int level = 0; level < 2; level++) {
-        const int sh = level == 0 ? 20 : 8;
-        for (int i = t; i < 4096; i += kThreads) sm.x.tk.u.hist[i] = 0;
-        __syncthreads();
-        if (level == 0 || (tk >> 20) == prefix) atomicAdd(&sm.x.tk.u.hist[(tk >> sh) & 4095u], 1u);
-        __syncthreads();
-        uint32_t b, ab;
-        select_bin(sm, 4096, need - above, &b, &ab);
-        above += ab;
-        prefix = level == 0 ? b : ((prefix << 12) | b);
-    }
-    const uint32_t tau = prefix << 8;   // >= need thread maxima have key >= tau
-    GS_STAMP(3);
+    const uint32_t nmax = (uint32_t)min(n4, kThreads);      // threads holding elements
+    if (need > nmax) return 0;
+    for (int i = t; i < kSelBins; i += kThreads) sm.x.tk.u.hist[i] = 0u;
     if (t == 0) sm.ncand = 0;
-    __syncthreads();
+    // Thread maximum and NaN test (slots past the row hold -inf).
+    float fmx = -INFINITY;
+    uint64_t nanm = 0;
 #pragma unroll
     for (int u = 0; u < kRegF4; u++) {
-        const int q = u * kThreads + t;
-        if (q < n4) {
-            const float xs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+        fmx = fmaxf(fmx, fmaxf(fmaxf(rv[u].x, rv[u].y), fmaxf(rv[u].z, rv[u].w)));
+        nanm |= __ballot(__builtin_isunordered(rv[u].x, rv[u].y));
+        nanm |= __ballot(__builtin_isunordered(rv[u].z, rv[u].w));
+    }
+    const bool holds = t < n4;
+    const uint32_t tk = f2key(fmx);
+    {
+        const uint32_t wmax = wave_max_u32(holds ? tk : 0u);
+        const uint32_t wmin = wave_min_u32(holds ? tk : 0xffffffffu);
+        if (lane == 0) { sm.red_u32[w] = wmax; sm.red_i32[w] = (int)wmin; sm.red_f32[w] = nanm ? 1.0f : 0.0f; }
+    }
+    __syncthreads();
+    uint32_t kmax = 0u, kmin = 0xffffffffu;
+    bool anynan = false;
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int i = 4 * q + c;
-                if (f2key(xs[c]) >= tau && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) {
-                    const int slot = atomicAdd(&sm.ncand, 1);
-                    if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(xs[c] / T), (uint32_t)i);
-                }
+    for (int i = 0; i < kWaves; i++) {
+        kmax = max(kmax, sm.red_u32[i]);
+        kmin = min(kmin, (uint32_t)sm.red_i32[i]);
+        anynan |= sm.red_f32[i] != 0.0f;
+    }
+    if (anynan) { *ok = true; *status = GS_ERR_NAN; return 0; }
+    GS_STAMP(2);
+    // Histogram of the thread maxima: bin = (kmax - key) >> shift.  Bin b
+    // is stored at ((b >> 2) & 7) * 256 + (b >> 5) * 4 + (b & 3), so that
+    // lane L's 32 consecutive bins are 8 uint4 at q * 256 + 4 * L: the
+    // scan below reads them without bank conflicts.
+    const uint32_t spread = kmax - kmin;
+    const int shift = spread < (uint32_t)kSelBins ? 0 : (32 - __clz((int)spread)) - 11;
+    if (holds) {
+        const uint32_t bin = (kmax - tk) >> shift;
+        atomicAdd(&sm.x.tk.u.hist[((bin >> 2) & 7u) * 256u + (bin >> 5) * 4u + (bin & 3u)], 1u);
+    }
+    __syncthreads();
+    // Bin of the need-th largest thread maximum, scanned by every wave.
+    uint32_t sel;
+    {
+        const uint4 *h4 = reinterpret_cast<const uint4 *>(sm.x.tk.u.hist) + lane;
+        uint32_t hv[kSelBins / 64];
+#pragma unroll
+        for (int q = 0; q < kSelBins / 256; q++) {
+            const uint4 v = h4[q * 64];
+            hv[4 * q] = v.x; hv[4 * q + 1] = v.y; hv[4 * q + 2] = v.z; hv[4 * q + 3] = v.w;
+        }
+        uint32_t mine = 0u;
+#pragma unroll
+        for (int q = 0; q < kSelBins / 64; q++) mine += hv[q];
+        const uint32_t incl = wave_scan_add(mine);
+        const uint32_t excl = incl - mine;
+        const uint64_t hit = __ballot(excl < need && incl >= need);
+        const int L = (int)__builtin_ctzll(hit);            // exists: need <= nmax = total
+        uint32_t c = excl, b = 0u;
+        bool found = false;
+#pragma unroll
+        for (int q = 0; q < kSelBins / 64; q++) {
+            c += hv[q];
+            if (!found && c >= need) { b = (uint32_t)q; found = true; }
+        }
+        sel = (uint32_t)L * (kSelBins / 64) + (uint32_t)__builtin_amdgcn_readlane((int)b, L);
+    }
+    // Keys >= tau are exactly those whose bin is <= sel; at least `need`
+    // thread maxima are among them.  tf is the same bound as a float
+    // (x >= tf <=> f2key(x) >= tau for every non-NaN x).  A bound at -inf
+    // (too few finite logits) is left to the general path.
+    const uint64_t span = ((uint64_t)(sel + 1u) << shift) - 1u;
+    const uint32_t tau = span >= kmax ? 0u : kmax - (uint32_t)span;
+    if (tau <= f2key(-INFINITY)) { __syncthreads(); return 0; }
+    const float tf = key2f(tau);
+    GS_STAMP(3);
+    // Candidates: a counting pass (one compare per element, counts in
+    // scalar registers), one LDS reservation per wave, then the writes in
+    // the same order.  Entries hold the raw (value, id); the penalty bitmap
+    // and the division by T are applied afterwards, one candidate per thread.
+    uint32_t wcnt = 0u;
+#pragma unroll
+    for (int u = 0; u < kRegF4; u++) {
+        wcnt += (uint32_t)__popcll(__ballot(rv[u].x >= tf));
+        wcnt += (uint32_t)__popcll(__ballot(rv[u].y >= tf));
+        wcnt += (uint32_t)__popcll(__ballot(rv[u].z >= tf));
+        wcnt += (uint32_t)__popcll(__ballot(rv[u].w >= tf));
+    }
+    uint32_t wpos = 0u;
+    if (lane == 0 && wcnt) wpos = atomicAdd((uint32_t *)&sm.ncand, wcnt);
+    wpos = (uint32_t)__builtin_amdgcn_readfirstlane((int)wpos);
+#pragma unroll
+    for (int u = 0; u < kRegF4; u++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float x = f4c(rv[u], c);
+            const uint64_t m = __ballot(x >= tf);
+            if (m) {
+                const uint32_t pos = wpos + (uint32_t)__popcll(m & lanemask_lt());
+                if (x >= tf && pos < (uint32_t)kCandCap)
+                    sm.x.tk.cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(4 * (u * kThreads + t) + c);
+                wpos += (uint32_t)__popcll(m);
             }
         }
     }
+    constexpr uint32_t kPenFlag = 0x80000000u;   // entry holds an already penalized value
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {
             const uint32_t id = sm.hkey[s];
             if (id == kEmpty) continue;
-            const float x = __uint_as_float(sm.hval[s]);
-            if (f2key(x) >= tau) {
+            const uint32_t xb = sm.hval[s];
+            if (f2key(__uint_as_float(xb)) >= tau) {
                 const int slot = atomicAdd(&sm.ncand, 1);
-                if (slot < kCandCap) sm.x.tk.cand[slot] = cand_of(f2key(x / T), id);
+                if (slot < kCandCap) sm.x.tk.cand[slot] = ((uint64_t)xb << 32) | (id | kPenFlag);
             }
         }
     }
     __syncthreads();
     GS_STAMP(4);
     const int nc = sm.ncand;
+    if (nc > kCandCap || nc < k) { __syncthreads(); return 0; }   // the fallback reuses the LDS
+    // Raw entries -> (key of y, ~id); a penalized id found in the row is
+    // dropped (key 0 sorts last), its table entry stands for it.
+    for (int i = t; i < nc; i += kThreads) {
+        const uint64_t e = sm.x.tk.cand[i];
+        const float x = __uint_as_float((uint32_t)(e >> 32));
+        const uint32_t tag = (uint32_t)e;
+        const uint32_t id = tag & ~kPenFlag;
+        const bool drop = has_pen && !(tag & kPenFlag) && ((sm.x.tk.pbits[id >> 5] >> (id & 31u)) & 1u);
+        sm.x.tk.cand[i] = drop ? (uint64_t)(~id) : cand_of(f2key(x / T), id);
+    }
+    for (int i = nc + t; i < ((nc + 7) & ~7); i += kThreads) sm.x.tk.cand[i] = 0ull;   // pad: never larger
     __syncthreads();
-    if (nc > kCandCap || nc < k) return 0;
-    sort_cand_desc(sm, nc);
+    // Rank sort (keys unique), G threads per candidate, 8 entries per step
+    // (four 16-byte LDS reads in flight); only the first k are placed.
+    uint64_t *top = reinterpret_cast<uint64_t *>(sm.x.tk.u.hist);   // 2048 u64
+    {
+        const int nc8 = (nc + 7) >> 3;                 // steps of 8 (padding entries are 0)
+        const int lg = nc <= kThreads / 4 ? 2 : (nc <= kThreads / 2 ? 1 : 0);
+        const int G = 1 << lg;
+        const int len = (nc8 + G - 1) >> lg;           // steps per thread
+        for (int base = 0; base < (nc << lg); base += kThreads) {
+            const int gi = base + t;
+            const int i = gi >> lg, part = gi & (G - 1);
+            const bool act = i < nc;
+            const uint64_t me = act ? sm.x.tk.cand[i] : ~0ull;
+            const int s0 = part * len, s1 = min(nc8, s0 + len);
+            const ulonglong2 *c2 = reinterpret_cast<const ulonglong2 *>(sm.x.tk.cand);
+            int rk = 0;
+            for (int st = s0; st < s1; st++) {
+                const ulonglong2 a0 = c2[4 * st], a1 = c2[4 * st + 1], a2 = c2[4 * st + 2], a3 = c2[4 * st + 3];
+                rk += (a0.x > me) + (a0.y > me) + (a1.x > me) + (a1.y > me) +
+                      (a2.x > me) + (a2.y > me) + (a3.x > me) + (a3.y > me);
+            }
+            if (lg >= 1) rk += __shfl_xor(rk, 1, 64);
+            if (lg >= 2) rk += __shfl_xor(rk, 2, 64);
+            if (act && part == 0 && rk < k) top[rk] = me;
+        }
+    }
+    __syncthreads();
     GS_STAMP(5);
-    if (tau > 0x007fffffu) {
-        const float y_out = key2f(tau - 1u) / T;
-        const uint32_t yk = (uint32_t)(sm.x.tk.cand[k - 1] >> 32);
-        if (!(f2key(y_out) < yk)) return 0;
+    {
+        const uint32_t yk = (uint32_t)(top[k - 1] >> 32);   // 0: fewer than k kept
+        const bool bad = yk == 0u || (tau > 0x007fffffu && !(f2key(key2f(tau - 1u) / T) < yk));
+        if (bad) { __syncthreads(); return 0; }
     }
     *ok = true;
-    auto yv = [&](int j) { return key2f((uint32_t)(sm.x.tk.cand[j] >> 32)); };
-    auto ix = [&](int j) { return ~(uint32_t)sm.x.tk.cand[j]; };
+    auto yv = [&](int j) { return key2f((uint32_t)(top[j] >> 32)); };
+    auto ix = [&](int j) { return ~(uint32_t)top[j]; };
     *status = GS_OK;
     return finish_sorted(sm, k, yv, ix, top_p, r);
 }
@@ -921,7 +1050,8 @@ sample_rows_kernel(RowArgs a)
     // Small top-k rows that fit in registers: issue the row loads before the
     // penalty table is built, so the two overlap.
     const int keep0 = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
-    const bool regpath = MODE == kModeSmall && p.temperature > 0.0f && V > 1 && (V & 3) == 0 &&
+    const bool regpath = MODE == kModeSmall && p.temperature > 0.0f && p.temperature < INFINITY &&
+                         V > 1 && (V & 3) == 0 &&
                          V <= kThreads * 4 * kRegF4 && keep0 < V &&
                          ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
     float4 rv[kRegF4];
@@ -930,10 +1060,13 @@ sample_rows_kernel(RowArgs a)
         const int n4 = V >> 2;
 #pragma unroll
         for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+#pragma unroll
+        for (int u = 0; u < kRegF4; u++)   // slots past the row: -inf, below every bound used
+            if (u * kThreads + t >= n4) rv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     }
+    const PenLoad pl = has_pen ? pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W) : PenLoad{kEmpty, 0.0f};
     __syncthreads();
-    if (has_pen) build_penalty(sm, row, V, a.recent + (size_t)b * a.ld_recent, W,
-                               p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
+    if (has_pen) build_penalty(sm, pl, p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
     GS_STAMP(8 * MODE + 1);
 
     // The uniform draw for this row (only consumed if T > 0).
@@ -960,8 +1093,19 @@ sample_rows_kernel(RowArgs a)
             status = GS_ERR_NAN;
         } else {
             bool ok;
-            if (regpath)
-                tok = topk_row_reg(sm, rv, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r, &status, &ok);
+            if (regpath) {
+#ifdef GS_TIMING
+                // development builds: the same code runs twice, the second time warm
+                const int reps = a.done ? 1 : 2;
+#else
+                const int reps = 1;
+#endif
+#pragma nounroll
+                for (int rep = 0; rep < reps; rep++) {
+                    tok = topk_row_reg(sm, rv, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r, &status, &ok);
+                    if (rep + 1 < reps) GS_STAMP(6);
+                }
+            }
             else
                 tok = topk_row_tmax(sm, row, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r,
                                     aligned, &status, &ok);

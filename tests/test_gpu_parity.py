@@ -187,7 +187,7 @@ def test_edge_cases(gpu, torch, oracle):
     cases.append(("signed_zeros", xz, (1.0, 0, 0.97, 1.0)))
     x = (rng.standard_normal(V) * 30).astype(np.float32)
     cases.append(("peaked_k0", x, (1.0, 0, 0.9, 1.0)))
-    rec = np.concatenate([rng.integers(0, V, 60), [0, 0, 0, V + 5, 2 ** 32 - 1]]).astype(np.uint32)
+    rec = np.concatenate([rng.integers(0, V, 60), [0, 0, 0, V + 5, 2 ** 31, 2 ** 32 - 1]]).astype(np.uint32)
     for name, x, (T, k, p, rep) in cases:
         for u in (0.0, 0.37, 0.9999):
             _say("edge", name, "u", u)
@@ -196,6 +196,57 @@ def test_edge_cases(gpu, torch, oracle):
             want = oracle.sample(x, T, k, p, rep, rec, r=u)
             assert st[0] == 0, (name, st[0])
             assert tok[0] == want, (name, u, tok[0], want)
+
+
+@pytest.mark.parametrize("V", [32000, 32768, 4096, 1000, 8])
+def test_topk_register_rows(gpu, torch, oracle, V):
+    """Top-k rows held in registers (V <= 32768): penalties with rep below and
+    above 1 (the penalized ids include the largest logits), windows up to the
+    maximum, ids outside [0, V), ties, masked rows and k up to kMaxTopK."""
+    import workloads
+    rng = np.random.default_rng(V)
+    W = 1024
+    rows, prm, recs = [], [], []
+    for case in range(24):
+        kind = case % 6
+        if kind == 0:
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+        elif kind == 1:
+            x = (rng.integers(-4, 4, V) / 4).astype(np.float32)
+        elif kind == 2:
+            x = np.full(V, -np.inf, np.float32)
+            x[rng.choice(V, min(V, 50), replace=False)] = rng.standard_normal(min(V, 50))
+        elif kind == 3:
+            x = np.zeros(V, np.float32)
+        elif kind == 4:
+            x = (rng.standard_normal(V) * 0.01 + 5).astype(np.float32)
+        else:
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+            x[rng.choice(V, min(V, 5), replace=False)] += 10
+        top = np.argsort(-x, kind="stable")[:16].astype(np.uint32)
+        nrec = [0, 64, 1024, 300][case % 4]
+        rec = np.full(W, 2 ** 32 - 1, np.uint32)
+        body = np.concatenate([top, rng.integers(0, V, W).astype(np.uint32)])[:nrec]
+        rec[:nrec] = body
+        if nrec:
+            rec[:3] = [V, 2 ** 31, 2 ** 31 + 7]
+        k = [1, 2, 40, 100, 1000, 1024][case % 6]
+        k = min(k, V - 1) if V > 1 else 1
+        rep = [1.3, 0.7, 1.0, 1.1][(case // 6) % 4]
+        T = [0.7, 1.0, 2.5, 0.3][case % 4]
+        p = [0.9, 0.5, 1.0, 0.99][(case // 3) % 4]
+        rows.append(x)
+        prm.append((T, k, p, rep))
+        recs.append(rec)
+    x = np.stack(rows)
+    pr = workloads.params_rows(prm)
+    rec = np.stack(recs)
+    for u0 in (0.0, 0.41, 0.9999):
+        u = np.full(len(rows), u0, np.float32)
+        _say("topk_register V", V, "u", u0)
+        tok, st, _ = run_batch(gpu, torch, x, params=pr, u=u, recent=rec)
+        want = oracle.sample_batch(x, pr, u, recent=rec)
+        check_tokens("topk_reg V%d u%.2f" % (V, u0), tok, want, st)
 
 
 def test_errors(gpu, torch):
