@@ -23,10 +23,10 @@ struct gs_sampler {
     size_t rec_cap;
     uint32_t *h_tok;             // pinned, mapped, coherent: kernel writes the token here
     int32_t *h_status;
-    uint32_t *h_done;            // completion flag of single-row calls (sequence number)
+    uint64_t *h_done;            // single-row calls: (sequence << 32) | (status & 0xff) << 24 | token
     uint32_t *d_tok_map;         // device aliases of h_tok / h_status / h_done
     int32_t *d_status_map;
-    uint32_t *d_done_map;
+    uint64_t *d_done_map;
     uint32_t seq;
     const char *dev_lo, *dev_hi; // last device allocation seen by is_device_ptr
     uint32_t *scratch;           // full-vocabulary path
@@ -112,9 +112,9 @@ int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out)
     }
     s->h_status = (int32_t *)(s->h_tok + 4);
     s->d_status_map = (int32_t *)(s->d_tok_map + 4);
-    s->h_done = s->h_tok + 8;
-    s->d_done_map = s->d_tok_map + 8;
-    *(volatile uint32_t *)s->h_done = 0u;
+    s->h_done = reinterpret_cast<uint64_t *>(s->h_tok + 8);        // 32 bytes in: 8-byte aligned
+    s->d_done_map = reinterpret_cast<uint64_t *>(s->d_tok_map + 8);
+    *(volatile uint64_t *)s->h_done = 0u;
     *out = s;
     return GS_OK;
 }
@@ -227,19 +227,31 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
         a.done_val = seq;
     }
     if (gs::launch_sample_rows(a, 1, !full, full, s->stream) != hipSuccess) return GS_ERR_HIP;
-    bool synced = full;
-    if (!full) {
-        volatile uint32_t *f = s->h_done;
-        for (uint32_t spins = 0; *f != seq; spins++) {
-            if (spins > (1u << 22)) { synced = true; break; }   // slow call: fall back to the runtime
+    int st;
+    uint32_t tok;
+    if (full) {
+        if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
+        st = *(volatile int32_t *)s->h_status;
+        tok = *(volatile uint32_t *)s->h_tok;
+    } else {
+        volatile uint64_t *f = s->h_done;
+        uint64_t w = *f;
+        for (uint32_t spins = 0; (uint32_t)(w >> 32) != seq; spins++) {
+            if (spins > (1u << 22)) {           // slow call: wait through the runtime
+                if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
+                w = *f;
+                if ((uint32_t)(w >> 32) != seq) return GS_ERR_HIP;
+                break;
+            }
             __builtin_ia32_pause();
+            w = *f;
         }
+        st = (int)(int8_t)(uint8_t)(w >> 24);
+        tok = (uint32_t)w & 0xffffffu;
     }
-    if (synced && hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
     if (s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, 1);   // one draw iff T > 0
-    int st = *(volatile int32_t *)s->h_status;
     if (st != GS_OK) return st;
-    *out_token = *(volatile uint32_t *)s->h_tok;
+    *out_token = tok;
     return GS_OK;
 }
 

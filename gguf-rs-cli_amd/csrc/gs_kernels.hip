@@ -21,16 +21,18 @@ namespace gs {
 #ifdef GS_TIMING
 // Stage timestamps of row 0 (development builds only).
 __device__ uint64_t g_stamp[32];
-__device__ int g_fails[1024];
+__device__ int g_fails[1280];
 __constant__ unsigned g_row;   // scalar loads: a stamp adds no memory wait
 __device__ uint32_t g_stages[256 * 32];   // per row: realtime at each stamp (mode 1)
 #define GS_STAMP(i) do { if (threadIdx.x == 0) { const uint64_t _t = __builtin_amdgcn_s_memrealtime(); if (blockIdx.x == g_row) g_stamp[i] = _t; if (blockIdx.x < 256 && (i) >= 8 && (i) < 24) g_stages[blockIdx.x * 32 + (i)] = (uint32_t)_t; } } while (0)
 #define GS_DIAG(i, v) do { if (blockIdx.x == g_row && threadIdx.x == 0) g_stamp[i] = (uint64_t)(v); } while (0)
+#define GS_SUB0(i) do { if (threadIdx.x == 0 && blockIdx.x == g_row) g_stamp[16 + (i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #define GS_SUB(i) do { if (blockIdx.x == g_row && threadIdx.x == 0 && g_fails[899] < 1) g_fails[900 + (i)] = (int)__builtin_amdgcn_s_memrealtime(); } while (0)
 #else
 #define GS_STAMP(i) do { } while (0)
 #define GS_DIAG(i, v) do { } while (0)
 #define GS_SUB(i) do { } while (0)
+#define GS_SUB0(i) do { } while (0)
 #endif
 
 constexpr int kHashSlots = 2 * kMaxWindow;     // open addressing, load <= 1/2
@@ -361,6 +363,7 @@ __device__ int finish_sorted(RowSmem &sm, int n, YV yv, IX idx, float top_p, flo
             int tk = finish_wave(n, yv, idx, top_p, r);
             if (lane_id() == 0) sm.tok = tk;
         }
+        GS_SUB0(6);
         __syncthreads();
         const int tk = sm.tok;
         __syncthreads();
@@ -726,18 +729,48 @@ __device__ __forceinline__ float f4c(const float4 &v, int c)
 {
     return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
 }
-__device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int k, float T, float top_p,
-                            bool has_pen, int nuniq, float r, int *status, bool *ok)
+// LDS state of topk_row_reg, cleared before the kernel's first barrier.
+__device__ __forceinline__ void reg_clear(RowSmem &sm, bool has_pen)
+{
+    const int t = threadIdx.x;
+    if (has_pen) {
+        for (int i = t; i < kHashSlots; i += kThreads) { sm.hkey[i] = kEmpty; sm.hval[i] = 0u; }
+        for (int i = t; i < kPenBitsWords; i += kThreads) sm.x.tk.pbits[i] = 0u;
+    }
+    for (int i = t; i < kSelBins; i += kThreads) sm.x.tk.u.hist[i] = 0u;
+    if (t == 0) sm.ncand = 0;
+}
+
+__device__ int topk_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
+                            float top_p, bool has_pen, float pen, float r, int *status, bool *ok)
 {
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int n4 = V >> 2;
     *ok = false;
-    const uint32_t need = (uint32_t)k + (uint32_t)nuniq;
-    const uint32_t nmax = (uint32_t)min(n4, kThreads);      // threads holding elements
-    if (need > nmax) return 0;
-    for (int i = t; i < kSelBins; i += kThreads) sm.x.tk.u.hist[i] = 0u;
-    if (t == 0) sm.ncand = 0;
-    // Thread maximum and NaN test (slots past the row hold -inf).
+    // Penalty table (src/sampler.rs:23-30), built alongside the row pass:
+    // the ids go in now, the thread that created a slot stores the
+    // penalized value after the next barrier, when the count is complete.
+    int myslot = -1;
+    if (has_pen && pl.id != kEmpty) {
+        uint32_t h = hash_slot(pl.id);
+        for (;;) {
+            const uint32_t prev = atomicCAS(&sm.hkey[h], kEmpty, pl.id);
+            if (prev == kEmpty || prev == pl.id) {
+                if (prev == kEmpty) { atomicAdd(&sm.nuniq, 1); myslot = (int)h; }
+                atomicAdd(&sm.hval[h], 1u);
+                break;
+            }
+            h = (h + 1) & (kHashSlots - 1);
+        }
+        atomicOr(&sm.x.tk.pbits[pl.id >> 5], 1u << (pl.id & 31u));   // V <= 32768: every id has a bit
+    }
+    // Slots past the row (clamped loads) become -inf, below every bound
+    // used.  Done here, after the table inserts: overwriting a register that
+    // a load is still filling waits for that load.
+#pragma unroll
+    for (int u = 0; u < kRegF4; u++)
+        if (u * kThreads + t >= n4) rv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    // Thread maximum and NaN test.
     float fmx = -INFINITY;
     uint64_t nanm = 0;
 #pragma unroll
@@ -762,6 +795,35 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
         kmin = min(kmin, (uint32_t)sm.red_i32[i]);
         anynan |= sm.red_f32[i] != 0.0f;
     }
+    if (myslot >= 0) {
+        const float l = penalize(pl.raw, sm.hval[myslot], pen);
+        sm.hval[myslot] = __float_as_uint(l);
+        if (isnan(l / T)) sm.flag_nan = 1;
+    }
+    // The bitmap is complete: a thread holding a penalized element takes
+    // its maximum over the others, so the 1024 thread maxima are distinct
+    // unpenalized elements and k of them bound the k-th largest.
+    uint32_t tku = tk;
+    if (has_pen) {
+        uint32_t nib[kRegF4], anyp = 0u;
+#pragma unroll
+        for (int u = 0; u < kRegF4; u++) {
+            const int q = u * kThreads + t;
+            nib[u] = q < n4 ? (sm.x.tk.pbits[q >> 3] >> ((q & 7) * 4)) & 15u : 0u;
+            anyp |= nib[u];
+        }
+        if (__builtin_expect(anyp != 0u, 0)) {
+            float f = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < kRegF4; u++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if (!((nib[u] >> c) & 1u)) f = fmaxf(f, f4c(rv[u], c));
+            tku = f2key(f);
+        }
+    }
+    const uint32_t need = (uint32_t)k;
+    const uint32_t nmax = (uint32_t)min(n4, kThreads);      // threads holding elements
     if (anynan) { *ok = true; *status = GS_ERR_NAN; return 0; }
     GS_STAMP(2);
     // Histogram of the thread maxima: bin = (kmax - key) >> shift.  Bin b
@@ -771,10 +833,14 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
     const uint32_t spread = kmax - kmin;
     const int shift = spread < (uint32_t)kSelBins ? 0 : (32 - __clz((int)spread)) - 11;
     if (holds) {
-        const uint32_t bin = (kmax - tk) >> shift;
+        const uint32_t bin = min((kmax - tku) >> shift, (uint32_t)kSelBins - 1u);
         atomicAdd(&sm.x.tk.u.hist[((bin >> 2) & 7u) * 256u + (bin >> 5) * 4u + (bin & 3u)], 1u);
     }
     __syncthreads();
+    // The table holds penalized values from here on (also for the general
+    // paths the caller falls back to).
+    if (sm.flag_nan) { *ok = true; *status = GS_ERR_NAN; return 0; }
+    if (need > nmax) return 0;
     // Bin of the need-th largest thread maximum, scanned by every wave.
     uint32_t sel;
     {
@@ -792,12 +858,13 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
         const uint32_t excl = incl - mine;
         const uint64_t hit = __ballot(excl < need && incl >= need);
         const int L = (int)__builtin_ctzll(hit);            // exists: need <= nmax = total
+        // In lane L: the first bin whose running count reaches need (the
+        // running count is monotone, so it is the number of prefixes below).
         uint32_t c = excl, b = 0u;
-        bool found = false;
 #pragma unroll
-        for (int q = 0; q < kSelBins / 64; q++) {
+        for (int q = 0; q < kSelBins / 64 - 1; q++) {
             c += hv[q];
-            if (!found && c >= need) { b = (uint32_t)q; found = true; }
+            b += c < need ? 1u : 0u;
         }
         sel = (uint32_t)L * (kSelBins / 64) + (uint32_t)__builtin_amdgcn_readlane((int)b, L);
     }
@@ -822,6 +889,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
         wcnt += (uint32_t)__popcll(__ballot(rv[u].z >= tf));
         wcnt += (uint32_t)__popcll(__ballot(rv[u].w >= tf));
     }
+    GS_SUB0(0);
     uint32_t wpos = 0u;
     if (lane == 0 && wcnt) wpos = atomicAdd((uint32_t *)&sm.ncand, wcnt);
     wpos = (uint32_t)__builtin_amdgcn_readfirstlane((int)wpos);
@@ -831,7 +899,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
         for (int c = 0; c < 4; c++) {
             const float x = f4c(rv[u], c);
             const uint64_t m = __ballot(x >= tf);
-            if (m) {
+            if (__builtin_expect(m != 0, 0)) {   // rare: the common path falls through
                 const uint32_t pos = wpos + (uint32_t)__popcll(m & lanemask_lt());
                 if (x >= tf && pos < (uint32_t)kCandCap)
                     sm.x.tk.cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(4 * (u * kThreads + t) + c);
@@ -839,6 +907,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
             }
         }
     }
+    GS_SUB0(1);
     constexpr uint32_t kPenFlag = 0x80000000u;   // entry holds an already penalized value
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {
@@ -851,6 +920,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
             }
         }
     }
+    GS_SUB0(2);
     __syncthreads();
     GS_STAMP(4);
     const int nc = sm.ncand;
@@ -866,7 +936,9 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
         sm.x.tk.cand[i] = drop ? (uint64_t)(~id) : cand_of(f2key(x / T), id);
     }
     for (int i = nc + t; i < ((nc + 7) & ~7); i += kThreads) sm.x.tk.cand[i] = 0ull;   // pad: never larger
+    GS_SUB0(3);
     __syncthreads();
+    GS_SUB0(4);
     // Rank sort (keys unique), G threads per candidate, 8 entries per step
     // (four 16-byte LDS reads in flight); only the first k are placed.
     uint64_t *top = reinterpret_cast<uint64_t *>(sm.x.tk.u.hist);   // 2048 u64
@@ -893,6 +965,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float4 (&rv)[kRegF4], int V, int 
             if (act && part == 0 && rk < k) top[rk] = me;
         }
     }
+    GS_SUB0(5);
     __syncthreads();
     GS_STAMP(5);
     {
@@ -1035,6 +1108,8 @@ sample_rows_kernel(RowArgs a)
     if (MODE == kModeSort && a.fb != nullptr && a.fb[b] == 0) return;
     GS_STAMP(8 * MODE);
 #ifdef GS_TIMING
+    if (MODE == kModeSmall && blockIdx.x == g_row && (threadIdx.x & 63) == 0)
+        g_fails[1100 + (threadIdx.x >> 6)] = (int)__builtin_amdgcn_s_memrealtime();
     const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
 #endif
     const float *row = a.logits + (size_t)b * a.ld;
@@ -1060,13 +1135,11 @@ sample_rows_kernel(RowArgs a)
         const int n4 = V >> 2;
 #pragma unroll
         for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
-#pragma unroll
-        for (int u = 0; u < kRegF4; u++)   // slots past the row: -inf, below every bound used
-            if (u * kThreads + t >= n4) rv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     }
     const PenLoad pl = has_pen ? pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W) : PenLoad{kEmpty, 0.0f};
+    if (regpath) reg_clear(sm, has_pen);   // the register path builds its penalty table itself
     __syncthreads();
-    if (has_pen) build_penalty(sm, pl, p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
+    if (has_pen && !regpath) build_penalty(sm, pl, p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
     GS_STAMP(8 * MODE + 1);
 
     // The uniform draw for this row (only consumed if T > 0).
@@ -1093,19 +1166,9 @@ sample_rows_kernel(RowArgs a)
             status = GS_ERR_NAN;
         } else {
             bool ok;
-            if (regpath) {
-#ifdef GS_TIMING
-                // development builds: the same code runs twice, the second time warm
-                const int reps = a.done ? 1 : 2;
-#else
-                const int reps = 1;
-#endif
-#pragma nounroll
-                for (int rep = 0; rep < reps; rep++) {
-                    tok = topk_row_reg(sm, rv, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r, &status, &ok);
-                    if (rep + 1 < reps) GS_STAMP(6);
-                }
-            }
+            if (regpath)
+                tok = topk_row_reg(sm, rv, pl, V, keep, p.temperature, p.top_p, has_pen, p.rep_penalty, r,
+                                   &status, &ok);
             else
                 tok = topk_row_tmax(sm, row, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r,
                                     aligned, &status, &ok);
@@ -1140,11 +1203,15 @@ sample_rows_kernel(RowArgs a)
     if (t == 0 && b < 256 && MODE == kModeBins) g_fails[256 + b] = (int)(__builtin_amdgcn_s_memrealtime() - t_begin);
 #endif
     if (t == 0) {
-        a.tokens[b] = (uint32_t)tok;
-        if (a.status) a.status[b] = status;
         if (a.done) {
-            __threadfence_system();           // token and status before the flag
-            __hip_atomic_store(a.done, a.done_val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            // Token, status and the call's sequence number in one 64-bit
+            // store: the host sees all three or none, so no fence is needed.
+            const uint64_t word = ((uint64_t)a.done_val << 32) | ((uint64_t)((uint32_t)status & 0xffu) << 24) |
+                                  (uint64_t)((uint32_t)tok & 0xffffffu);
+            __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else {
+            a.tokens[b] = (uint32_t)tok;
+            if (a.status) a.status[b] = status;
         }
     }
 }
@@ -1178,7 +1245,7 @@ extern "C" int gs_debug_stamps(uint64_t *out)
 }
 extern "C" int gs_debug_fails(int *out)
 {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_fails), sizeof(int) * 1024) == hipSuccess ? 0 : -5;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_fails), sizeof(int) * 1280) == hipSuccess ? 0 : -5;
 }
 extern "C" int gs_debug_row(unsigned row)
 {

@@ -26,8 +26,9 @@ struct RowArgs {
     int32_t *fb;                   // per row: 1 = binned path failed, use the sort path
     uint32_t *scratch;             // full-vocabulary path: 4*V u32 per row
     size_t scratch_stride;         // u32 elements per row
-    uint32_t *done;                // optional (single-row calls): set to done_val after the
-    uint32_t done_val;             // token, with a system-scope fence, for host polling
+    uint64_t *done;                // optional (single-row calls, B = 1): receives
+    uint32_t done_val;             // (done_val << 32) | (status & 0xff) << 24 | token in one store,
+                                   // instead of tokens/status, for host polling
 };
 
 // Per-row scratch (u32 units) of the full-vocabulary paths: the sort path

@@ -110,6 +110,30 @@ def _ptr(x):
     raise TypeError("unsupported buffer type %r" % type(x))
 
 
+_TORCH = None
+
+
+def _torch_fast_args(logits, recent):
+    """(ptr, V, recent ptr, W) for a contiguous torch f32 row and a torch
+    window of 4-byte ids (or None / empty); None for anything else."""
+    global _TORCH
+    if _TORCH is None:
+        import sys
+        t = sys.modules.get("torch")
+        if t is None:
+            return None
+        _TORCH = (t.Tensor, t.float32, (t.int32, t.uint32))
+    tensor, f32, ids = _TORCH
+    if type(logits) is not tensor or logits.dtype is not f32 or not logits.is_contiguous():
+        return None
+    if recent is None or (type(recent) is tuple and not recent):
+        return logits.data_ptr(), logits.numel(), None, 0
+    if type(recent) is not tensor or recent.dtype not in ids or not recent.is_contiguous():
+        return None
+    W = recent.numel()
+    return logits.data_ptr(), logits.numel(), (recent.data_ptr() if W else None), W
+
+
 def _stream_handle(stream):
     if stream is None:
         return None
@@ -127,6 +151,8 @@ class Sampler:
         self._lib = load_library()
         self._h = ctypes.c_void_p()
         self.params = GsParams(temperature, top_k, top_p, rep_penalty)
+        self._out = ctypes.c_uint32()
+        self._outref = ctypes.byref(self._out)
         _check(self._lib.gs_sampler_create(ctypes.byref(self.params), seed, ctypes.byref(self._h)),
                "gs_sampler_create")
 
@@ -164,6 +190,12 @@ class Sampler:
     def sample(self, logits, recent=()):
         """sample(logits, recent) -> token; logits: numpy f32 (host) or a
         torch f32 tensor (host or device).  Synchronous."""
+        fast = _torch_fast_args(logits, recent)
+        if fast is not None:
+            rc = self._lib.gs_sample(self._h, fast[0], fast[1], fast[2], fast[3], self._outref)
+            if rc != GS_OK:
+                raise SamplerError(rc, "gs_sample")
+            return self._out.value
         import numpy as np
         keep = []
         if isinstance(logits, (list, tuple)):
@@ -178,7 +210,11 @@ class Sampler:
         V = int(logits.numel() if hasattr(logits, "numel") else logits.size)
         if recent is None or (not hasattr(recent, "data_ptr") and not hasattr(recent, "ctypes")):
             recent = np.ascontiguousarray(np.asarray(list(recent or ()), dtype=np.uint32))
+        elif isinstance(recent, np.ndarray):
+            recent = np.ascontiguousarray(recent.astype(np.uint32, copy=False))   # ids are u32 (&[u32])
         keep.append(recent)
+        if hasattr(recent, "element_size") and recent.element_size() != 4:
+            raise TypeError("recent ids must be 4-byte integers")
         W = int(recent.numel() if hasattr(recent, "numel") else recent.size)
         out = ctypes.c_uint32()
         _check(self._lib.gs_sample(self._h, _ptr(logits), V, _ptr(recent) if W else None, W,
