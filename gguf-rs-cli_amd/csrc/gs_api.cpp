@@ -19,8 +19,8 @@ struct gs_sampler {
     hipStream_t stream;          // stream of the synchronous single-row call
     float *d_row;                // staging for host logits
     size_t row_cap;
-    uint32_t *d_rec;             // staging for host recent ids
-    size_t rec_cap;
+    uint32_t *h_rec;             // pinned, mapped: a host window is copied here and read
+    uint32_t *d_rec_map;         // by the kernel through this alias (no copy command)
     uint32_t *h_tok;             // pinned, mapped, coherent: kernel writes the token here
     int32_t *h_status;
     uint64_t *h_done;            // single-row calls: (sequence << 32) | (status & 0xff) << 24 | token
@@ -112,6 +112,12 @@ int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out)
     }
     s->h_status = (int32_t *)(s->h_tok + 4);
     s->d_status_map = (int32_t *)(s->d_tok_map + 4);
+    if (hipHostMalloc((void **)&s->h_rec, sizeof(uint32_t) * gs::kMaxWindow,
+                      hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer((void **)&s->d_rec_map, s->h_rec, 0) != hipSuccess) {
+        gs_sampler_destroy(s);
+        return GS_ERR_HIP;
+    }
     s->h_done = reinterpret_cast<uint64_t *>(s->h_tok + 8);        // 32 bytes in: 8-byte aligned
     s->d_done_map = reinterpret_cast<uint64_t *>(s->d_tok_map + 8);
     *(volatile uint64_t *)s->h_done = 0u;
@@ -127,7 +133,7 @@ int gs_sampler_destroy(gs_sampler *s)
     (void)hipSetDevice(s->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     if (s->d_row) (void)hipFree(s->d_row);
-    if (s->d_rec) (void)hipFree(s->d_rec);
+    if (s->h_rec) (void)hipHostFree(s->h_rec);
     if (s->scratch) (void)hipFree(s->scratch);
     if (s->fb) (void)hipFree(s->fb);
     if (s->h_tok) (void)hipHostFree(s->h_tok);
@@ -188,15 +194,13 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
             return GS_ERR_HIP;
         d_logits = s->d_row;
     }
+    // A host window (the reference's &[u32]) is copied into mapped pinned
+    // memory; the kernel reads it there.  The previous call's kernel has
+    // finished (every call waits for its result), so the buffer is free.
     const uint32_t *d_rec = recent;
     if (W > 0 && !is_device_ptr(s, recent)) {
-        void *p = s->d_rec;
-        rc = grow(&p, &s->rec_cap, W * sizeof(uint32_t));
-        s->d_rec = (uint32_t *)p;
-        if (rc) return rc;
-        if (hipMemcpyAsync(s->d_rec, recent, W * sizeof(uint32_t), hipMemcpyHostToDevice, s->stream) != hipSuccess)
-            return GS_ERR_HIP;
-        d_rec = s->d_rec;
+        memcpy(s->h_rec, recent, W * sizeof(uint32_t));
+        d_rec = s->d_rec_map;
     }
     if (needs_full_path(s->params, V) && (rc = reserve_scratch(s, 1, V))) return rc;
     gs::RowArgs a;

@@ -66,6 +66,7 @@ struct RowSmem {
     float red_f32[kWaves];
     int red_i32[kWaves];
     double red_f64[kWaves];
+    alignas(16) float fin[256];                 // finish_wave: the values being accumulated
     int tok;
     union {
         TopkSmem tk;
@@ -303,52 +304,79 @@ __device__ __forceinline__ float rdl(float v, int l)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Sequential f32 accumulation cum_{j+1} = cum_j + sh[j], j in [0, len), in
+// the reference's order, stopping at the first j with pred(cum_{j+1}).
+// One wave; sh is wave-private LDS, zero past the values (len <= 256).  The
+// values are read with uniform addresses (LDS broadcast) eight at a time,
+// so the adds form a plain VGPR chain; lane i of each group keeps the
+// running sum after its element, and one ballot per group finds the stop.
+// Returns j (or len) and the running sum there (or after len) in *sum.
+template <class P>
+__device__ __forceinline__ int wave_seq(const float *sh, int len, P pred, float *sum)
+{
+    const int lane = lane_id();
+    float cum = 0.0f;
+#pragma nounroll
+    for (int g = 0; g < len; g += 8) {
+        const float4 a = *reinterpret_cast<const float4 *>(sh + g);
+        const float4 b = *reinterpret_cast<const float4 *>(sh + g + 4);
+        const float vals[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const int base = g & 63;
+        float cv = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            cum = cum + vals[i];
+            cv = lane == base + i ? cum : cv;
+        }
+        const int j = (g - base) + lane;
+        const uint64_t hit = __ballot(lane >= base && lane < base + 8 && j < len && pred(cv));
+        if (hit) {
+            const int L = (int)__builtin_ctzll(hit);
+            *sum = rdl(cv, L);
+            return (g - base) + L;
+        }
+    }
+    *sum = cum;   // the zero padding past len leaves the sum unchanged
+    return len;
+}
+
 template <class YV, class IX>
-__device__ int finish_wave(int n, YV yv, IX idx, float top_p, float r)
+__device__ int finish_wave(RowSmem &sm, int n, YV yv, IX idx, float top_p, float r)
 {
     const int lane = lane_id();
     const float m = yv(0);
     if (isinf(m)) return (int)idx(n - 1);
-    float v[4];
+    float *sh = sm.fin;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        int j = c * 64 + lane;
-        v[c] = (j < n) ? glibc_expf(yv(j) - m) : 0.0f;
+        const int j = c * 64 + lane;
+        sh[j] = (j < n) ? glibc_expf(yv(j) - m) : 0.0f;
     }
-    float sum = 0.0f;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float sum;
+    (void)wave_seq(sh, n, [](float) { return false; }, &sum);          // src/sampler.rs:54
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int lim = min(64, n - c * 64);
-        for (int l = 0; l < lim; l++) sum += rdl(v[c], l);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; c++) v[c] = v[c] / sum;
+    for (int c = 0; c < 4; c++) sh[c * 64 + lane] = sh[c * 64 + lane] / sum;   // :55 (0 / sum = 0)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     int cut = n;
     if (top_p < 1.0f) {
-        float cum = 0.0f;
-        bool done = false;
+        float s2;
+        const int stop = wave_seq(sh, n, [top_p](float c) { return c >= top_p; }, &s2);   // :59-64
+        cut = stop < n ? stop + 1 : n;
+        // the renormalising sum (:67) equals the running sum at the cut
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const int lim = min(64, n - c * 64);
-            for (int l = 0; l < lim && !done; l++) {
-                cum += rdl(v[c], l);
-                if (cum >= top_p) { cut = c * 64 + l + 1; done = true; }
-            }
+            const int j = c * 64 + lane;
+            sh[j] = j < cut ? sh[j] / s2 : 0.0f;
         }
-        const float s2 = cum;   // the renormalising sum (src/sampler.rs:67) equals the running sum at the cut
-#pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = v[c] / s2;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
     }
-    float cum = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int lim = min(64, cut - c * 64);
-        for (int l = 0; l < lim; l++) {
-            cum += rdl(v[c], l);
-            if (r < cum) return (int)idx(c * 64 + l);
-        }
-    }
-    return (int)idx(cut - 1);
+    float c;
+    const int pick = wave_seq(sh, cut, [r](float cc) { return r < cc; }, &c);   // :72-77
+    return (int)idx(pick < cut ? pick : cut - 1);
 }
 
 // --------------------------------------------------------------------------
@@ -360,7 +388,7 @@ __device__ int finish_sorted(RowSmem &sm, int n, YV yv, IX idx, float top_p, flo
 {
     if (n <= kWaveFinishMax) {
         if (wave_id() == 0) {
-            int tk = finish_wave(n, yv, idx, top_p, r);
+            int tk = finish_wave(sm, n, yv, idx, top_p, r);
             if (lane_id() == 0) sm.tok = tk;
         }
         GS_SUB0(6);

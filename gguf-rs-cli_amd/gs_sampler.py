@@ -114,20 +114,27 @@ _TORCH = None
 
 
 def _torch_fast_args(logits, recent):
-    """(ptr, V, recent ptr, W) for a contiguous torch f32 row and a torch
-    window of 4-byte ids (or None / empty); None for anything else."""
+    """(ptr, V, recent ptr, W) for a contiguous torch f32 row and a window
+    that is a torch tensor of 4-byte ids, a contiguous numpy uint32 array or
+    None / empty; None for anything else."""
     global _TORCH
     if _TORCH is None:
         import sys
         t = sys.modules.get("torch")
         if t is None:
             return None
-        _TORCH = (t.Tensor, t.float32, (t.int32, t.uint32))
-    tensor, f32, ids = _TORCH
+        import numpy as np
+        _TORCH = (t.Tensor, t.float32, (t.int32, t.uint32), np.ndarray, np.dtype(np.uint32))
+    tensor, f32, ids, ndarray, u32 = _TORCH
     if type(logits) is not tensor or logits.dtype is not f32 or not logits.is_contiguous():
         return None
     if recent is None or (type(recent) is tuple and not recent):
         return logits.data_ptr(), logits.numel(), None, 0
+    if type(recent) is ndarray:
+        if recent.dtype != u32 or not recent.flags.c_contiguous:
+            return None
+        W = recent.size
+        return logits.data_ptr(), logits.numel(), (recent.ctypes.data if W else None), W
     if type(recent) is not tensor or recent.dtype not in ids or not recent.is_contiguous():
         return None
     W = recent.numel()
