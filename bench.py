@@ -147,6 +147,23 @@ def kernel_only_c1(gs, torch, reps=200):
     return e0.elapsed_time(e1) / reps * 1e3
 
 
+def c1_isolated(gs, torch, reps=50):
+    """The c1 single-row kernel launched alone: step-0 row, device window,
+    a synchronization after every launch (the profile's workload)."""
+    import workloads
+    w = workloads.make("c1", steps=1)
+    d_lg = torch.from_numpy(w["logits"]).cuda()
+    d_win = torch.from_numpy(w["init_recent"].view(np.int32)).cuda().reshape(1, w["W"])
+    d_u = torch.zeros(1, dtype=torch.float32, device="cuda")
+    d_tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = gs.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
+    st = torch.cuda.current_stream()
+    for _ in range(reps):
+        s.sample_batch(d_lg, d_tok, recent=d_win, u=d_u, stream=st)
+        torch.cuda.synchronize()
+    log("c1 isolated: %d launches, token %d" % (reps, int(d_tok[0])))
+
+
 def calib_copy(torch, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of a known size: its FETCH_SIZE and
     WRITE_SIZE per dispatch give the scale factor of those counters."""
@@ -197,6 +214,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--c3-only", action="store_true",
                     help="time only the c3 batch (for counter runs)")
+    ap.add_argument("--c1-kernel", action="store_true",
+                    help="only 50 isolated single-row launches of the c1 kernel (for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 1 GiB device copy 5x (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -210,6 +229,9 @@ def main():
     torch.cuda.init()
     if args.calib_copy:
         calib_copy(torch)
+        return
+    if args.c1_kernel:
+        c1_isolated(gs, torch)
         return
     c3 = bench_c3(gs, torch, args.steps, args.warmup)
     log("c3: %.3f ms/step" % c3["ms"])
