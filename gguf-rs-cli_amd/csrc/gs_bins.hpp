@@ -1468,7 +1468,12 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     if (t == 0 && blockIdx.x < 256) g_fails[512 + blockIdx.x] = ((bn.ncollect >> 16) ? 1 : 0) | (s_exact ? 0 : 4);
 #endif
     if (bn.ncollect >> 16) {
-        if (!use_ix || !collect_now_ix(sm, row, t_one, T, gl, ix)) collect_now(sm, row, V, t_one, T, has_pen, gl);
+        if (!use_ix || !collect_now_ix(sm, row, t_one, T, gl, ix)) {
+#ifdef GS_TIMING
+            if (t == 0 && blockIdx.x < 256) g_fails[512 + blockIdx.x] |= 16;
+#endif
+            collect_now(sm, row, V, t_one, T, has_pen, gl);
+        }
         if (!finish_now(sm, gl, tmp)) BINS_FAIL();
     }
     // runs carry the accumulation-2 grids now: always regroup; the walk array
@@ -1571,6 +1576,9 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
             gather = !block_or((int)bad, sm);
         }
         if (gather) {
+#ifdef GS_TIMING
+            if (t == 0 && blockIdx.x < 256) g_fails[512 + blockIdx.x] |= 8;
+#endif
             const uint32_t p0 = bn.off[0], p1 = bn.ixlast >= 0 ? bn.off[bn.ixlast + 1] : p0;
             auto act = [&](uint32_t i, float y, const Cls &c) {
                 if (c.cl == 1) {
@@ -1632,7 +1640,12 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     if (t == 0 && blockIdx.x < 256 && bn.ncollect) g_fails[512 + blockIdx.x] |= 2;
 #endif
     if (bn.ncollect) {
-        if (!use_ix || !collect_now_ix(sm, row, t_one, T, gl, ix)) collect_now(sm, row, V, t_one, T, has_pen, gl);
+        if (!use_ix || !collect_now_ix(sm, row, t_one, T, gl, ix)) {
+#ifdef GS_TIMING
+            if (t == 0 && blockIdx.x < 256) g_fails[512 + blockIdx.x] |= 32;
+#endif
+            collect_now(sm, row, V, t_one, T, has_pen, gl);
+        }
         if (!finish_now(sm, gl, tmp)) BINS_FAIL();
     }
     if (!build_groups(sm)) BINS_FAIL();

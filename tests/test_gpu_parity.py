@@ -249,6 +249,44 @@ def test_topk_register_rows(gpu, torch, oracle, V):
         check_tokens("topk_reg V%d u%.2f" % (V, u0), tok, want, st)
 
 
+@pytest.mark.parametrize("V", [4096, 40000])
+def test_odd_penalties(gpu, torch, oracle, V):
+    """Penalties that push logits to +-inf, 0 or NaN (rep 0, negative, inf,
+    NaN, tiny, huge) on the register path (V <= 32768), the longer top-k
+    path and the full-vocabulary path; the window holds the largest logits,
+    -inf entries and repeats.  A NaN the reference would panic on must come
+    back as GS_ERR_NAN."""
+    import workloads
+    rng = np.random.default_rng(V + 1)
+    W = 96
+    reps = [0.0, -1.0, np.inf, np.nan, 1e-30, 1e30, 0.5, -0.0]
+    rows, prm, recs = [], [], []
+    for i, rep in enumerate(reps):
+        for k in (40, 0):
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+            if i % 2:
+                x[rng.choice(V, 5, replace=False)] = -np.inf
+            top = np.argsort(-x, kind="stable")[:8].astype(np.uint32)
+            neg = np.nonzero(x == -np.inf)[0].astype(np.uint32)
+            rec = np.concatenate([top, top[:2], neg, rng.integers(0, V, W).astype(np.uint32)])[:W]
+            rows.append(x)
+            prm.append((0.7 if k else 1.0, k, 0.9, rep))
+            recs.append(rec)
+    x = np.stack(rows)
+    pr = workloads.params_rows(prm)
+    rec = np.stack(recs)
+    for u0 in (0.0, 0.6):
+        u = np.full(len(rows), u0, np.float32)
+        _say("odd penalties V", V, "u", u0)
+        tok, st, _ = run_batch(gpu, torch, x, params=pr, u=u, recent=rec)
+        want = oracle.sample_batch(x, pr, u, recent=rec)
+        for j in range(len(rows)):
+            if want[j] < 0:
+                assert st[j] == want[j], (j, prm[j], st[j], want[j])
+            else:
+                assert st[j] == 0 and tok[j] == want[j], (j, prm[j], st[j], tok[j], want[j])
+
+
 def test_errors(gpu, torch):
     x = np.ones((3, 100), np.float32)
     x[1, 50] = np.nan
