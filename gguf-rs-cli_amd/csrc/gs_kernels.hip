@@ -769,15 +769,12 @@ __device__ __forceinline__ void reg_clear(RowSmem &sm, bool has_pen)
     if (t == 0) sm.ncand = 0;
 }
 
-__device__ int topk_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
-                            float top_p, bool has_pen, float pen, float r, int *status, bool *ok)
+// Penalty table of a register row (src/sampler.rs:23-30), built alongside
+// the row pass: this thread's window id goes in now; the thread that created
+// a slot (the returned slot, else -1) stores the penalized value after the
+// next barrier, when the count is complete.  Also sets the id's bit.
+__device__ __forceinline__ int pen_insert(RowSmem &sm, const PenLoad &pl, bool has_pen)
 {
-    const int t = threadIdx.x, lane = lane_id(), w = wave_id();
-    const int n4 = V >> 2;
-    *ok = false;
-    // Penalty table (src/sampler.rs:23-30), built alongside the row pass:
-    // the ids go in now, the thread that created a slot stores the
-    // penalized value after the next barrier, when the count is complete.
     int myslot = -1;
     if (has_pen && pl.id != kEmpty) {
         uint32_t h = hash_slot(pl.id);
@@ -792,6 +789,75 @@ __device__ int topk_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int V
         }
         atomicOr(&sm.x.tk.pbits[pl.id >> 5], 1u << (pl.id & 31u));   // V <= 32768: every id has a bit
     }
+    return myslot;
+}
+
+// Greedy (T <= 0) for rows held in registers: the argmax of the penalized
+// logits, the last index among equal maxima (src/sampler.rs:15-19: max_by
+// keeps the last of equal elements; -0 and +0 compare equal).  A NaN
+// anywhere makes the reference panic (V > 1).
+__device__ int greedy_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int V, bool has_pen, float pen,
+                              int *status)
+{
+    const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+    const int n4 = V >> 2;
+    const int myslot = pen_insert(sm, pl, has_pen);
+    uint64_t nanm = 0;
+#pragma unroll
+    for (int u = 0; u < kRegF4; u++) {
+        nanm |= __ballot(__builtin_isunordered(rv[u].x, rv[u].y));
+        nanm |= __ballot(__builtin_isunordered(rv[u].z, rv[u].w));
+    }
+    __syncthreads();   // counts and bitmap complete
+    float bv = -INFINITY;
+    int bi = -1;
+    bool pnan = false;
+    // elements in index order (u, then c), so >= keeps the last maximum
+#pragma unroll
+    for (int u = 0; u < kRegF4; u++) {
+        const int q = u * kThreads + t;
+        const uint32_t nib = (has_pen && q < n4) ? (sm.x.tk.pbits[q >> 3] >> ((q & 7) * 4)) & 15u : 0u;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float x = f4c(rv[u], c);
+            if (q < n4 && !((nib >> c) & 1u) && x >= bv) { bv = x; bi = 4 * q + c; }
+        }
+    }
+    if (myslot >= 0) {
+        const float pv = penalize(pl.raw, sm.hval[myslot], pen);
+        pnan = isnan(pv);
+        if (pv > bv || (pv == bv && (int)pl.id > bi)) { bv = pv; bi = (int)pl.id; }
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+        const float ov = __shfl_xor(bv, d, 64);
+        const int oi = __shfl_xor(bi, d, 64);
+        if (ov > bv || (ov == bv && oi > bi)) { bv = ov; bi = oi; }
+    }
+    const bool wnan = (nanm != 0) || __any(pnan);
+    if (lane == 0) { sm.red_f32[w] = bv; sm.red_i32[w] = bi; sm.red_u32[w] = wnan ? 1u : 0u; }
+    __syncthreads();
+    float v = sm.red_f32[0];
+    int ix = sm.red_i32[0];
+    uint32_t anynan = sm.red_u32[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; i++) {
+        const float ov = sm.red_f32[i];
+        const int oi = sm.red_i32[i];
+        if (ov > v || (ov == v && oi > ix)) { v = ov; ix = oi; }
+        anynan |= sm.red_u32[i];
+    }
+    *status = (anynan && V > 1) ? GS_ERR_NAN : GS_OK;
+    return ix < 0 ? 0 : ix;
+}
+
+__device__ int topk_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
+                            float top_p, bool has_pen, float pen, float r, int *status, bool *ok)
+{
+    const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+    const int n4 = V >> 2;
+    *ok = false;
+    const int myslot = pen_insert(sm, pl, has_pen);
     // Slots past the row (clamped loads) become -inf, below every bound
     // used.  Done here, after the table inserts: overwriting a register that
     // a load is still filling waits for that load.
@@ -1153,10 +1219,10 @@ sample_rows_kernel(RowArgs a)
     // Small top-k rows that fit in registers: issue the row loads before the
     // penalty table is built, so the two overlap.
     const int keep0 = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
-    const bool regpath = MODE == kModeSmall && p.temperature > 0.0f && p.temperature < INFINITY &&
-                         V > 1 && (V & 3) == 0 &&
-                         V <= kThreads * 4 * kRegF4 && keep0 < V &&
-                         ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+    const bool regfit = MODE == kModeSmall && V > 1 && (V & 3) == 0 && V <= kThreads * 4 * kRegF4 &&
+                        ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+    const bool reg_greedy = regfit && p.temperature <= 0.0f;
+    const bool regpath = (regfit && p.temperature > 0.0f && p.temperature < INFINITY && keep0 < V) || reg_greedy;
     float4 rv[kRegF4];
     if (regpath) {
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
@@ -1182,7 +1248,8 @@ sample_rows_kernel(RowArgs a)
         } else if (!(p.temperature > 0.0f)) {
             // src/sampler.rs:39: `if temperature <= 0.0` -- a NaN temperature is
             // not <= 0, so it falls through to the division below.
-            if (p.temperature <= 0.0f) greedy_row(sm, row, V, has_pen, &tok, &status);
+            if (reg_greedy) tok = greedy_row_reg(sm, rv, pl, V, has_pen, p.rep_penalty, &status);
+            else if (p.temperature <= 0.0f) greedy_row(sm, row, V, has_pen, &tok, &status);
             else {
                 // T is NaN: every scaled logit is NaN; the sort panics for V > 1.
                 tok = 0;

@@ -249,6 +249,50 @@ def test_topk_register_rows(gpu, torch, oracle, V):
         check_tokens("topk_reg V%d u%.2f" % (V, u0), tok, want, st)
 
 
+@pytest.mark.parametrize("V", [32000, 4096, 8, 40000])
+def test_greedy_rows(gpu, torch, oracle, V):
+    """Greedy (T <= 0) rows, register path (V <= 32768) and the row loop:
+    ties (the last maximal index wins), -0 and +0, all -inf, a penalized
+    maximum, penalties in both directions and NaN rows."""
+    import workloads
+    rng = np.random.default_rng(V + 7)
+    rows, prm, recs = [], [], []
+    W = 64
+    for case in range(12):
+        kind = case % 6
+        if kind == 0:
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+        elif kind == 1:
+            x = rng.integers(-3, 3, V).astype(np.float32)
+        elif kind == 2:
+            x = np.full(V, -np.inf, np.float32)
+        elif kind == 3:
+            x = np.where(rng.random(V) < 0.5, np.float32(-0.0), np.float32(0.0)).astype(np.float32)
+        elif kind == 4:
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+            x[rng.choice(V, 3, replace=False)] = x.max()
+        else:
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+            if case >= 6 and V > 1:
+                x[rng.integers(0, V)] = np.nan
+        top = np.argsort(-x, kind="stable")[:4].astype(np.uint32)
+        rec = np.concatenate([top, rng.integers(0, V, W).astype(np.uint32)])[:W]
+        rows.append(x)
+        prm.append(([0.0, -1.0][case % 2], 40, 0.9, [1.0, 1.3, 0.6, 1.1][case % 4]))
+        recs.append(rec)
+    x = np.stack(rows)
+    pr = workloads.params_rows(prm)
+    rec = np.stack(recs)
+    u = np.zeros(len(rows), np.float32)
+    tok, st, _ = run_batch(gpu, torch, x, params=pr, u=u, recent=rec)
+    want = oracle.sample_batch(x, pr, u, recent=rec)
+    for j in range(len(rows)):
+        if want[j] < 0:
+            assert st[j] == want[j], (j, prm[j], st[j], want[j])
+        else:
+            assert st[j] == 0 and tok[j] == want[j], (j, prm[j], st[j], tok[j], want[j])
+
+
 @pytest.mark.parametrize("V", [4096, 40000])
 def test_odd_penalties(gpu, torch, oracle, V):
     """Penalties that push logits to +-inf, 0 or NaN (rep 0, negative, inf,
