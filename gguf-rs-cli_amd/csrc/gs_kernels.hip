@@ -97,13 +97,13 @@ __device__ __forceinline__ int hash_find(const RowSmem &sm, uint32_t id)
 // [0, V) are skipped, as logits.get_mut does at src/sampler.rs:26.
 struct PenLoad { uint32_t id; float raw; };
 static_assert(kMaxWindow <= kThreads, "one window entry per thread");
-__device__ __forceinline__ PenLoad pen_load(const float *row, int V, const uint32_t *rec, int W)
+__device__ __forceinline__ PenLoad pen_load(const float *row, int V, const uint32_t *rec, int W, bool with_raw)
 {
     PenLoad p{kEmpty, 0.0f};
     const int t = threadIdx.x;
     if (t < W) {
         const uint32_t id = ldg(rec + t);
-        if (id < (uint32_t)V) { p.id = id; p.raw = ldg(row + id); }
+        if (id < (uint32_t)V) { p.id = id; if (with_raw) p.raw = ldg(row + id); }
     }
     return p;
 }
@@ -796,11 +796,12 @@ __device__ __forceinline__ int pen_insert(RowSmem &sm, const PenLoad &pl, bool h
 // logits, the last index among equal maxima (src/sampler.rs:15-19: max_by
 // keeps the last of equal elements; -0 and +0 compare equal).  A NaN
 // anywhere makes the reference panic (V > 1).
-__device__ int greedy_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int V, bool has_pen, float pen,
-                              int *status)
+__device__ int greedy_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4], PenLoad pl, int V, bool has_pen,
+                              float pen, int *status)
 {
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int n4 = V >> 2;
+    if (pl.id != kEmpty) pl.raw = ldg(row + pl.id);
     const int myslot = pen_insert(sm, pl, has_pen);
     uint64_t nanm = 0;
 #pragma unroll
@@ -851,12 +852,13 @@ __device__ int greedy_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int
     return ix < 0 ? 0 : ix;
 }
 
-__device__ int topk_row_reg(RowSmem &sm, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
+__device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
                             float top_p, bool has_pen, float pen, float r, int *status, bool *ok)
 {
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int n4 = V >> 2;
     *ok = false;
+    if (pl.id != kEmpty) pl.raw = ldg(row + pl.id);
     const int myslot = pen_insert(sm, pl, has_pen);
     // Slots past the row (clamped loads) become -inf, below every bound
     // used.  Done here, after the table inserts: overwriting a register that
@@ -1230,7 +1232,10 @@ sample_rows_kernel(RowArgs a)
 #pragma unroll
         for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
     }
-    const PenLoad pl = has_pen ? pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W) : PenLoad{kEmpty, 0.0f};
+    // The register paths load the raw logits of the window ids themselves,
+    // after the first barrier: the load depends on the id, and waiting for
+    // the id here would hold every wave at that barrier.
+    PenLoad pl = has_pen ? pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W, !regpath) : PenLoad{kEmpty, 0.0f};
     if (regpath) reg_clear(sm, has_pen);   // the register path builds its penalty table itself
     __syncthreads();
     if (has_pen && !regpath) build_penalty(sm, pl, p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
@@ -1248,7 +1253,7 @@ sample_rows_kernel(RowArgs a)
         } else if (!(p.temperature > 0.0f)) {
             // src/sampler.rs:39: `if temperature <= 0.0` -- a NaN temperature is
             // not <= 0, so it falls through to the division below.
-            if (reg_greedy) tok = greedy_row_reg(sm, rv, pl, V, has_pen, p.rep_penalty, &status);
+            if (reg_greedy) tok = greedy_row_reg(sm, row, rv, pl, V, has_pen, p.rep_penalty, &status);
             else if (p.temperature <= 0.0f) greedy_row(sm, row, V, has_pen, &tok, &status);
             else {
                 // T is NaN: every scaled logit is NaN; the sort panics for V > 1.
@@ -1262,7 +1267,7 @@ sample_rows_kernel(RowArgs a)
         } else {
             bool ok;
             if (regpath)
-                tok = topk_row_reg(sm, rv, pl, V, keep, p.temperature, p.top_p, has_pen, p.rep_penalty, r,
+                tok = topk_row_reg(sm, row, rv, pl, V, keep, p.temperature, p.top_p, has_pen, p.rep_penalty, r,
                                    &status, &ok);
             else
                 tok = topk_row_tmax(sm, row, V, keep, p.temperature, p.top_p, has_pen, sm.nuniq, r,
