@@ -198,7 +198,8 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     // memory; the kernel reads it there.  The previous call's kernel has
     // finished (every call waits for its result), so the buffer is free.
     const uint32_t *d_rec = recent;
-    if (W > 0 && !is_device_ptr(s, recent)) {
+    const bool host_win = W > 0 && !is_device_ptr(s, recent);
+    if (host_win) {
         memcpy(s->h_rec, recent, W * sizeof(uint32_t));
         d_rec = s->d_rec_map;
     }
@@ -221,37 +222,50 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     a.scratch = s->scratch;
     a.scratch_stride = gs::scratch_u32_per_row(V);
     a.fb = s->fb;
-    const bool full = needs_full_path(s->params, V);
-    // A single small-path kernel signals completion through the mapped flag,
-    // so the host polls it instead of a stream synchronisation; the
-    // full-vocabulary path (several kernels) synchronises the stream.
-    const uint32_t seq = ++s->seq;
-    if (!full) {
-        a.done = s->d_done_map;
-        a.done_val = seq;
+    if (host_win && W <= (size_t)gs::kKernWin) {
+        // a short host window also travels in the kernel arguments: the
+        // register path reads it there instead of across the bus
+        memcpy(a.kwin, recent, W * sizeof(uint32_t));
+        a.kwin_n = (int)W;
     }
-    if (gs::launch_sample_rows(a, 1, !full, full, s->stream) != hipSuccess) return GS_ERR_HIP;
+    const bool full = needs_full_path(s->params, V);
     int st;
     uint32_t tok;
     if (full) {
+        // the full-vocabulary path (several kernels) synchronises the stream
+        if (gs::launch_sample_rows(a, 1, false, true, s->stream) != hipSuccess) return GS_ERR_HIP;
         if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
         st = *(volatile int32_t *)s->h_status;
         tok = *(volatile uint32_t *)s->h_tok;
     } else {
-        volatile uint64_t *f = s->h_done;
-        uint64_t w = *f;
-        for (uint32_t spins = 0; (uint32_t)(w >> 32) != seq; spins++) {
-            if (spins > (1u << 22)) {           // slow call: wait through the runtime
-                if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
+        // One small-path kernel signals completion through the mapped word,
+        // which the host polls instead of synchronising the stream.  Rows
+        // that fit in registers take the dedicated kernel; the rare row it
+        // cannot finish is run again by the general one.
+        a.done = s->d_done_map;
+        bool reg = gs::reg_row_fits(s->params, V, a.logits);
+        for (;;) {
+            a.done_val = ++s->seq;
+            const hipError_t le = reg ? gs::launch_reg_row(a, s->stream)
+                                      : gs::launch_sample_rows(a, 1, true, false, s->stream);
+            if (le != hipSuccess) return GS_ERR_HIP;
+            volatile uint64_t *f = s->h_done;
+            uint64_t w = *f;
+            for (uint32_t spins = 0; (uint32_t)(w >> 32) != s->seq; spins++) {
+                if (spins > (1u << 22)) {           // slow call: wait through the runtime
+                    if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
+                    w = *f;
+                    if ((uint32_t)(w >> 32) != s->seq) return GS_ERR_HIP;
+                    break;
+                }
+                __builtin_ia32_pause();
                 w = *f;
-                if ((uint32_t)(w >> 32) != seq) return GS_ERR_HIP;
-                break;
             }
-            __builtin_ia32_pause();
-            w = *f;
+            st = (int)(int8_t)(uint8_t)(w >> 24);
+            tok = (uint32_t)w & 0xffffffu;
+            if (!(reg && st == gs::kStatusRetryHost)) break;
+            reg = false;
         }
-        st = (int)(int8_t)(uint8_t)(w >> 24);
-        tok = (uint32_t)w & 0xffffffu;
     }
     if (s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, 1);   // one draw iff T > 0
     if (st != GS_OK) return st;

@@ -801,6 +801,7 @@ __device__ int greedy_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4
 {
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int n4 = V >> 2;
+    if (pl.id >= (uint32_t)V) pl.id = kEmpty;   // also kEmpty itself
     if (pl.id != kEmpty) pl.raw = ldg(row + pl.id);
     const int myslot = pen_insert(sm, pl, has_pen);
     uint64_t nanm = 0;
@@ -858,6 +859,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int n4 = V >> 2;
     *ok = false;
+    if (pl.id >= (uint32_t)V) pl.id = kEmpty;   // also kEmpty itself
     if (pl.id != kEmpty) pl.raw = ldg(row + pl.id);
     const int myslot = pen_insert(sm, pl, has_pen);
     // Slots past the row (clamped loads) become -inf, below every bound
@@ -1225,6 +1227,26 @@ sample_rows_kernel(RowArgs a)
                         ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
     const bool reg_greedy = regfit && p.temperature <= 0.0f;
     const bool regpath = (regfit && p.temperature > 0.0f && p.temperature < INFINITY && keep0 < V) || reg_greedy;
+    // The register paths issue the window id load first and the row loads
+    // after it, and test the id (ids >= V are skipped) only after the first
+    // barrier: loads complete in issue order, so a test before the row loads
+    // are issued, or a wait for a load issued after them, would hold every
+    // wave at that barrier until the whole row has arrived.  They load the
+    // raw logits of the window ids themselves, after that barrier.  A short
+    // host window arrives in the kernel arguments (kwin).
+    PenLoad pl{kEmpty, 0.0f};
+    const uint32_t *wsrc = nullptr;        // wave-uniform: no divergent join waits for the id
+    if (regpath && has_pen && W > 0) {
+        if (a.kwin_n) {
+            const char __attribute__((address_space(4))) *ka =
+                (const char __attribute__((address_space(4))) *)__builtin_amdgcn_kernarg_segment_ptr();
+            wsrc = reinterpret_cast<const uint32_t *>((uintptr_t)(ka + offsetof(RowArgs, kwin)));
+        } else {
+            wsrc = a.recent + (size_t)b * a.ld_recent;
+        }
+    }
+    uint32_t rid = kEmpty;
+    if (wsrc) rid = ldg(wsrc + min(t, W - 1));
     float4 rv[kRegF4];
     if (regpath) {
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
@@ -1232,13 +1254,11 @@ sample_rows_kernel(RowArgs a)
 #pragma unroll
         for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
     }
-    // The register paths load the raw logits of the window ids themselves,
-    // after the first barrier: the load depends on the id, and waiting for
-    // the id here would hold every wave at that barrier.
-    PenLoad pl = has_pen ? pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W, !regpath) : PenLoad{kEmpty, 0.0f};
+    if (has_pen && !regpath) pl = pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W, true);
     if (regpath) reg_clear(sm, has_pen);   // the register path builds its penalty table itself
     __syncthreads();
     if (has_pen && !regpath) build_penalty(sm, pl, p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
+    if (wsrc && t < W) pl.id = rid;        // tested against V by the register paths
     GS_STAMP(8 * MODE + 1);
 
     // The uniform draw for this row (only consumed if T > 0).
@@ -1316,6 +1336,73 @@ sample_rows_kernel(RowArgs a)
     }
 }
 
+// Single-row register path as a kernel of its own (B = 1): only the code of
+// the register-resident rows (V <= 32768, V % 4 == 0, 16-byte aligned row,
+// greedy or 0 < k < V with k <= kMaxTopK, finite T), so it needs far fewer
+// registers and no scratch.  The rare rows whose bound check fails report
+// kStatusRetry; the host then runs sample_rows_kernel<kModeSmall> on the row.
+constexpr int kStatusRetry = 0x7f;
+__global__ void __launch_bounds__(kThreads)
+reg_row_kernel(RowArgs a)
+{
+    __shared__ RowSmem sm;
+    const int t = threadIdx.x;
+    const int V = a.V;
+    const gs_params p = a.uparams;
+    const float *row = a.logits;
+    GS_STAMP(0);
+    if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
+    const bool has_pen = (p.rep_penalty != 1.0f) && (a.recent != nullptr || a.kwin_n);
+    const int W = has_pen ? a.W : 0;
+    // Window id first, then the row (see sample_rows_kernel).
+    const uint32_t *wsrc = nullptr;
+    if (W > 0) {
+        if (a.kwin_n) {
+            const char __attribute__((address_space(4))) *ka =
+                (const char __attribute__((address_space(4))) *)__builtin_amdgcn_kernarg_segment_ptr();
+            wsrc = reinterpret_cast<const uint32_t *>((uintptr_t)(ka + offsetof(RowArgs, kwin)));
+        } else {
+            wsrc = a.recent;
+        }
+    }
+    uint32_t rid = kEmpty;
+    if (wsrc) rid = ldg(wsrc + min(t, W - 1));
+    float4 rv[kRegF4];
+    {
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        const int n4 = V >> 2;
+#pragma unroll
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+    }
+    reg_clear(sm, has_pen);
+    __syncthreads();
+    GS_STAMP(1);
+    PenLoad pl{kEmpty, 0.0f};
+    if (t < W) pl.id = rid;
+    int tok, status = GS_OK;
+    if (p.temperature <= 0.0f) {
+        tok = greedy_row_reg(sm, row, rv, pl, V, has_pen, p.rep_penalty, &status);
+    } else {
+        const float r = a.u ? a.u[0] : lcg_value(a.lcg_state);
+        const int keep = (int)p.top_k;
+        bool ok;
+        tok = topk_row_reg(sm, row, rv, pl, V, keep, p.temperature, p.top_p, has_pen, p.rep_penalty, r,
+                           &status, &ok);
+        if (!ok) { tok = 0; status = kStatusRetry; }
+    }
+    GS_STAMP(7);
+    if (t == 0) {
+        if (a.done) {
+            const uint64_t word = ((uint64_t)a.done_val << 32) | ((uint64_t)((uint32_t)status & 0xffu) << 24) |
+                                  (uint64_t)((uint32_t)tok & 0xffffffu);
+            __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else {
+            a.tokens[0] = (uint32_t)tok;
+            if (a.status) a.status[0] = status;
+        }
+    }
+}
+
 __global__ void window_push_kernel(uint32_t *win, int B, size_t ld, int W, size_t pos,
                                    const uint32_t *tok)
 {
@@ -1367,6 +1454,18 @@ hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hi
         hipLaunchKernelGGL(sample_rows_kernel<kModeSort>, dim3(B), dim3(kThreads), 0, st, a);
     }
     return hipGetLastError();
+}
+hipError_t launch_reg_row(const RowArgs &a, hipStream_t st)
+{
+    hipLaunchKernelGGL(reg_row_kernel, dim3(1), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
+bool reg_row_fits(const gs_params &p, size_t V, const void *row)
+{
+    if (V < 2 || (V & 3) != 0 || V > (size_t)(kThreads * 4 * kRegF4) || ((uintptr_t)row & 15u) != 0) return false;
+    if (p.temperature <= 0.0f) return true;                  // greedy (a NaN T is not <= 0)
+    return p.temperature > 0.0f && p.temperature < INFINITY && p.top_k > 0 && (size_t)p.top_k < V &&
+           p.top_k <= (uint32_t)kMaxTopK;
 }
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st)

@@ -8,6 +8,7 @@ namespace gs {
 
 constexpr int kMaxWindow = 1024;   // unique penalized ids held in the LDS hash
 constexpr int kMaxTopK = 1024;     // largest k served by the LDS top-k path
+constexpr int kKernWin = 64;       // host windows up to this length travel in the kernel arguments
 
 struct RowArgs {
     const float *logits;
@@ -29,6 +30,8 @@ struct RowArgs {
     uint64_t *done;                // optional (single-row calls, B = 1): receives
     uint32_t done_val;             // (done_val << 32) | (status & 0xff) << 24 | token in one store,
                                    // instead of tokens/status, for host polling
+    int kwin_n;                    // single-row calls: a host window of W <= kKernWin ids passed
+    uint32_t kwin[kKernWin];       // by value here (used instead of `recent` when kwin_n != 0)
 };
 
 // Per-row scratch (u32 units) of the full-vocabulary paths: the sort path
@@ -42,6 +45,10 @@ inline size_t scratch_u32_per_row(size_t V)
 }
 
 hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st);
+// Single-row register path (B = 1); rows it cannot finish report kStatusRetryHost.
+constexpr int kStatusRetryHost = 0x7f;
+bool reg_row_fits(const gs_params &p, size_t V, const void *row);
+hipError_t launch_reg_row(const RowArgs &a, hipStream_t st);
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st);
 hipError_t launch_synth(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0,
