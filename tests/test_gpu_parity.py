@@ -249,6 +249,57 @@ def test_topk_register_rows(gpu, torch, oracle, V):
         check_tokens("topk_reg V%d u%.2f" % (V, u0), tok, want, st)
 
 
+@pytest.mark.parametrize("V", [32000, 32768, 4096, 64, 8, 40000])
+def test_single_row_calls(gpu, torch, oracle, V):
+    """gs_sample one row at a time (the reference's call shape): device and
+    host logits, host windows short enough for the kernel arguments (<= 64
+    ids) and longer ones, device windows; top-k and greedy rows; rows the
+    register kernel hands back to the general kernel (k above the number of
+    threads holding elements, too few finite logits).  The draw is the
+    sampler's LCG, seeded per call."""
+    rng = np.random.default_rng(V + 11)
+    for case in range(30):
+        kind = case % 5
+        if kind == 0:
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+        elif kind == 1:
+            x = (rng.integers(-4, 4, V) / 4).astype(np.float32)
+        elif kind == 2:
+            x = np.full(V, -np.inf, np.float32)
+            x[rng.choice(V, min(V, 3), replace=False)] = rng.standard_normal(min(V, 3))
+        elif kind == 3:
+            x = (rng.standard_normal(V) * 3).astype(np.float32)
+            x[rng.choice(V, min(V, 5), replace=False)] += 10
+        else:
+            x = (rng.standard_normal(V) * 0.01 + 5).astype(np.float32)
+        nrec = [0, 64, 7, 300, 1024, 64][case % 6]
+        top = np.argsort(-x, kind="stable")[:8].astype(np.uint32)
+        rec = np.concatenate([top, rng.integers(0, V, 1024).astype(np.uint32)])[:nrec]
+        if nrec > 4:
+            rec[2:4] = [V, 2 ** 31 + 5]
+        T = [0.7, 1.0, 0.0, 2.5, -1.0, 0.3][case % 6]
+        k = [40, 1, 1000, 60, 20, 5][(case // 2) % 6]
+        k = min(k, V - 1)
+        p = [0.9, 1.0, 0.5][case % 3]
+        rep = [1.1, 1.3, 0.8, 1.0][(case // 3) % 4]
+        seed = 1000 + case
+        dev_row = case % 2 == 0
+        dev_win = case % 4 == 3
+        xr = torch.from_numpy(x).cuda() if dev_row else x
+        rr = torch.from_numpy(rec.view(np.int32)).cuda() if (dev_win and nrec) else rec
+        s = gpu.Sampler(T, k, p, rep, seed=seed)
+        want = oracle.sample(x, T, k, p, rep, recent=rec, state=seed)
+        _say("single V", V, "case", case, "T", T, "k", k, "W", nrec, "dev", dev_row, dev_win)
+        if want < 0:
+            with pytest.raises(gpu.SamplerError) as ei:
+                s.sample(xr, rr)
+            assert ei.value.code == want, (case, ei.value.code, want)
+        else:
+            got = s.sample(xr, rr)
+            assert got == want, (V, case, T, k, p, rep, nrec, got, want)
+        assert s.state == (oracle.lcg_draws(seed, 1)[1] if T > 0 else seed), case
+
+
 @pytest.mark.parametrize("V", [32000, 4096, 8, 40000])
 def test_greedy_rows(gpu, torch, oracle, V):
     """Greedy (T <= 0) rows, register path (V <= 32768) and the row loop:
