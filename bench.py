@@ -148,20 +148,25 @@ def kernel_only_c1(gs, torch, reps=200):
 
 
 def c1_isolated(gs, torch, reps=50):
-    """The c1 single-row kernel launched alone: step-0 row, device window,
-    a synchronization after every launch (the profile's workload)."""
+    """The c1 single-row kernels launched alone on the step-0 row: `reps`
+    gs_sample calls (the register kernel, host window as in the reference),
+    then `reps` batch-entry launches with B=1 and a device window (the
+    general kernel), a synchronization after every launch (the profile's
+    workload)."""
     import workloads
     w = workloads.make("c1", steps=1)
     d_lg = torch.from_numpy(w["logits"]).cuda()
+    win = np.ascontiguousarray(w["init_recent"].astype(np.uint32))
     d_win = torch.from_numpy(w["init_recent"].view(np.int32)).cuda().reshape(1, w["W"])
     d_u = torch.zeros(1, dtype=torch.float32, device="cuda")
     d_tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     s = gs.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
+    toks = [s.sample(d_lg[0], win) for _ in range(reps)]
     st = torch.cuda.current_stream()
     for _ in range(reps):
         s.sample_batch(d_lg, d_tok, recent=d_win, u=d_u, stream=st)
         torch.cuda.synchronize()
-    log("c1 isolated: %d launches, token %d" % (reps, int(d_tok[0])))
+    log("c1 isolated: %d + %d launches, tokens %d / %d" % (reps, reps, toks[-1], int(d_tok[0])))
 
 
 def calib_copy(torch, nbytes=1 << 30, reps=5):
@@ -215,7 +220,7 @@ def main():
     ap.add_argument("--c3-only", action="store_true",
                     help="time only the c3 batch (for counter runs)")
     ap.add_argument("--c1-kernel", action="store_true",
-                    help="only 50 isolated single-row launches of the c1 kernel (for profiling)")
+                    help="only isolated single-row launches of the c1 kernels (for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 1 GiB device copy 5x (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -262,7 +267,8 @@ def main():
                      "frac": achieved / PEAK_HBM_GBS, "traffic": profiled_traffic(),
                      "kernel": "gs::sample_rows_kernel", "bytes_per_launch": c3["bytes"]},
         "c1_latency": {"p50_us": c1["p50_us"], "p90_us": c1["p90_us"], "call": "gs_sample via the C ABI",
-                       "p50_us_python_wrapper": c1["p50_us_python"], "kernel_us": c1k,
+                       "p50_us_python_wrapper": c1["p50_us_python"],
+                       "kernel_us_batch_entry": c1k,
                        "V": 32000, "B": 1, "steps": 256},
     }
     if not args.no_cpu:
