@@ -169,6 +169,65 @@ def c1_isolated(gs, torch, reps=50):
     log("c1 isolated: %d + %d launches, tokens %d / %d" % (reps, reps, toks[-1], int(d_tok[0])))
 
 
+def bench_gemv(gs, torch, steps=50, warmup=5, cpu=True):
+    """The logits projection before the sampler (src/model/llama.rs:333-334):
+    Qwen2.5-7B's output matrix, Q6_K [152064 x 3584] (the output.weight of a
+    Q4_K_M file), synthetic blocks, one f32 vector (the reference's decode
+    step).  Timed with HIP events on the launch stream; bytes = the matrix's
+    GGUF bytes + x + logits.  A sample of rows is checked against the oracle's
+    exact value, and the oracle's matvec (the reference's CPU path) is timed
+    on a bounded sample of rows."""
+    import workloads
+    qt, rows, cols = workloads.Q6_K, 152064, 3584
+    blocks = workloads.synth_qblocks(qt, rows, cols, seed=11)
+    m = gs.QMatrix(qt, blocks, rows, cols)
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal(cols).astype(np.float32)
+    d_x = torch.from_numpy(x).cuda()
+    d_o = torch.empty(rows, dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream()
+    for _ in range(warmup):
+        m.gemv(d_x, d_o, stream=st)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        m.gemv(d_x, d_o, stream=st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    nbytes = workloads.qmatrix_bytes(qt, rows, cols) + 4 * cols + 4 * rows
+    out = {"kernel": "gs::q6k_gemv_xreg", "qtype": "Q6_K", "rows": rows, "cols": cols, "B": 1,
+           "us": us, "bytes_per_launch": nbytes,
+           "roofline": {"bound": "hbm", "achieved": nbytes / us / 1e3, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": nbytes / us / 1e3 / PEAK_HBM_GBS}}
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        got = d_o.cpu().numpy()
+        rb = workloads.qmatrix_bytes(qt, 1, cols)
+        sample = np.sort(rng.choice(rows, 4096, replace=False))
+        sub = np.ascontiguousarray(blocks.reshape(rows, rb)[sample]).reshape(-1)
+        nthr = min(16, os.cpu_count() or 1)
+        ex, ab = oracle.matvec(qt, sub, len(sample), cols, x, nthreads=nthr, exact=True)
+        smax = np.abs(blocks.reshape(-1, 210)[:, 192:208].view(np.int8)).max() * \
+            blocks.reshape(-1, 210)[:, 208:210].copy().view(np.float16).astype(np.float64).max()
+        tol = 2.0 ** -16 * (ab + 64 * smax * np.abs(x).astype(np.float64).sum())
+        out["rows_checked"] = int(len(sample))
+        out["rows_within_tolerance"] = int((np.abs(got[sample] - ex) <= tol).sum())
+        t0 = oracle.now()
+        oracle.matvec(qt, sub, len(sample), cols, x, nthreads=nthr)
+        t1 = oracle.now()
+        cpu_us = (t1 - t0) / len(sample) * rows * 1e6
+        out["cpu_baseline"] = {"value": cpu_us, "unit": "us per full matvec (extrapolated)", "cores": nthr,
+                               "kind": "port",
+                               "sample": "oracle matvec (src/tensor/dequant.rs:277-318 restated) on %d "
+                                         "random rows of the %d, %d threads" % (len(sample), rows, nthr)}
+    m.close()
+    return out
+
+
 def calib_copy(torch, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of a known size: its FETCH_SIZE and
     WRITE_SIZE per dispatch give the scale factor of those counters."""
@@ -221,6 +280,8 @@ def main():
                     help="time only the c3 batch (for counter runs)")
     ap.add_argument("--c1-kernel", action="store_true",
                     help="only isolated single-row launches of the c1 kernels (for profiling)")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the Q6_K logits projection (for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 1 GiB device copy 5x (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -238,6 +299,10 @@ def main():
     if args.c1_kernel:
         c1_isolated(gs, torch)
         return
+    if args.gemv_only:
+        g = bench_gemv(gs, torch, steps=args.steps, warmup=args.warmup, cpu=False)
+        log("gemv: %.1f us, %.0f GB/s" % (g["us"], g["roofline"]["achieved"]))
+        return
     c3 = bench_c3(gs, torch, args.steps, args.warmup)
     log("c3: %.3f ms/step" % c3["ms"])
     if args.c3_only:
@@ -246,6 +311,9 @@ def main():
     log("c1: p50 %.1f us (C ABI), %.1f us (Python wrapper)" % (c1["p50_us"], c1["p50_us_python"]))
     c1k = kernel_only_c1(gs, torch)
     log("c1 kernel: %.1f us" % c1k)
+    gemv = bench_gemv(gs, torch, cpu=not args.no_cpu)
+    log("lm_head gemv: %.1f us, %.0f GB/s (%.1f%% of peak)" % (
+        gemv["us"], gemv["roofline"]["achieved"], 100 * gemv["roofline"]["frac"]))
     value = c3["B"] / (c3["ms"] / 1e3)
     achieved = c3["bytes"] / (c3["ms"] / 1e3) / 1e9
     out = {
@@ -270,6 +338,7 @@ def main():
                        "p50_us_python_wrapper": c1["p50_us_python"],
                        "kernel_us_batch_entry": c1k,
                        "V": 32000, "B": 1, "steps": 256},
+        "lm_head_gemv": gemv,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(c3)

@@ -1,0 +1,497 @@
+// gs_gemv.hip -- gfx950 quantized matrix-vector product that produces the
+// logits (the reference's output projection, src/model/llama.rs:333-334 on
+// the GPU path, :405-407 on the CPU path), for Q8_0 and Q6_K weights.
+//
+// HBM-bound: every weight byte is read once per call and nothing else of
+// size moves.  Device layout (rearranged at upload from the GGUF blocks, the
+// same 210 / 34 bytes per block as the file), chosen so that every load
+// instruction of a wave reads one contiguous run of memory:
+//   Q6_K: three planes of 16-byte chunks, one chunk per quarter block and
+//         plane (ql[64h + l0 ..], ql[64h + 32 + l0 ..], qh[32h + l0 ..] for
+//         quarter (h, l0), see below), indexed row * 4nb + quarter; a plane of
+//         32-bit words, the quarter's four int8 scales; the f16 d per block.
+//   Q8_0: 16-byte chunks of int8 quants, row * 2nb + half block; f16 d per block.
+// Weight loads are non-temporal (each byte is used once).
+//
+// One wave per row, rows strided over all waves of the grid.  A lane takes a
+// fixed slice of the columns (Q6_K: a quarter block, 64 weights = 16 values
+// of l in one half of a block; Q8_0: half blocks of 16 weights), so its slice
+// of x stays in registers for every row the wave visits (when a row fits in
+// one pass of the wave, cols <= 4096), with the sums of x over its 16-weight
+// groups.  Weights are decoded four to a 32-bit word and converted with the
+// byte-to-float instructions; the offset of the stored values (Q6_K q + 32,
+// Q8_0 q + 128 after flipping the sign bit) is taken out once per group:
+// sum (u - o) x = sum u x - o * sum x.  The next row's loads are issued
+// before the current row is computed.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+#include <new>
+
+#include "../../include/gs_gemv.h"
+#include "../../include/gs_sampler.h"
+
+namespace gs {
+
+constexpr int kGemvThreads = 256;       // 4 waves per workgroup
+constexpr int kMaxCols = 16384;         // x staged in LDS (64 KB) on the general path
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Streaming loads of the weights (read once per call: non-temporal).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ntl4(const void *p)
+{
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ntl2(const void *p)
+{
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
+    return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// Row sums of kRB rows at once (kRB = 4, 8 or 16): each lane's partial of
+// row k is written to the wave's LDS tile t[k][lane]; lane L then adds the
+// 64 kRB / 64 partials t[L % kRB][..] of its share, and log2(64 / kRB)
+// shuffles combine the shares.  Lanes 0 .. kRB-1 return the sums of rows
+// 0 .. kRB-1.
+template <int kRB>
+__device__ __forceinline__ float rows_sum(float (&part)[kRB], float *t)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < kRB; k++) t[k * 64 + lane] = part[k];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    constexpr int kC = 64 / kRB;           // lanes per row, 64 / kC partials each
+    const float4 *q = reinterpret_cast<const float4 *>(t + (lane % kRB) * 64 + (64 / kC) * (lane / kRB));
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16 / kC; i++) {
+        const float4 v = q[i];
+        s += (v.x + v.y) + (v.z + v.w);
+    }
+#pragma unroll
+    for (int d = kRB; d < 64; d <<= 1) s += __shfl_xor(s, d, 64);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();       // the tile is free for the next batch
+    return s;
+}
+
+// Bytes 0..3 of a word as floats (v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ float ub(uint32_t w, int t) { return (float)((w >> (8 * t)) & 0xffu); }
+
+// ---------------------------------------------------------------- Q6_K -----
+// Quarter qi of a row: block j = qi / 4, half h = (qi / 2) % 2, l0 = 16 (qi % 2).
+// Its 64 weights sit at 256 j + 128 h + 32 g + l, g = 0..3, l = l0 .. l0 + 15
+// (src/tensor/dequant.rs:203-214): group g takes the low nibble of
+// ql[64h + l] (g 0) / ql[64h + 32 + l] (g 1), the high nibbles (g 2, 3), and
+// bits 2g..2g+1 of qh[32h + l]; its scale is sc[8h + l0/16 + 2g].
+struct Q6Quarter {
+    uint4 a, b, c;      // ql[64h + l0 ..], ql[64h + 32 + l0 ..], qh[32h + l0 ..]
+    uint32_t s;         // byte g: sc[8h + l0/16 + 2g]
+    uint16_t d;
+};
+
+// Planes of a Q6_K matrix on the device (see the layout above); e indexes
+// quarters (row * 4nb + quarter), blocks are e / 4.
+struct Q6Planes {
+    const uint8_t *a, *b, *c;
+    const uint32_t *s;
+    const uint16_t *d;
+};
+
+// e < 2^28 (the upload limits a plane to 4 GB): 32-bit offsets from the
+// wave-uniform plane bases.
+__device__ __forceinline__ Q6Quarter q6_load(const Q6Planes &P, uint32_t e)
+{
+    Q6Quarter q;
+    q.a = ntl4(P.a + e * 16u);
+    q.b = ntl4(P.b + e * 16u);
+    q.c = ntl4(P.c + e * 16u);
+    q.s = __builtin_nontemporal_load(P.s + e);
+    q.d = __builtin_nontemporal_load(P.d + (e >> 2));
+    return q;
+}
+
+// sum over the quarter's four groups of scale_g * sum (u - 32) x.
+// xg[g][i] = x at the group's i-th weight, sx[g] = sum of xg[g].
+__device__ __forceinline__ float q6_dot(const Q6Quarter &q, const float (&xg)[4][16], const float (&sx)[4])
+{
+    float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t A[4] = {q.a.x, q.a.y, q.a.z, q.a.w};
+    const uint32_t B[4] = {q.b.x, q.b.y, q.b.z, q.b.w};
+    const uint32_t C[4] = {q.c.x, q.c.y, q.c.z, q.c.w};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t a = A[w], b = B[w], c = C[w];
+        const uint32_t u[4] = {(a & 0x0F0F0F0Fu) | ((c & 0x03030303u) << 4),
+                               (b & 0x0F0F0F0Fu) | ((c & 0x0C0C0C0Cu) << 2),
+                               ((a >> 4) & 0x0F0F0F0Fu) | (c & 0x30303030u),
+                               ((b >> 4) & 0x0F0F0F0Fu) | ((c >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) dot[g] = fmaf(ub(u[g], t), xg[g][4 * w + t], dot[g]);
+    }
+    const float d = h2f(q.d);
+    float acc = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const float scl = d * (float)(int8_t)(uint8_t)(q.s >> (8 * g));   // (d * scale), as the reference
+        acc = fmaf(scl, fmaf(-32.0f, sx[g], dot[g]), acc);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ void q6_xslice(const float *x, int j, int h, int l0, float (&xg)[4][16], float (&sx)[4])
+{
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const float4 *p = reinterpret_cast<const float4 *>(x + 256 * j + 128 * h + 32 * g + l0);
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = p[i];
+            xg[g][4 * i] = v.x; xg[g][4 * i + 1] = v.y; xg[g][4 * i + 2] = v.z; xg[g][4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) s += xg[g][i];
+        sx[g] = s;
+    }
+}
+
+// Rows of up to 16 blocks (cols <= 4096): one quarter per lane, x in
+// registers.  One 1024-thread workgroup per CU stages x in LDS once; each
+// wave then takes a contiguous run of rows.
+constexpr int kRegThreads = 1024;
+template <int kRB>
+__global__ void __launch_bounds__(kRegThreads)
+q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[4096];
+    __shared__ float tiles[kRegThreads / 64][kRB * 64];
+    const int cols = 256 * nb;
+    for (int i = threadIdx.x; i < cols; i += kRegThreads) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (kRegThreads / 64);
+    const int gw = blockIdx.x * (kRegThreads / 64) + (threadIdx.x >> 6);
+    const int NQ = 4 * nb;
+    const bool act = lane < NQ;
+    const int qi = act ? lane : 0;
+    const int j = qi >> 2, h = (qi >> 1) & 1, l0 = (qi & 1) * 16;
+    float xg[4][16], sx[4];
+    q6_xslice(xs, j, h, l0, xg, sx);
+    const int rpw = (rows + nw - 1) / nw;
+    const int r0 = gw * rpw, r1 = min(rows, r0 + rpw);
+    if (r0 >= r1) return;
+    float *tile = tiles[threadIdx.x >> 6];
+    const uint32_t e0 = (uint32_t)r0 * NQ + qi, e1 = (uint32_t)(r1 - 1) * NQ + qi;
+    Q6Quarter cur = q6_load(P, e0);
+    int rb = r0;
+    // full batches: the next row's loads are issued before this row is
+    // computed (the last row of the wave reloads itself)
+    for (; rb + kRB <= r1; rb += kRB) {
+        float part[kRB];
+#pragma unroll
+        for (int k = 0; k < kRB; k++) {
+            const Q6Quarter nxt = q6_load(P, min((uint32_t)(rb + k + 1) * NQ + qi, e1));
+            part[k] = act ? q6_dot(cur, xg, sx) : 0.0f;
+            cur = nxt;
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB) out[rb + lane] = v;
+    }
+    if (rb < r1) {                             // the last, partial batch
+        float part[kRB];
+#pragma unroll
+        for (int k = 0; k < kRB; k++) {
+            part[k] = 0.0f;
+            if (rb + k < r1) {                 // wave-uniform
+                if (act) part[k] = q6_dot(cur, xg, sx);
+                cur = q6_load(P, min((uint32_t)(rb + k + 1) * NQ + qi, e1));
+            }
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB && rb + lane < r1) out[rb + lane] = v;
+    }
+}
+
+// Any row length up to kMaxCols: x staged in LDS, lanes loop over quarters.
+__global__ void __launch_bounds__(kGemvThreads)
+q6k_gemv_lds(Q6Planes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[kMaxCols];
+    const int cols = 256 * nb;
+    for (int i = threadIdx.x; i < cols; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (kGemvThreads / 64);
+    const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+    const int NQ = 4 * nb;
+    for (int r = gw; r < rows; r += nw) {
+        float v = 0.0f;
+        for (int qi = lane; qi < NQ; qi += 64) {
+            const int j = qi >> 2, h = (qi >> 1) & 1, l0 = (qi & 1) * 16;
+            float xg[4][16], sx[4];
+            q6_xslice(xs, j, h, l0, xg, sx);
+            v += q6_dot(q6_load(P, (uint32_t)r * NQ + qi), xg, sx);
+        }
+        v = wave_sum(v);
+        if (lane == 0) out[r] = v;
+    }
+}
+
+// ---------------------------------------------------------------- Q8_0 -----
+// Half block hb of a row: block hb / 2, weights 32 (hb / 2) + 16 (hb % 2) .. + 15.
+__device__ __forceinline__ float q8_dot(uint4 q, uint16_t d16, const float *xs16, float sx)
+{
+    const uint32_t W[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+    float dot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) dot = fmaf(ub(W[w], t), xs16[4 * w + t], dot);
+    return h2f(d16) * fmaf(-128.0f, sx, dot);
+}
+
+#ifndef GS_RB6
+#define GS_RB6 8
+#endif
+#ifndef GS_RB8
+#define GS_RB8 4
+#endif
+constexpr int kRB6 = GS_RB6, kRB8 = GS_RB8;   // rows per reduction batch (Q6_K, Q8_0)
+constexpr int kQ8Halves = 4;            // half blocks per lane on the register path (cols <= 4096)
+
+template <int kRB>
+__global__ void __launch_bounds__(kRegThreads)
+q80_gemv_xreg(const uint8_t *bits, const uint16_t *dq, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[4096];
+    __shared__ float tiles[kRegThreads / 64][kRB * 64];
+    const int cols = 32 * nb;
+    for (int i = threadIdx.x; i < cols; i += kRegThreads) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (kRegThreads / 64);
+    const int gw = blockIdx.x * (kRegThreads / 64) + (threadIdx.x >> 6);
+    const int nh = 2 * nb;
+    float xv[kQ8Halves][16], sx[kQ8Halves];
+    bool act[kQ8Halves];
+    int hb[kQ8Halves];
+#pragma unroll
+    for (int k = 0; k < kQ8Halves; k++) {
+        act[k] = lane + 64 * k < nh;
+        hb[k] = act[k] ? lane + 64 * k : 0;
+        const float4 *p = reinterpret_cast<const float4 *>(xs + 16 * hb[k]);
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = p[i];
+            xv[k][4 * i] = v.x; xv[k][4 * i + 1] = v.y; xv[k][4 * i + 2] = v.z; xv[k][4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) s += xv[k][i];
+        sx[k] = s;
+    }
+    const int rpw = (rows + nw - 1) / nw;
+    const int r0 = gw * rpw, r1 = min(rows, r0 + rpw);
+    if (r0 >= r1) return;
+    auto load = [&](int r, uint4 (&q)[kQ8Halves], uint16_t (&d)[kQ8Halves]) {
+#pragma unroll
+        for (int k = 0; k < kQ8Halves; k++) {
+            const size_t e = (size_t)r * nh + hb[k];
+            q[k] = ntl4(bits + e * 16);
+            d[k] = __builtin_nontemporal_load(dq + (e >> 1));
+        }
+    };
+    float *tile = tiles[threadIdx.x >> 6];
+    uint4 cq[kQ8Halves];
+    uint16_t cd[kQ8Halves];
+    load(r0, cq, cd);
+    for (int rb = r0; rb < r1; rb += kRB) {
+        float part[kRB];
+#pragma unroll
+        for (int kk = 0; kk < kRB; kk++) {
+            const int r = rb + kk;
+            part[kk] = 0.0f;
+            if (r < r1) {                      // wave-uniform
+                uint4 nq[kQ8Halves];
+                uint16_t nd[kQ8Halves];
+                load(min(r + 1, r1 - 1), nq, nd);
+                float v = 0.0f;
+#pragma unroll
+                for (int k = 0; k < kQ8Halves; k++)
+                    if (act[k]) v += q8_dot(cq[k], cd[k], xv[k], sx[k]);
+                part[kk] = v;
+#pragma unroll
+                for (int k = 0; k < kQ8Halves; k++) { cq[k] = nq[k]; cd[k] = nd[k]; }
+            }
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB && rb + lane < r1) out[rb + lane] = v;
+    }
+}
+
+__global__ void __launch_bounds__(kGemvThreads)
+q80_gemv_lds(const uint8_t *bits, const uint16_t *dq, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[kMaxCols];
+    const int cols = 32 * nb;
+    for (int i = threadIdx.x; i < cols; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (kGemvThreads / 64);
+    const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+    for (int r = gw; r < rows; r += nw) {
+        float v = 0.0f;
+        for (int hbk = lane; hbk < 2 * nb; hbk += 64) {
+            const size_t blk = (size_t)r * nb + (hbk >> 1);
+            const uint4 q = ntl4(bits + blk * 32 + 16 * (hbk & 1));
+            const float *xp = xs + 16 * hbk;
+            float s = 0.0f;
+            for (int i = 0; i < 16; i++) s += xp[i];
+            v += q8_dot(q, __builtin_nontemporal_load(dq + blk), xp, s);
+        }
+        v = wave_sum(v);
+        if (lane == 0) out[r] = v;
+    }
+}
+
+} // namespace gs
+
+// ------------------------------------------------------------- host side ---
+struct gs_qmatrix {
+    uint32_t qtype;
+    size_t rows, cols, nb;     // nb: blocks per row
+    int device;
+    int cus;                   // compute units: one 1024-thread workgroup each on the register paths
+    uint8_t *base;             // one device allocation holding the planes
+    gs::Q6Planes q6;           // Q6_K
+    const uint8_t *q8;         // Q8_0: int8 quants
+    const uint16_t *d;         // f16 d per block (both types)
+};
+
+extern "C" {
+
+int gs_qmatrix_upload(uint32_t qtype, const void *blocks, size_t rows, size_t cols, gs_qmatrix **out)
+{
+    if (!out) return GS_ERR_INVALID;
+    *out = nullptr;
+    if (!blocks || rows == 0 || cols == 0) return GS_ERR_INVALID;
+    if (qtype != GS_QTYPE_Q8_0 && qtype != GS_QTYPE_Q6_K) return GS_ERR_UNSUPPORTED;
+    const bool q6 = qtype == GS_QTYPE_Q6_K;
+    const size_t bw = q6 ? 256 : 32;        // weights per block
+    const size_t bb = q6 ? 210 : 34;        // bytes per GGUF block
+    if (cols % bw != 0 || cols > (size_t)gs::kMaxCols || rows > 0x7fffffffu) return GS_ERR_UNSUPPORTED;
+    if (rows * (cols / 64) >= (1ull << 28)) return GS_ERR_UNSUPPORTED;   // 32-bit chunk offsets
+    const size_t nb = cols / bw, n = rows * nb;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    // planes: Q6_K a | b | c (64 bytes per block each) | scale words (16) | d (2);
+    //         Q8_0 quants (32 bytes per block) | d (2)
+    const size_t pa = q6 ? al(n * 64) : al(n * 32);
+    const size_t off_b = pa, off_c = q6 ? 2 * pa : pa, off_s = q6 ? 3 * pa : pa;
+    const size_t off_d = q6 ? off_s + al(n * 16) : pa;
+    const size_t total = off_d + n * 2;
+    uint8_t *h = new (std::nothrow) uint8_t[total];
+    if (!h) return GS_ERR_NOMEM;
+    const uint8_t *src = (const uint8_t *)blocks;
+    for (size_t i = 0; i < n; i++) {
+        const uint8_t *b = src + i * bb;
+        if (q6) {
+            // quarter qq = 2h + l0/16 of block i: element e = 4i + qq of each plane
+            for (int qq = 0; qq < 4; qq++) {
+                const int hh = qq >> 1, l0 = (qq & 1) * 16, is = l0 / 16;
+                const size_t e = 4 * i + qq;
+                memcpy(h + e * 16, b + 64 * hh + l0, 16);                  // ql[64h + l0 ..]
+                memcpy(h + off_b + e * 16, b + 64 * hh + 32 + l0, 16);     // ql[64h + 32 + l0 ..]
+                memcpy(h + off_c + e * 16, b + 128 + 32 * hh + l0, 16);    // qh[32h + l0 ..]
+                for (int g = 0; g < 4; g++) h[off_s + e * 4 + g] = b[192 + 8 * hh + is + 2 * g];
+            }
+            memcpy(h + off_d + i * 2, b + 208, 2);
+        } else {
+            memcpy(h + i * 32, b + 2, 32);
+            memcpy(h + off_d + i * 2, b, 2);
+        }
+    }
+    gs_qmatrix *m = new (std::nothrow) gs_qmatrix();
+    if (!m) { delete[] h; return GS_ERR_NOMEM; }
+    m->qtype = qtype; m->rows = rows; m->cols = cols; m->nb = nb;
+    if (hipGetDevice(&m->device) != hipSuccess ||
+        hipDeviceGetAttribute(&m->cus, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess) {
+        delete[] h; delete m; return GS_ERR_HIP;
+    }
+    if (m->cus <= 0) m->cus = 256;
+    if (hipMalloc((void **)&m->base, total) != hipSuccess) {
+        (void)hipGetLastError(); delete[] h; delete m; return GS_ERR_NOMEM;
+    }
+    const hipError_t ce = hipMemcpy(m->base, h, total, hipMemcpyHostToDevice);
+    delete[] h;
+    if (ce != hipSuccess) { (void)hipFree(m->base); delete m; return GS_ERR_HIP; }
+    m->d = (const uint16_t *)(m->base + off_d);
+    if (q6) m->q6 = gs::Q6Planes{m->base, m->base + off_b, m->base + off_c, (const uint32_t *)(m->base + off_s), m->d};
+    else m->q8 = m->base;
+    *out = m;
+    return GS_OK;
+}
+
+int gs_qmatrix_destroy(gs_qmatrix *m)
+{
+    if (!m) return GS_ERR_INVALID;
+    int dev;
+    (void)hipGetDevice(&dev);
+    (void)hipSetDevice(m->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(m->base);
+    (void)hipSetDevice(dev);
+    delete m;
+    return GS_OK;
+}
+
+int gs_qmatrix_shape(const gs_qmatrix *m, uint32_t *qtype, size_t *rows, size_t *cols)
+{
+    if (!m) return GS_ERR_INVALID;
+    if (qtype) *qtype = m->qtype;
+    if (rows) *rows = m->rows;
+    if (cols) *cols = m->cols;
+    return GS_OK;
+}
+
+int gs_gemv(const gs_qmatrix *m, const float *d_x, size_t B, float *d_out, void *stream)
+{
+    if (!m || (B > 0 && (!d_x || !d_out))) return GS_ERR_INVALID;
+    if (((uintptr_t)d_x & 15u) != 0 || (B > 1 && (m->cols & 3) != 0)) return GS_ERR_INVALID;   // x is read as float4
+    const hipStream_t st = (hipStream_t)stream;
+    const int rows = (int)m->rows, nb = (int)m->nb;
+    for (size_t b = 0; b < B; b++) {
+        const float *x = d_x + b * m->cols;
+        float *o = d_out + b * m->rows;
+        if (m->qtype == GS_QTYPE_Q6_K) {
+            if (4 * nb <= 64)
+                hipLaunchKernelGGL(gs::q6k_gemv_xreg<gs::kRB6>, dim3(m->cus), dim3(gs::kRegThreads), 0, st, m->q6, x, o, rows, nb);
+            else
+                hipLaunchKernelGGL(gs::q6k_gemv_lds, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q6, x, o, rows, nb);
+        } else {
+            if (2 * nb <= 64 * gs::kQ8Halves)
+                hipLaunchKernelGGL(gs::q80_gemv_xreg<gs::kRB8>, dim3(m->cus), dim3(gs::kRegThreads), 0, st, m->q8, m->d, x, o, rows, nb);
+            else
+                hipLaunchKernelGGL(gs::q80_gemv_lds, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q8, m->d, x, o, rows, nb);
+        }
+        if (hipGetLastError() != hipSuccess) return GS_ERR_HIP;
+    }
+    return GS_OK;
+}
+
+} // extern "C"

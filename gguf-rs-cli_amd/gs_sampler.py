@@ -43,6 +43,8 @@ EXPORTS = [
     "gs_sampler_set_seed", "gs_sampler_get_state", "gs_sampler_set_state",
     "gs_sampler_reserve", "gs_sample", "gs_sample_batch", "gs_window_push",
     "gs_synth_logits", "gs_limits", "gs_version",
+    # include/gs_gemv.h
+    "gs_qmatrix_upload", "gs_qmatrix_destroy", "gs_qmatrix_shape", "gs_gemv",
 ]
 
 
@@ -83,6 +85,10 @@ def load_library(path=LIB_PATH):
         "gs_synth_logits": ([P, SZ, SZ, SZ, U64, U64, ctypes.c_float, P], I),
         "gs_limits": ([ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)], I),
         "gs_version": ([], ctypes.c_char_p),
+        "gs_qmatrix_upload": ([ctypes.c_uint32, P, SZ, SZ, ctypes.POINTER(P)], I),
+        "gs_qmatrix_destroy": ([P], I),
+        "gs_qmatrix_shape": ([P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(SZ), ctypes.POINTER(SZ)], I),
+        "gs_gemv": ([P, P, SZ, P, P], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -302,3 +308,45 @@ def sample(logits, temperature, top_k, top_p, rep_penalty, recent):
     g = _get_global()
     g.set_params(temperature, top_k, top_p, rep_penalty)
     return g.sample(logits, recent)
+
+
+# ---- quantized output projection (include/gs_gemv.h) --------------------------
+QTYPE_Q8_0 = 8     # GgmlType::Q8_0 (src/gguf/types.rs:45)
+QTYPE_Q6_K = 14    # GgmlType::Q6K  (src/gguf/types.rs:47)
+
+
+class QMatrix:
+    """A quantized matrix on the device: Gpu::upload (src/gpu/mod.rs:222-238)
+    of a Q8_0 / Q6_K GGUF tensor.  `blocks` are the tensor's raw bytes (a
+    numpy uint8 array or bytes), rows x cols weights, cols = dims[0].
+    gemv(x, out) is Gpu::cmd_gemv (src/gpu/mod.rs:438-443): out = W x for
+    device f32 vectors (torch tensors or device addresses), B = len(x) / cols
+    vectors per call."""
+
+    def __init__(self, qtype, blocks, rows, cols):
+        import numpy as np
+        self._lib = load_library()
+        b = np.ascontiguousarray(np.frombuffer(blocks, dtype=np.uint8) if isinstance(blocks, (bytes, bytearray))
+                                 else blocks, dtype=np.uint8)
+        h = ctypes.c_void_p()
+        _check(self._lib.gs_qmatrix_upload(qtype, b.ctypes.data, rows, cols, ctypes.byref(h)),
+               "gs_qmatrix_upload")
+        self._h = h
+        self.qtype, self.rows, self.cols = qtype, rows, cols
+
+    def gemv(self, x, out, B=1, stream=None):
+        st = None
+        if stream is not None:
+            st = stream.cuda_stream if hasattr(stream, "cuda_stream") else stream
+        _check(self._lib.gs_gemv(self._h, _ptr(x), B, _ptr(out), st), "gs_gemv")
+
+    def close(self):
+        if self._h:
+            self._lib.gs_qmatrix_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -97,3 +97,32 @@ def algorithmic_bytes_per_row(V, W, hetero=False, window_append=False):
     """One read of the row, the window (if the penalty is active), the draw,
     the token write, per-row params (heterogeneous only), window append."""
     return 4 * V + 4 * W + 4 + 4 + (16 if hetero else 0) + (4 if window_append else 0)
+
+
+# ---- quantized output matrices (the logits projection) ------------------------
+# GGUF block sizes (src/gguf/types.rs:62-71): Q8_0 34 bytes / 32 weights,
+# Q6_K 210 bytes / 256 weights.
+Q8_0, Q6_K = 8, 14
+QBLOCK = {Q8_0: (32, 34), Q6_K: (256, 210)}
+
+
+def qmatrix_bytes(qtype, rows, cols):
+    w, b = QBLOCK[qtype]
+    return rows * (cols // w) * b
+
+
+def synth_qblocks(qtype, rows, cols, seed=0, dscale=0.002):
+    """Seeded random GGUF blocks for a rows x cols matrix: uniform quant bits,
+    int8 sub-block scales and small positive f16 block scales (values like a
+    trained output matrix's, about 1e-3..1e-2 per weight)."""
+    w, nb = QBLOCK[qtype]
+    rng = np.random.default_rng(seed)
+    n = rows * (cols // w)
+    blk = rng.integers(0, 256, size=(n, nb), dtype=np.uint8)
+    d = (rng.random(n) * dscale + dscale / 4).astype(np.float16).view(np.uint8).reshape(n, 2)
+    if qtype == Q8_0:
+        blk[:, 0:2] = d
+    else:
+        blk[:, 192:208] = rng.integers(-64, 64, size=(n, 16)).astype(np.int8).view(np.uint8)
+        blk[:, 208:210] = d
+    return blk.reshape(-1)

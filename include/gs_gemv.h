@@ -1,0 +1,64 @@
+/*
+ * gs_gemv.h -- C ABI of the gfx950 quantized GEMV that produces the logits.
+ *
+ * The step before the sampler in gguf-rs-cli's decode (src/model/llama.rs:333-334):
+ * the output projection `gpu.cmd_gemv(output, &xn, &logits)`, one f32 logit per
+ * row of the quantized output matrix.  The reference uploads a GGUF tensor with
+ *
+ *   pub fn upload(&mut self, wt: &QuantTensor) -> Option<GpuTensor>   src/gpu/mod.rs:222-238
+ *
+ * (repacking the blocks with pack_q6k_for_gpu / pack_q8_0_for_gpu,
+ * src/tensor/dequant.rs:369-409) and runs
+ *
+ *   pub fn cmd_gemv(&mut self, wt: &GpuTensor, inp: &ActBuf, out: &ActBuf)   src/gpu/mod.rs:438-443
+ *
+ * with the Q6_K or Q8_0 shader (src/gpu/q6k_gemv.glsl, src/gpu/q8_0_gemv.glsl).
+ * Its CPU path is QuantTensor::matvec / row_dot (src/tensor/dequant.rs:277-318).
+ *
+ * Weights are the GGUF tensor's raw blocks (what QuantTensor::data() returns,
+ * src/tensor/dequant.rs:265-267): Q8_0 = 34 bytes per 32 weights (f16 d, 32 int8),
+ * Q6_K = 210 bytes per 256 weights (ql[128], qh[64], int8 scales[16], f16 d).
+ * The result is out[r] = sum_c W[r][c] * x[c], W dequantized as the reference
+ * does it (Q8_0: q * d; Q6_K: (d * scale) * q); the summation order is the
+ * kernel's own, so results agree with the reference's to f32 rounding, not bit
+ * for bit.  Same status codes as gs_sampler.h.
+ */
+#ifndef GS_GEMV_H
+#define GS_GEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Block types, numbered as GgmlType (src/gguf/types.rs:43-48). */
+#define GS_QTYPE_Q8_0  8u
+#define GS_QTYPE_Q6_K  14u
+
+typedef struct gs_qmatrix gs_qmatrix;
+
+/* Replaces Gpu::upload (src/gpu/mod.rs:222-238) for Q8_0 and Q6_K tensors.
+ * `blocks` is a host pointer to rows*cols weights in GGUF block order
+ * (row-major, dims[0] = cols as in QuantTensor::new, src/tensor/dequant.rs:256-263).
+ * The blocks are split into the device layout (bit planes, int8 scales, f16 d)
+ * and copied to the current HIP device; synchronous.  cols must be a multiple
+ * of the block size (32 / 256) -- where the reference's upload returns None
+ * and falls back to the CPU, this returns GS_ERR_UNSUPPORTED -- and at most
+ * 16384. */
+int gs_qmatrix_upload(uint32_t qtype, const void *blocks, size_t rows, size_t cols, gs_qmatrix **out);
+int gs_qmatrix_destroy(gs_qmatrix *m);
+int gs_qmatrix_shape(const gs_qmatrix *m, uint32_t *qtype, size_t *rows, size_t *cols);
+
+/* Replaces Gpu::cmd_gemv (src/gpu/mod.rs:438-443): for b < B,
+ * d_out[b*rows + r] = sum_c W[r][c] * d_x[b*cols + c].  Device pointers;
+ * asynchronous on `stream` (NULL = default stream).  B = 1 is the reference's
+ * decode step; each further vector is another pass over the weights. */
+int gs_gemv(const gs_qmatrix *m, const float *d_x, size_t B, float *d_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GS_GEMV_H */

@@ -1,0 +1,184 @@
+/* gemv_oracle.c -- CPU restatement of gguf-rs-cli's quantized matrix-vector
+ * product for the Q8_0 and Q6_K block types (the logits projection,
+ * src/model/llama.rs:405-407 on the CPU path).
+ * TEST INFRASTRUCTURE ONLY (parity checker); never linked into the product.
+ *
+ * Follows src/tensor/dequant.rs:
+ *   dq80      :86-94   Q8_0 dequantization, w = (q as f32) * d
+ *   dq6k      :197-219 Q6_K dequantization, w = (d * (scale as f32)) * q
+ *   row_dot   :277-313 Q8_0: per block a sequential f32 sum of (q * d) * x,
+ *                      then a sequential sum of the block sums;
+ *                      other types (Q6_K): dequantize the row, then a
+ *                      sequential f32 sum of w * x
+ *   matvec    :315-318 out[i] = row_dot(i, x), rows in parallel
+ * f16 -> f32 is the `half` crate's (2.7.1, Cargo.lock:219) to_f32, an exact
+ * conversion.  Rust's f32 Iterator::sum is a left fold, restated as a loop.
+ * Built with -ffp-contract=off: every f32 op is one IEEE op, as in Rust. */
+#include <math.h>
+#include <pthread.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define QT_Q8_0 8u
+#define QT_Q6_K 14u
+
+/* IEEE binary16 -> binary32, exact (every f16 is an f32). */
+float oracle_f16_to_f32(uint16_t h)
+{
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t ex = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    uint32_t bits;
+    if (ex == 0x1fu) {
+        bits = sign | 0x7f800000u | (man << 13);           /* inf / nan (payload kept) */
+    } else if (ex != 0) {
+        bits = sign | ((ex + 112u) << 23) | (man << 13);   /* normal: rebias 15 -> 127 */
+    } else if (man == 0) {
+        bits = sign;                                       /* +-0 */
+    } else {
+        /* subnormal: man * 2^-24, renormalised */
+        int e = -1;
+        uint32_t m = man;
+        do { m <<= 1; e++; } while (!(m & 0x400u));
+        bits = sign | ((uint32_t)(112 - e) << 23) | ((m & 0x3ffu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* dq80 (dequant.rs:86-94): n weights from n/32 blocks of 34 bytes. */
+void oracle_dequant_q8_0(const uint8_t *data, size_t n, float *o)
+{
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *d = data + b * 34;
+        const float sc = oracle_f16_to_f32(rd16(d));
+        for (int i = 0; i < 32; i++) o[b * 32 + i] = (float)(int8_t)d[2 + i] * sc;
+    }
+}
+
+/* dq6k (dequant.rs:197-219): n weights from n/256 blocks of 210 bytes. */
+void oracle_dequant_q6_k(const uint8_t *data, size_t n, float *o)
+{
+    for (size_t b = 0; b < n / 256; b++) {
+        const uint8_t *d = data + b * 210;
+        const uint8_t *ql = d, *qh = d + 128;
+        const int8_t *sc = (const int8_t *)(d + 192);
+        const float df = oracle_f16_to_f32(rd16(d + 208));
+        size_t y = b * 256, qlo = 0, qhi = 0, si = 0;
+        for (int half = 0; half < 2; half++) {
+            for (int l = 0; l < 32; l++) {
+                const int q1 = ((ql[qlo + l] & 0xF) | (((qh[qhi + l] >> 0) & 3) * 16)) - 32;
+                const int q2 = ((ql[qlo + l + 32] & 0xF) | (((qh[qhi + l] >> 2) & 3) * 16)) - 32;
+                const int q3 = ((ql[qlo + l] >> 4) | (((qh[qhi + l] >> 4) & 3) * 16)) - 32;
+                const int q4 = ((ql[qlo + l + 32] >> 4) | (((qh[qhi + l] >> 6) & 3) * 16)) - 32;
+                const int is = l / 16;
+                o[y + l] = df * (float)sc[si + is] * (float)q1;
+                o[y + l + 32] = df * (float)sc[si + is + 2] * (float)q2;
+                o[y + l + 64] = df * (float)sc[si + is + 4] * (float)q3;
+                o[y + l + 96] = df * (float)sc[si + is + 6] * (float)q4;
+            }
+            y += 128; qlo += 64; qhi += 32; si += 8;
+        }
+    }
+}
+
+static size_t row_bytes(uint32_t qt, size_t cols)
+{
+    return qt == QT_Q8_0 ? cols / 32 * 34 : cols / 256 * 210;
+}
+
+/* row_dot (dequant.rs:277-313) for one row's blocks.  `w` is scratch for
+ * `cols` floats (the Q6_K dequantized row). */
+static float row_dot(uint32_t qt, const uint8_t *d, size_t cols, const float *x, float *w)
+{
+    if (qt == QT_Q8_0) {
+        float acc = 0.0f;
+        for (size_t blk = 0; blk < cols / 32; blk++) {
+            const uint8_t *db = d + blk * 34;
+            const float sc = oracle_f16_to_f32(rd16(db));
+            float s = 0.0f;
+            for (int i = 0; i < 32; i++) s += (float)(int8_t)db[2 + i] * sc * x[blk * 32 + i];
+            acc += s;
+        }
+        return acc;
+    }
+    oracle_dequant_q6_k(d, cols, w);
+    float acc = 0.0f;
+    for (size_t i = 0; i < cols; i++) acc += w[i] * x[i];
+    return acc;
+}
+
+float oracle_row_dot(uint32_t qtype, const uint8_t *row_blocks, size_t cols, const float *x)
+{
+    float *w = (float *)malloc(sizeof(float) * (cols ? cols : 1));
+    if (!w) return NAN;
+    const float r = row_dot(qtype, row_blocks, cols, x, w);
+    free(w);
+    return r;
+}
+
+/* The exact value of the same product: the reference's f32 weights times x,
+ * summed in double (each product w*x of two f32 is exact in double, and a
+ * double sum of a few thousand of them carries a relative error below 2^-40),
+ * and the sum of |w * x| for tolerances. */
+static double row_exact(uint32_t qt, const uint8_t *d, size_t cols, const float *x, float *w, double *abs_sum)
+{
+    if (qt == QT_Q8_0) oracle_dequant_q8_0(d, cols, w);
+    else oracle_dequant_q6_k(d, cols, w);
+    double s = 0.0, a = 0.0;
+    for (size_t i = 0; i < cols; i++) {
+        const double p = (double)w[i] * (double)x[i];
+        s += p;
+        a += fabs(p);
+    }
+    *abs_sum = a;
+    return s;
+}
+
+typedef struct {
+    uint32_t qt; const uint8_t *blocks; size_t rows, cols; const float *x;
+    float *out; double *exact; double *abs_sum; size_t r0, r1;
+} job_t;
+
+static void *run_rows(void *arg)
+{
+    job_t *j = (job_t *)arg;
+    float *w = (float *)malloc(sizeof(float) * (j->cols ? j->cols : 1));
+    if (!w) return NULL;
+    const size_t rb = row_bytes(j->qt, j->cols);
+    for (size_t r = j->r0; r < j->r1; r++) {
+        const uint8_t *d = j->blocks + r * rb;
+        if (j->out) j->out[r] = row_dot(j->qt, d, j->cols, j->x, w);
+        if (j->exact) j->exact[r] = row_exact(j->qt, d, j->cols, j->x, w, &j->abs_sum[r]);
+    }
+    free(w);
+    return NULL;
+}
+
+/* matvec (dequant.rs:315-318) over `nthreads` threads (the reference uses
+ * rayon's pool; every row is computed the same way on any thread).  Either
+ * output may be NULL: `out` gets the reference's f32 results, `exact` and
+ * `abs_sum` the double values above.  Returns 0, or -1 for a bad type. */
+int oracle_matvec(uint32_t qtype, const uint8_t *blocks, size_t rows, size_t cols, const float *x,
+                  float *out, double *exact, double *abs_sum, int nthreads)
+{
+    if (qtype != QT_Q8_0 && qtype != QT_Q6_K) return -1;
+    if (nthreads < 1) nthreads = 1;
+    if ((size_t)nthreads > rows) nthreads = rows ? (int)rows : 1;
+    pthread_t th[64];
+    job_t jobs[64];
+    if (nthreads > 64) nthreads = 64;
+    for (int i = 0; i < nthreads; i++) {
+        jobs[i] = (job_t){qtype, blocks, rows, cols, x, out, exact, abs_sum,
+                          rows * (size_t)i / (size_t)nthreads, rows * (size_t)(i + 1) / (size_t)nthreads};
+        if (nthreads == 1) run_rows(&jobs[i]);
+        else pthread_create(&th[i], NULL, run_rows, &jobs[i]);
+    }
+    if (nthreads > 1)
+        for (int i = 0; i < nthreads; i++) pthread_join(th[i], NULL);
+    return 0;
+}

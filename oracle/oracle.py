@@ -3,7 +3,8 @@
 TEST INFRASTRUCTURE ONLY: the parity checker for the HIP sampler.  Imported
 by tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py;
 never by the product path.  The oracle restates gguf-rs-cli src/sampler.rs
-(see sampler_oracle.c for the per-function citations).
+(see sampler_oracle.c for the per-function citations) and the Q8_0 / Q6_K
+dequantization and matvec of src/tensor/dequant.rs (gemv_oracle.c).
 """
 import ctypes
 import os
@@ -59,6 +60,13 @@ def load(build_if_missing=True):
     lib.oracle_synth_logits.argtypes = [P, SZ, U64, U64, F]
     lib.oracle_device_loop.argtypes = [SZ, SZ, SZ, U64, F, P, P, SZ, P, P, ctypes.c_int, ctypes.c_int]
     lib.oracle_now.restype = ctypes.c_double
+    lib.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.oracle_f16_to_f32.restype = F
+    lib.oracle_dequant_q8_0.argtypes = [P, SZ, P]
+    lib.oracle_dequant_q6_k.argtypes = [P, SZ, P]
+    lib.oracle_row_dot.argtypes = [ctypes.c_uint32, P, SZ, P]
+    lib.oracle_row_dot.restype = F
+    lib.oracle_matvec.argtypes = [ctypes.c_uint32, P, SZ, SZ, P, P, P, P, ctypes.c_int]
     _lib = lib
     return lib
 
@@ -190,3 +198,47 @@ def device_loop(B, V, steps, seed, sigma, params, window, u, nthreads=1, fast_to
 
 def now():
     return load().oracle_now()
+
+
+# ---- quantized matvec (src/tensor/dequant.rs) -------------------------------
+QT_Q8_0 = 8
+QT_Q6_K = 14
+
+
+def dequant(qtype, blocks, n):
+    """dq80 / dq6k (src/tensor/dequant.rs:86-94, 197-219): n f32 weights."""
+    lib = load()
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    f = lib.oracle_dequant_q8_0 if qtype == QT_Q8_0 else lib.oracle_dequant_q6_k
+    f(b.ctypes.data, n, out.ctypes.data)
+    return out
+
+
+def row_dot(qtype, row_blocks, cols, x):
+    """QuantTensor::row_dot (src/tensor/dequant.rs:277-313), f32 result."""
+    lib = load()
+    b = np.ascontiguousarray(row_blocks, dtype=np.uint8)
+    xx = _f32(x)
+    return float(np.float32(lib.oracle_row_dot(qtype, b.ctypes.data, cols, xx.ctypes.data)))
+
+
+def matvec(qtype, blocks, rows, cols, x, nthreads=1, exact=False):
+    """QuantTensor::matvec (src/tensor/dequant.rs:315-318).  Returns the
+    reference's f32 outputs, or with exact=True (float64 exact values of the
+    reference's weights times x, float64 sums of |w x|)."""
+    lib = load()
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    xx = _f32(x)
+    if exact:
+        ex = np.empty(rows, np.float64)
+        ab = np.empty(rows, np.float64)
+        rc = lib.oracle_matvec(qtype, b.ctypes.data, rows, cols, xx.ctypes.data, None,
+                               ex.ctypes.data, ab.ctypes.data, nthreads)
+        assert rc == 0
+        return ex, ab
+    out = np.empty(rows, np.float32)
+    rc = lib.oracle_matvec(qtype, b.ctypes.data, rows, cols, xx.ctypes.data, out.ctypes.data,
+                           None, None, nthreads)
+    assert rc == 0
+    return out

@@ -30,3 +30,12 @@ def gpu():
     import gs_sampler
     gs_sampler.load_library()
     return gs_sampler
+
+
+@pytest.fixture(scope="session")
+def torch():
+    """torch with a visible GPU (GPU tests only)."""
+    import torch as _t
+    if not _t.cuda.is_available():
+        pytest.skip("no GPU")
+    return _t

@@ -8,9 +8,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def declared():
-    h = open(os.path.join(ROOT, "include", "gs_sampler.h")).read()
-    h = re.sub(r"/\*.*?\*/", "", h, flags=re.S)
-    return sorted(set(re.findall(r"\b(gs_[a-z_]+)\s*\(", h)))
+    import glob
+    names = set()
+    for path in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))):
+        h = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
+        names |= set(re.findall(r"\b(gs_[a-z_]+)\s*\(", h))
+    return sorted(names)
 
 
 def test_header_declares_api():
@@ -25,6 +28,23 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared() if not hasattr(lib, n)]
     assert not missing, missing
     assert sorted(gs_sampler.EXPORTS) == declared()
+
+
+def test_gemv_arguments_rejected_without_gpu():
+    import ctypes as C
+    import gs_sampler
+    lib = gs_sampler.load_library()
+    h = C.c_void_p()
+    blk = (C.c_uint8 * 210)()
+    assert lib.gs_qmatrix_upload(14, None, 1, 256, C.byref(h)) == gs_sampler.GS_ERR_INVALID
+    assert lib.gs_qmatrix_upload(14, blk, 1, 256, None) == gs_sampler.GS_ERR_INVALID
+    # cols not a multiple of the block size: the reference's upload returns None
+    assert lib.gs_qmatrix_upload(14, blk, 1, 128, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
+    assert lib.gs_qmatrix_upload(8, blk, 1, 48, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
+    assert lib.gs_qmatrix_upload(12, blk, 1, 256, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
+    assert lib.gs_qmatrix_upload(14, blk, 1, 256 * 65, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
+    assert lib.gs_qmatrix_destroy(None) == gs_sampler.GS_ERR_INVALID
+    assert lib.gs_gemv(None, None, 1, None, None) == gs_sampler.GS_ERR_INVALID
 
 
 def test_limits_and_version():

@@ -1,0 +1,191 @@
+"""The quantized output projection (the logits producer, src/model/llama.rs:333-334):
+CPU pins of the oracle's Q8_0 / Q6_K dequantization and matvec
+(src/tensor/dequant.rs:86-94, 197-219, 277-318), and GPU parity of gs_gemv
+(include/gs_gemv.h) against it.
+
+The GPU sums in its own order, so parity is a tolerance: with exact the
+float64 value of the reference's f32 weights times x (oracle.matvec exact=True),
+|gpu - exact| <= 2^-16 * (sum |w x| + 64 * max|d scale| * sum |x|).  The second
+term covers the per-group offset (sum (u - o) x = sum u x - o sum x) the kernel
+uses; a wrong weight index or scale moves a row by a whole |w x| term, far
+above the bound.
+"""
+import numpy as np
+import pytest
+
+Q8_0, Q6_K = 8, 14
+
+
+def _f32_bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+# ---- oracle pins (CPU) ------------------------------------------------------
+def test_f16_conversion_all_patterns(oracle):
+    """half::f16::to_f32 is an exact conversion: every pattern against numpy."""
+    lib = oracle.load()
+    h = np.arange(65536, dtype=np.uint32)
+    want = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    got = np.array([lib.oracle_f16_to_f32(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(_f32_bits(got[~nan]), _f32_bits(want[~nan]))
+
+
+def _q6_block(ql=None, qh=None, sc=None, d=1.0):
+    b = np.zeros(210, np.uint8)
+    if ql is not None:
+        b[0:128] = ql
+    if qh is not None:
+        b[128:192] = qh
+    b[192:208] = np.asarray(sc if sc is not None else np.ones(16), np.int8).view(np.uint8)
+    b[208:210] = np.array([d], np.float16).view(np.uint8)
+    return b
+
+
+def test_q6k_zero_block_and_linearity(oracle):
+    """All quant bits 0 give q = -32 everywhere; weights scale with d and with
+    each sub-block scale (16 weights per scale, in order)."""
+    sc = np.arange(1, 17)
+    w = oracle.dequant(Q6_K, _q6_block(sc=sc, d=0.5), 256)
+    assert np.array_equal(w, (-32.0 * 0.5 * np.repeat(sc, 16)).astype(np.float32))
+    w2 = oracle.dequant(Q6_K, _q6_block(sc=-sc, d=0.25), 256)
+    assert np.array_equal(w2, (32.0 * 0.25 * np.repeat(sc, 16)).astype(np.float32))
+
+
+def test_q6k_single_bit_probes(oracle):
+    """Each quant bit moves exactly one weight, by the value of that bit times
+    d * scale, at the position the GGML Q6_K layout gives it: ql byte 64h + l
+    holds weights 128h + l (low nibble) and 128h + l + 64 (high), ql byte
+    64h + 32 + l weights 128h + l + 32 and + 96; qh byte 32h + l holds bits
+    4-5 of those four weights, two bits each, in that order (0, 32, 64, 96)."""
+    base = oracle.dequant(Q6_K, _q6_block(sc=np.full(16, 3), d=2.0), 256)
+    for h in range(2):
+        for l in (0, 5, 31):
+            for nib, off in ((0, 0), (4, 64)):
+                for k, (byte, woff) in enumerate(((64 * h + l, 0), (64 * h + 32 + l, 32))):
+                    for bit in range(4):
+                        ql = np.zeros(128, np.uint8)
+                        ql[byte] = 1 << (nib + bit)
+                        w = oracle.dequant(Q6_K, _q6_block(ql=ql, sc=np.full(16, 3), d=2.0), 256)
+                        diff = np.nonzero(w != base)[0]
+                        assert list(diff) == [128 * h + l + woff + off], (h, l, nib, k, bit, diff)
+                        assert w[diff[0]] - base[diff[0]] == (1 << bit) * 6.0
+            for pair, woff in enumerate((0, 32, 64, 96)):
+                for bit in range(2):
+                    qh = np.zeros(64, np.uint8)
+                    qh[32 * h + l] = 1 << (2 * pair + bit)
+                    w = oracle.dequant(Q6_K, _q6_block(qh=qh, sc=np.full(16, 3), d=2.0), 256)
+                    diff = np.nonzero(w != base)[0]
+                    assert list(diff) == [128 * h + l + woff], (h, l, pair, bit, diff)
+                    assert w[diff[0]] - base[diff[0]] == (16 << bit) * 6.0
+
+
+def test_q8_0_bytes_and_scale(oracle):
+    """Q8_0: byte 2 + i is weight i as int8, times the f16 d in bytes 0-1."""
+    q = np.arange(-128, 128, 8, dtype=np.int8)[:32]
+    b = np.concatenate([np.array([0.125], np.float16).view(np.uint8), q.view(np.uint8)])
+    w = oracle.dequant(Q8_0, b, 32)
+    assert np.array_equal(w, q.astype(np.float32) * np.float32(0.125))
+
+
+def test_row_dot_order_and_unit_vectors(oracle):
+    """row_dot: Q6_K sums w * x left to right in f32 (numpy's sequential
+    accumulate); Q8_0 sums each block left to right, then the block sums.
+    A unit vector picks one weight exactly."""
+    import workloads
+    rng = np.random.default_rng(3)
+    for qt, cols in ((Q6_K, 512), (Q8_0, 96)):
+        blocks = workloads.synth_qblocks(qt, 1, cols, seed=5)
+        w = oracle.dequant(qt, blocks, cols)
+        x = rng.standard_normal(cols).astype(np.float32)
+        got = oracle.row_dot(qt, blocks, cols, x)
+        p = (w * x).astype(np.float32) if qt == Q6_K else None
+        if qt == Q6_K:
+            want = np.add.accumulate(p, dtype=np.float32)[-1]
+        else:
+            q = blocks.reshape(-1, 34)[:, 2:].view(np.int8).astype(np.float32)
+            d = blocks.reshape(-1, 34)[:, :2].copy().view(np.float16).astype(np.float32)
+            pb = (q * d[:, :1]).astype(np.float32) * x.reshape(-1, 32)
+            sums = np.array([np.add.accumulate(r, dtype=np.float32)[-1] for r in pb], np.float32)
+            want = np.add.accumulate(sums, dtype=np.float32)[-1]
+        assert np.float32(got) == want, (qt, got, want)
+        for k in (0, 7, cols - 1):
+            e = np.zeros(cols, np.float32)
+            e[k] = 1.0
+            assert np.float32(oracle.row_dot(qt, blocks, cols, e)) == w[k]
+
+
+def test_matvec_exact_bound(oracle):
+    """The reference's sequential f32 sums stay within n * 2^-24 * sum|w x| of
+    the exact value; matvec rows equal row_dot."""
+    import workloads
+    rng = np.random.default_rng(4)
+    for qt, rows, cols in ((Q6_K, 20, 1024), (Q8_0, 20, 1024)):
+        blocks = workloads.synth_qblocks(qt, rows, cols, seed=6)
+        x = rng.standard_normal(cols).astype(np.float32)
+        f32 = oracle.matvec(qt, blocks, rows, cols, x, nthreads=2)
+        ex, ab = oracle.matvec(qt, blocks, rows, cols, x, nthreads=2, exact=True)
+        assert np.all(np.abs(f32 - ex) <= cols * 2.0 ** -24 * ab)
+        rb = workloads.qmatrix_bytes(qt, 1, cols)
+        for r in (0, rows - 1):
+            assert np.float32(oracle.row_dot(qt, blocks[r * rb:(r + 1) * rb], cols, x)) == f32[r]
+
+
+# ---- GPU parity ---------------------------------------------------------------
+def _gpu_check(gpu, torch, oracle, qt, rows, cols, seed, B=1, x_kind="normal"):
+    import workloads
+    rng = np.random.default_rng(seed)
+    blocks = workloads.synth_qblocks(qt, rows, cols, seed=seed)
+    if x_kind == "normal":
+        x = rng.standard_normal((B, cols)).astype(np.float32)
+    elif x_kind == "spiky":
+        x = (rng.standard_normal((B, cols)) * np.exp(rng.standard_normal((B, cols)) * 2)).astype(np.float32)
+    else:
+        x = np.zeros((B, cols), np.float32)
+        x[:, rng.integers(0, cols, 3)] = 1.0
+    m = gpu.QMatrix(qt, blocks, rows, cols)
+    d_x = torch.from_numpy(x).cuda()
+    d_o = torch.full((B, rows), float("nan"), dtype=torch.float32, device="cuda")
+    m.gemv(d_x, d_o, B=B)
+    torch.cuda.synchronize()
+    got = d_o.cpu().numpy()
+    m.close()
+    if qt == Q6_K:
+        smax = np.abs(blocks.reshape(-1, 210)[:, 192:208].view(np.int8)).max() * \
+            blocks.reshape(-1, 210)[:, 208:210].copy().view(np.float16).astype(np.float64).max()
+    else:
+        smax = blocks.reshape(-1, 34)[:, :2].copy().view(np.float16).astype(np.float64).max()
+    for b in range(B):
+        ex, ab = oracle.matvec(qt, blocks, rows, cols, x[b], nthreads=8, exact=True)
+        tol = 2.0 ** -16 * (ab + 64 * smax * np.abs(x[b]).astype(np.float64).sum())
+        err = np.abs(got[b].astype(np.float64) - ex)
+        bad = np.nonzero(~(err <= tol))[0]
+        assert bad.size == 0, (qt, rows, cols, b, bad[:5], got[b][bad[:5]], ex[bad[:5]], tol[bad[:5]])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qt,rows,cols", [
+    (Q6_K, 1000, 3584),      # Qwen2.5-7B hidden size (register path, 56 of 64 lanes)
+    (Q6_K, 517, 4096),       # Llama hidden size (all 64 lanes)
+    (Q6_K, 37, 256),         # one block per row
+    (Q6_K, 300, 8192),       # LDS path
+    (Q6_K, 9, 16384),        # largest row
+    (Q8_0, 1000, 4096),      # Llama-2 hidden size (4 half blocks per lane)
+    (Q8_0, 333, 3584),
+    (Q8_0, 77, 32),          # one block per row
+    (Q8_0, 200, 8192),       # LDS path
+])
+def test_gemv_parity(gpu, torch, oracle, qt, rows, cols):
+    _gpu_check(gpu, torch, oracle, qt, rows, cols, seed=rows + cols)
+
+
+@pytest.mark.gpu
+def test_gemv_inputs(gpu, torch, oracle):
+    """Heavy-tailed and sparse x, several vectors per call, a row count below
+    the number of waves and one far above it."""
+    _gpu_check(gpu, torch, oracle, Q6_K, 2000, 3584, seed=1, x_kind="spiky")
+    _gpu_check(gpu, torch, oracle, Q8_0, 2000, 4096, seed=2, x_kind="sparse")
+    _gpu_check(gpu, torch, oracle, Q6_K, 64, 3584, seed=3, B=3)
+    _gpu_check(gpu, torch, oracle, Q6_K, 5, 1024, seed=4)
+    _gpu_check(gpu, torch, oracle, Q8_0, 40000, 1024, seed=5)
