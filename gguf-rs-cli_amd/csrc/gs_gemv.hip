@@ -172,21 +172,23 @@ __device__ __forceinline__ void q6_xslice(const float *x, int j, int h, int l0, 
 }
 
 // Rows of up to 16 blocks (cols <= 4096): one quarter per lane, x in
-// registers.  One 1024-thread workgroup per CU stages x in LDS once; each
-// wave then takes a contiguous run of rows.
-constexpr int kRegThreads = 1024;
-template <int kRB>
-__global__ void __launch_bounds__(kRegThreads)
+// registers.  One NT-thread workgroup per CU stages x in LDS once; each wave
+// then takes a contiguous run of rows and keeps the loads of the next PF rows
+// in flight while it computes one (PF divides kRB, so the ring of row
+// buffers is indexed statically).
+template <int kRB, int PF, int NT>
+__global__ void __launch_bounds__(NT)
 q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
 {
+    static_assert(kRB % PF == 0, "ring of PF row buffers, kRB rows per batch");
     __shared__ float xs[4096];
-    __shared__ float tiles[kRegThreads / 64][kRB * 64];
+    __shared__ float tiles[NT / 64][kRB * 64];
     const int cols = 256 * nb;
-    for (int i = threadIdx.x; i < cols; i += kRegThreads) xs[i] = x[i];
+    for (int i = threadIdx.x; i < cols; i += NT) xs[i] = x[i];
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int nw = gridDim.x * (kRegThreads / 64);
-    const int gw = blockIdx.x * (kRegThreads / 64) + (threadIdx.x >> 6);
+    const int nw = gridDim.x * (NT / 64);
+    const int gw = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
     const int NQ = 4 * nb;
     const bool act = lane < NQ;
     const int qi = act ? lane : 0;
@@ -197,18 +199,19 @@ q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
     const int r0 = gw * rpw, r1 = min(rows, r0 + rpw);
     if (r0 >= r1) return;
     float *tile = tiles[threadIdx.x >> 6];
-    const uint32_t e0 = (uint32_t)r0 * NQ + qi, e1 = (uint32_t)(r1 - 1) * NQ + qi;
-    Q6Quarter cur = q6_load(P, e0);
+    const uint32_t e1 = (uint32_t)(r1 - 1) * NQ + qi;
+    auto row_e = [&](int r) { return min((uint32_t)r * NQ + qi, e1); };   // past the run: its last row
+    Q6Quarter buf[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) buf[i] = q6_load(P, row_e(r0 + i));
     int rb = r0;
-    // full batches: the next row's loads are issued before this row is
-    // computed (the last row of the wave reloads itself)
-    for (; rb + kRB <= r1; rb += kRB) {
+    for (; rb + kRB <= r1; rb += kRB) {        // full batches
         float part[kRB];
 #pragma unroll
         for (int k = 0; k < kRB; k++) {
-            const Q6Quarter nxt = q6_load(P, min((uint32_t)(rb + k + 1) * NQ + qi, e1));
-            part[k] = act ? q6_dot(cur, xg, sx) : 0.0f;
-            cur = nxt;
+            const Q6Quarter nxt = q6_load(P, row_e(rb + k + PF));
+            part[k] = act ? q6_dot(buf[k % PF], xg, sx) : 0.0f;
+            buf[k % PF] = nxt;
         }
         const float v = rows_sum<kRB>(part, tile);
         if (lane < kRB) out[rb + lane] = v;
@@ -218,9 +221,10 @@ q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
 #pragma unroll
         for (int k = 0; k < kRB; k++) {
             part[k] = 0.0f;
-            if (rb + k < r1) {                 // wave-uniform
-                if (act) part[k] = q6_dot(cur, xg, sx);
-                cur = q6_load(P, min((uint32_t)(rb + k + 1) * NQ + qi, e1));
+            if (rb + k < r1 && act) part[k] = q6_dot(buf[k % PF], xg, sx);   // rows rb .. r1-1 are in the ring
+            if (k + 1 < kRB && (k + 1) % PF == 0 && rb + k + 1 < r1) {
+#pragma unroll
+                for (int i = 0; i < PF; i++) buf[i] = q6_load(P, row_e(rb + k + 1 + i));
             }
         }
         const float v = rows_sum<kRB>(part, tile);
@@ -266,27 +270,35 @@ __device__ __forceinline__ float q8_dot(uint4 q, uint16_t d16, const float *xs16
     return h2f(d16) * fmaf(-128.0f, sx, dot);
 }
 
-#ifndef GS_RB6
-#define GS_RB6 8
-#endif
-#ifndef GS_RB8
-#define GS_RB8 4
-#endif
-constexpr int kRB6 = GS_RB6, kRB8 = GS_RB8;   // rows per reduction batch (Q6_K, Q8_0)
+// Measured on MI355X at the Qwen2.5-7B shape (same box, interleaved runs):
+// Q6_K 768 threads (12 waves per CU, 157 VGPRs), 2 rows in flight, 8 rows
+// per reduction batch: 77-78 us; one row in flight at 1024 threads: 88-89 us;
+// 4 rows in flight (211 VGPRs, 8 waves): 84 us.  Q8_0: 4 rows per batch
+// (8 spill at 1024 threads with one row in flight).
+constexpr int kRB6 = 8, kPF6 = 2, kNT6 = 768;   // Q6_K: rows per batch, rows in flight, threads
+constexpr int kRB8 = 8, kPF8 = 2, kNT8 = 768;   // Q8_0: the same structure
 constexpr int kQ8Halves = 4;            // half blocks per lane on the register path (cols <= 4096)
 
-template <int kRB>
-__global__ void __launch_bounds__(kRegThreads)
+// One row's quants and scales for a lane (kQ8Halves half blocks).
+struct Q8Row {
+    uint4 q[kQ8Halves];
+    uint16_t d[kQ8Halves];
+};
+
+// As q6k_gemv_xreg: x (64 values per lane) in registers, PF rows in flight.
+template <int kRB, int PF, int NT>
+__global__ void __launch_bounds__(NT)
 q80_gemv_xreg(const uint8_t *bits, const uint16_t *dq, const float *x, float *out, int rows, int nb)
 {
+    static_assert(kRB % PF == 0, "ring of PF row buffers, kRB rows per batch");
     __shared__ float xs[4096];
-    __shared__ float tiles[kRegThreads / 64][kRB * 64];
+    __shared__ float tiles[NT / 64][kRB * 64];
     const int cols = 32 * nb;
-    for (int i = threadIdx.x; i < cols; i += kRegThreads) xs[i] = x[i];
+    for (int i = threadIdx.x; i < cols; i += NT) xs[i] = x[i];
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int nw = gridDim.x * (kRegThreads / 64);
-    const int gw = blockIdx.x * (kRegThreads / 64) + (threadIdx.x >> 6);
+    const int nw = gridDim.x * (NT / 64);
+    const int gw = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
     const int nh = 2 * nb;
     float xv[kQ8Halves][16], sx[kQ8Halves];
     bool act[kQ8Halves];
@@ -309,35 +321,48 @@ q80_gemv_xreg(const uint8_t *bits, const uint16_t *dq, const float *x, float *ou
     const int rpw = (rows + nw - 1) / nw;
     const int r0 = gw * rpw, r1 = min(rows, r0 + rpw);
     if (r0 >= r1) return;
-    auto load = [&](int r, uint4 (&q)[kQ8Halves], uint16_t (&d)[kQ8Halves]) {
+    float *tile = tiles[threadIdx.x >> 6];
+    auto load = [&](int r) {                   // rows past the run read its last row
+        const uint32_t rr = (uint32_t)min(r, r1 - 1);
+        Q8Row w;
 #pragma unroll
         for (int k = 0; k < kQ8Halves; k++) {
-            const size_t e = (size_t)r * nh + hb[k];
-            q[k] = ntl4(bits + e * 16);
-            d[k] = __builtin_nontemporal_load(dq + (e >> 1));
+            const uint32_t e = rr * (uint32_t)nh + (uint32_t)hb[k];
+            w.q[k] = ntl4(bits + e * 16u);
+            w.d[k] = __builtin_nontemporal_load(dq + (e >> 1));
         }
+        return w;
     };
-    float *tile = tiles[threadIdx.x >> 6];
-    uint4 cq[kQ8Halves];
-    uint16_t cd[kQ8Halves];
-    load(r0, cq, cd);
-    for (int rb = r0; rb < r1; rb += kRB) {
+    auto dot = [&](const Q8Row &w) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kQ8Halves; k++)
+            if (act[k]) v += q8_dot(w.q[k], w.d[k], xv[k], sx[k]);
+        return v;
+    };
+    Q8Row buf[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) buf[i] = load(r0 + i);
+    int rb = r0;
+    for (; rb + kRB <= r1; rb += kRB) {        // full batches
         float part[kRB];
 #pragma unroll
-        for (int kk = 0; kk < kRB; kk++) {
-            const int r = rb + kk;
-            part[kk] = 0.0f;
-            if (r < r1) {                      // wave-uniform
-                uint4 nq[kQ8Halves];
-                uint16_t nd[kQ8Halves];
-                load(min(r + 1, r1 - 1), nq, nd);
-                float v = 0.0f;
+        for (int k = 0; k < kRB; k++) {
+            const Q8Row nxt = load(rb + k + PF);
+            part[k] = dot(buf[k % PF]);
+            buf[k % PF] = nxt;
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB) out[rb + lane] = v;
+    }
+    if (rb < r1) {                             // the last, partial batch
+        float part[kRB];
 #pragma unroll
-                for (int k = 0; k < kQ8Halves; k++)
-                    if (act[k]) v += q8_dot(cq[k], cd[k], xv[k], sx[k]);
-                part[kk] = v;
+        for (int k = 0; k < kRB; k++) {
+            part[k] = rb + k < r1 ? dot(buf[k % PF]) : 0.0f;
+            if (k + 1 < kRB && (k + 1) % PF == 0 && rb + k + 1 < r1) {
 #pragma unroll
-                for (int k = 0; k < kQ8Halves; k++) { cq[k] = nq[k]; cd[k] = nd[k]; }
+                for (int i = 0; i < PF; i++) buf[i] = load(rb + k + 1 + i);
             }
         }
         const float v = rows_sum<kRB>(part, tile);
@@ -480,12 +505,12 @@ int gs_gemv(const gs_qmatrix *m, const float *d_x, size_t B, float *d_out, void 
         float *o = d_out + b * m->rows;
         if (m->qtype == GS_QTYPE_Q6_K) {
             if (4 * nb <= 64)
-                hipLaunchKernelGGL(gs::q6k_gemv_xreg<gs::kRB6>, dim3(m->cus), dim3(gs::kRegThreads), 0, st, m->q6, x, o, rows, nb);
+                hipLaunchKernelGGL((gs::q6k_gemv_xreg<gs::kRB6, gs::kPF6, gs::kNT6>), dim3(m->cus), dim3(gs::kNT6), 0, st, m->q6, x, o, rows, nb);
             else
                 hipLaunchKernelGGL(gs::q6k_gemv_lds, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q6, x, o, rows, nb);
         } else {
             if (2 * nb <= 64 * gs::kQ8Halves)
-                hipLaunchKernelGGL(gs::q80_gemv_xreg<gs::kRB8>, dim3(m->cus), dim3(gs::kRegThreads), 0, st, m->q8, m->d, x, o, rows, nb);
+                hipLaunchKernelGGL((gs::q80_gemv_xreg<gs::kRB8, gs::kPF8, gs::kNT8>), dim3(m->cus), dim3(gs::kNT8), 0, st, m->q8, m->d, x, o, rows, nb);
             else
                 hipLaunchKernelGGL(gs::q80_gemv_lds, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q8, m->d, x, o, rows, nb);
         }
