@@ -53,8 +53,9 @@ constexpr uint32_t kNow = 0x80000000u;            // cnt[] flag: collect in the 
 constexpr uint32_t kMetaCol = 1u, kMetaNow = 0x80u;  // meta flags: collected / collect in the next pass
 constexpr uint32_t kDeferCapG = 65536;            // deferred elements per row
 constexpr uint32_t kWalkCap = 65536;              // items of the walk array per row
-// deferred entry: id | bit 31 penalized value | bit 30 seq-2 done
-constexpr uint32_t kDone2 = 0x40000000u, kIdMask = 0x1fffffffu;
+// deferred entry: id | bit 31 penalized value | bit 30 seq-2 done (its
+// increment added) | bit 29 seq-3 increment pending (merged pass 3)
+constexpr uint32_t kDone2 = 0x40000000u, kPend3 = 0x20000000u, kIdMask = 0x1fffffffu;
 
 __device__ __forceinline__ int bin_of(float dp)
 {
@@ -296,13 +297,14 @@ __device__ bool build_groups(RowSmem &sm)
 }
 
 // Sum the bulk increments of accumulation `which` per run.
-__device__ void gather_runs(RowSmem &sm, int which)
+// (seq 3: from acc3 when given -- the merged pass 3 -- else from esum.)
+__device__ void gather_runs(RowSmem &sm, int which, const uint32_t *acc3 = nullptr)
 {
     BinsSmem &bn = sm.x.bn;
     const int t = threadIdx.x;
     for (int i = t; i <= bn.ngroups; i += kThreads) bn.run[i] = 0ull;
     __syncthreads();
-    const uint32_t *src = which == 2 ? bn.k2 : bn.esum;     // seq 3 reuses esum
+    const uint32_t *src = which == 2 ? bn.k2 : (acc3 ? acc3 : bn.esum);   // seq 3 reuses esum
     for (int b = t; b < kBins; b += kThreads) {
         const uint32_t mt = bn.meta[b];
         if ((mt & 1u) || bn.off[b + 1] == bn.off[b]) continue;     // nonempty bulk bins only
@@ -691,6 +693,7 @@ __device__ __forceinline__ int inc_s_range(float e, float Slo, float Shi, int b,
 struct PassK {
     float m0, m, inv_s, inv_s2, hw2;
     int ixlim;                     // pass 3: record indices of bins <= ixlim
+    float inv_s2c, hw3;            // merged pass 3: 1 / (centre of the s2 range), seq-3 tolerance
 };
 // Classification of one element: cl 0 nothing to do, 1 list it, 2 defer it,
 // 3 add increment k to bin b.  Branch-free; one LDS read (meta).
@@ -698,6 +701,8 @@ struct Cls {
     int b, cl;
     uint32_t k;
     bool wix;                      // record the element index in its bin's segment
+    uint32_t k3 = 0u;              // merged pass 3: seq-3 increment to add now
+    uint32_t dfl = 0u;             // flags of a deferred entry (kDone2: k is added now; kPend3)
 };
 // Pass 2: accumulation 1 (src/sampler.rs:54).
 __device__ __forceinline__ Cls classify1(const BinsSmem &bn, const PassK &K, float y)
@@ -726,6 +731,31 @@ __device__ __forceinline__ Cls classify3(const BinsSmem &bn, const PassK &K, flo
     c.wix = inr && c.b <= K.ixlim;
     return c;
 }
+// Pass 3 merged with pass 4 (rows with a nucleus cut and no penalty):
+// accumulation 2 as classify3 and, in the bins before the predicted draw
+// (meta bit 2), accumulation 3 with q = p / s2 for s2 known to a range
+// (tolerance hw3).  An element either increment of which cannot be decided
+// is deferred; the decided one is added now (dfl says which is pending).
+__device__ __forceinline__ Cls classify3m(const BinsSmem &bn, const PassK &K, float y)
+{
+    const float dp = y - K.m0;
+    const bool inr = (dp <= kDUp) && (dp >= -kDLo);
+    Cls c;
+    c.b = bin_clamp(dp);
+    const uint32_t mt = bn.meta[c.b];
+    const float p = fast_exp(y - K.m) * K.inv_s;
+    const bool ok2 = inc_of(ldexpf(p, 23 - meta_b(mt, 2)), K.hw2, &c.k);
+    uint32_t k3;
+    const bool ok3 = inc_of(ldexpf(p * K.inv_s2c, 23 - meta_b(mt, 3)), K.hw3, &k3);
+    const bool want3 = (mt & 4u) != 0u;
+    const bool bulk2 = inr && !(mt & kMetaNow) && !(mt & kMetaCol) && (mt & 2u);
+    const bool d2 = !ok2, d3 = want3 && !ok3;
+    c.cl = !inr ? 0 : ((mt & kMetaNow) ? 1 : (!bulk2 ? 0 : ((d2 || d3) ? 2 : 3)));
+    c.dfl = c.cl == 2 ? ((d2 ? 0u : kDone2) | (d3 ? kPend3 : 0u)) : 0u;
+    c.k3 = (bulk2 && want3 && !d3) ? k3 : 0u;
+    c.wix = inr && c.b <= K.ixlim;
+    return c;
+}
 // Pass 4: accumulation 3, q = p / s2 (src/sampler.rs:68, :74-75).
 __device__ __forceinline__ Cls classify4(const BinsSmem &bn, const PassK &K, float y)
 {
@@ -746,7 +776,8 @@ __device__ __forceinline__ Cls classify4(const BinsSmem &bn, const PassK &K, flo
 // as cls says.  Raw contributions of penalized ids are undone first.
 template <class ClsF>
 __device__ void bins_pass(RowSmem &sm, const float *row, int V, bool t_one, float T, bool has_pen,
-                          uint64_t *gl, uint32_t *defer, uint32_t dcap, uint32_t *acc, uint32_t *ix, ClsF cls)
+                          uint64_t *gl, uint32_t *defer, uint32_t dcap, uint32_t *acc, uint32_t *ix, ClsF cls,
+                          uint32_t *acc3 = nullptr)
 {
     BinsSmem &bn = sm.x.bn;
     const int t = threadIdx.x;
@@ -757,10 +788,12 @@ __device__ void bins_pass(RowSmem &sm, const float *row, int V, bool t_one, floa
             stg(gl + slot, list_entry(y, (uint32_t)i));
         } else if (c.cl == 2) {
             const int slot = atomicAdd(&bn.ndefer, 1);
-            if ((uint32_t)slot < dcap) stg(defer + slot, (uint32_t)i | flag);
+            if ((uint32_t)slot < dcap) stg(defer + slot, (uint32_t)i | flag | c.dfl);
+            if ((c.dfl & kDone2) && c.k) atomicAdd(&acc[c.b], c.k);
         } else if (c.cl == 3 && c.k) {
             atomicAdd(&acc[c.b], c.k);
         }
+        if (acc3 && c.k3) atomicAdd(&acc3[c.b], c.k3);
     };
     auto act0 = [&](int i, float y, const Cls &c) { act(i, y, c, 0u); };
     if (t_one) row_for_each_cls(row, V, [](float x) { return x; }, cls, act0);
@@ -1045,6 +1078,14 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     const int t = threadIdx.x;
     const bool t_one = (T == 1.0f);
     const bool nucleus = top_p < 1.0f;
+    // Rows with a nucleus cut, no penalty and a draw predicted beyond a fifth
+    // of the row compute the seq-3 increments in pass 3 (no pass 4, which
+    // would otherwise pass over the row); their per-bin sums use the penalty
+    // hash's LDS (4096 words), which such rows leave unused.  Set in plan B.
+    bool merge3 = false;
+    static_assert(2 * kHashSlots == kBins && offsetof(RowSmem, hval) == offsetof(RowSmem, hkey) + 4 * kHashSlots,
+                  "hkey and hval form one array of kBins words");
+    uint32_t *acc3 = nullptr;
     const float4 *r4 = reinterpret_cast<const float4 *>(row);
     const int n4 = V >> 2;
     if (n4 == 0) BINS_FAIL();
@@ -1347,7 +1388,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
         const double pre = block_excl_f64(loc, &stot, sm) + osum;
         stot += osum;
         double s2lo = 1.0, s2hi = 1.0;
-        if (t == 0) { bn.cut_g = kBins; bn.ixlim = -1; }
+        if (t == 0) { bn.cut_g = kBins; bn.ixlim = -1; bn.ixlast = -1; }
         __syncthreads();
         if (nucleus) {
             if (stot / Sc < (double)top_p * (1.0 + 2.0 * kDelta)) BINS_FAIL();   // the cut may not happen
@@ -1374,7 +1415,27 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
             bn.hw2 = 2.0f * kExpErr + (float)(((double)Shi - (double)Slo) / (double)Slo) + 0x1p-22f;
             bn.s2lo = (float)s2lo;
             bn.s2hi = (float)s2hi;
+            bn.inv_s2c = (float)(2.0 / (s2lo + s2hi));
+            bn.hw3 = bn.hw2 + (float)((s2hi - s2lo) / s2lo) + 0x1p-22f;
         }
+        const double s2c = 0.5 * (s2lo + s2hi);
+        // The bins that may precede the draw (seq 3): indexed in pass 3 when
+        // they hold at most a fifth of the row, else the merged pass 3.
+        if (nucleus) {
+            double lo = pre;
+#pragma unroll
+            for (int c = 0; c < kPer; c++) {
+                const double hi = lo + mass[c];
+                const uint32_t mt = mtv[c];
+                const double plo_ = lo * iSc;
+                if ((mt & 8u) && !(mt & 1u) && plo_ * dl < (double)top_p && plo_ / s2c * dl <= (double)r)
+                    atomicMax(&bn.ixlim, kPer * t + c);
+                lo = hi;
+            }
+        }
+        __syncthreads();
+        merge3 = nucleus && !has_pen && bn.ixlim >= 0 && bn.off[bn.ixlim + 1] - bn.off[0] > (uint32_t)V / 5u;
+        if (merge3) acc3 = reinterpret_cast<uint32_t *>(sm.hkey);
         double lo = pre;
 #pragma unroll
         for (int c = 0; c < kPer; c++) {
@@ -1386,8 +1447,8 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
                 bool col = ((mt >> 4) & 7u) != 0u;            // seq-1 ties need the order for S
                 const double ehi = e_at((float)b) * 1.001;
                 const double plo_ = lo * iSc, phi_ = hi * iSc, pe = ehi * iSc;
-                bool k2 = false;
-                int b2 = 0;
+                bool k2 = false, k3 = false;
+                int b2 = 0, b3 = 0;
                 if (nucleus) {
                     k2 = plo_ * dl < (double)top_p;
                     if (k2) {
@@ -1398,18 +1459,32 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
                         const int c2 = ilogb(pe);
                         if (c2 < b2) col |= cn * ldexp(1.0, c2 - b2) > kTieThr;
                         col |= cn * (ldexp(pe, 23 - b2) + 1.0) >= 4.0e9;
+                        // merged pass 3: the seq-3 decisions of plan C, with S
+                        // and s2 known to their ranges (far inside the margin)
+                        const double qlo = plo_ / s2c, qhi = phi_ / s2c;
+                        if (merge3 && qlo * dl <= (double)r) {
+                            k3 = true;
+                            b3 = grid_exp((float)qlo);
+                            col |= !(qlo > 0.0);
+                            col |= grid_exp((float)(qlo * dl)) != grid_exp((float)(qhi * dh));
+                            col |= qhi * dh > (double)r;
+                            const double qe = pe / s2c;
+                            const int c3 = ilogb(qe);
+                            if (c3 < b3) col |= cn * ldexp(1.0, c3 - b3) > kTieThr;
+                            col |= cn * (ldexp(qe, 23 - b3) + 1.0) >= 4.0e9;
+                            atomicMax(&bn.ixlast, b);
+                        }
                     }
                 }
                 bn.meta[b] = (mt & 0xff00u) | (mt & 0x78u) | (col ? 0x81u : 0u) | (k2 ? 2u : 0u) |
-                             ((uint32_t)(b2 + 128) << 16) | (128u << 24);
-                // index the bins that may precede the draw (seq 3)
-                if (k2 && plo_ / (0.5 * (s2lo + s2hi)) * dl <= (double)r) atomicMax(&bn.ixlim, b);
+                             (k3 ? 4u : 0u) | ((uint32_t)(b2 + 128) << 16) | ((uint32_t)(b3 + 128) << 24);
                 if (col) {
                     bn.cnt[b] = bn.off[b] | kNow;
                     atomicAdd(&bn.ncollect, 1);
                 }
             }
             bn.k2[b] = 0u;
+            if (merge3) acc3[b] = 0u;
             bn.icur[b] = bn.off[b];
             bn.pre_e[b] = (float)lo;
             lo = hi;
@@ -1419,7 +1494,6 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     __syncthreads();
     if (t == 0) {
         bn.ndefer = 0;
-        bn.ixlast = -1;
         // a large region is cheaper as passes over the row than as gathers
         if (bn.ixlim >= 0 && bn.off[bn.ixlim + 1] - bn.off[0] > (uint32_t)V / 5u) bn.ixlim = -1;
     }
@@ -1430,8 +1504,14 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     K.inv_s = bn.inv_s;
     K.hw2 = bn.hw2;
     K.ixlim = use_ix ? bn.ixlim : -1;
-    bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.k2, ix,
-              [&bn, K](float y) { return classify3(bn, K, y); });
+    K.inv_s2c = bn.inv_s2c;
+    K.hw3 = bn.hw3;
+    if (merge3)
+        bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.k2, ix,
+                  [&bn, K](float y) { return classify3m(bn, K, y); }, acc3);
+    else
+        bins_pass(sm, row, V, t_one, T, has_pen, gl, defer, dcap, bn.k2, ix,
+                  [&bn, K](float y) { return classify3(bn, K, y); });
     GS_STAMP(17);
     GS_DIAG(29, bn.ndefer | ((uint64_t)bn.ncollect << 32));
     if ((uint32_t)bn.ndefer > dcap) BINS_FAIL();
@@ -1447,7 +1527,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     const int nd = bn.ndefer;
     for (int j = t; j < nd; j += kThreads) {
         const uint32_t en = ldg(defer + j);
-        if (en == 0xffffffffu) continue;
+        if (en == 0xffffffffu || (en & kDone2)) continue;
         const float y = def_y(en);
         const int b = bin_of(y - m0);
         const uint32_t mt = bn.meta[b];
@@ -1522,6 +1602,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     }
     GS_STAMP(21);
 
+    if (!merge3) {
     // ---- plan C: accumulation 3, with S and s2 exact -------------------------
     // q = p / s2 (src/sampler.rs:68); the seq-3 running sum before bin b is
     // the bin's mass prefix / (S s2) to the rounding of the increments.  Bulk
@@ -1636,6 +1717,29 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     }
     __syncthreads();
     if (bn.fail) BINS_FAIL();
+    } else {
+        // merged pass 3: the pending seq-3 increments, now that S and s2 are
+        // exact; a rounding tie marks its bin for collection (its order
+        // decides the tie)
+        if (t == 0) bn.ncollect = 0;
+        __syncthreads();
+        for (int j = t; j < nd; j += kThreads) {
+            const uint32_t en = ldg(defer + j);
+            if (en == 0xffffffffu || !(en & kPend3)) continue;
+            const float y = def_y(en);
+            const int b = bin_of(y - m0);
+            const uint32_t mt = bn.meta[b];
+            if (mt & 1u) continue;
+            uint32_t k;
+            const int rc = inc_exact(glibc_expf(y - m) / S / s2, meta_b(mt, 3), &k);
+            if (rc < 0) { bn.fail = 1; continue; }
+            if (rc == 0) { mark(b); continue; }
+            if (k) atomicAdd(&acc3[b], k);
+        }
+        __syncthreads();
+        if (bn.fail) BINS_FAIL();
+        GS_STAMP(22);
+    }
 #ifdef GS_TIMING
     if (t == 0 && blockIdx.x < 256 && bn.ncollect) g_fails[512 + blockIdx.x] |= 2;
 #endif
@@ -1666,7 +1770,7 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
     const int n3 = nucleus ? bn.cut_g + 1 : N;
     if (n3 > N) BINS_FAIL();
     GS_STAMP(23);
-    gather_runs(sm, 3);
+    gather_runs(sm, 3, acc3);
     float c3;
     const int jd = walk(sm, W, n3, 3, [r](float c) { return r < c; }, &c3);
     if (jd < 0) BINS_FAIL();

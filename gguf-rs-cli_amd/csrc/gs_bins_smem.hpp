@@ -27,6 +27,7 @@ struct BinsSmem {
     uint32_t wbase[kMaxGroups + 1];// walk array: position of run g's marker
     float m0, m, s2lo, s2hi, Slo, Shi;
     float hw2, inv_s, inv_s2;
+    float inv_s2c, hw3;            // merged pass 3: 1 / centre of the s2 range, seq-3 tolerance
     int ngroups, ndefer, nover, fail, ncollect, nties;
     int cut_g, ixlim, ixlast;
 };
