@@ -228,6 +228,111 @@ def bench_gemv(gs, torch, steps=50, warmup=5, cpu=True):
     return out
 
 
+def bench_decode(gs, torch, K=32, reps=5, cpu=True, gemv_us=0.0):
+    """The device-resident decode step (include/gs_decode.h) at Qwen2.5-7B's
+    output shape, B = 1, the CLI's sampler defaults (src/main.rs:24-31),
+    W = 64: x = E[token] (a stand-in for the transformer), the Q6_K
+    [152064 x 3584] GEMV into HBM, draw, sample, commit.  K steps are
+    captured in one HIP graph; the figure is graph time / K, events on the
+    replay stream.  Beside it: the same K steps launched eagerly, the sampler
+    alone on the same logits, and the reference's flow per token (the logits
+    read back to the host, src/gpu/mod.rs:364-381, then sampled on the CPU by
+    the oracle, the restated src/sampler.rs)."""
+    import workloads
+    qt, V, cols, B, W = workloads.Q6_K, 152064, 3584, 1, 64
+    blocks = workloads.synth_qblocks(qt, V, cols, seed=11)
+    m = gs.QMatrix(qt, blocks, V, cols)
+    del blocks
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    E = torch.randn((V, cols), generator=g, device="cuda") * 0.05
+    sampler = gs.Sampler(0.7, 40, 0.9, 1.1, seed=42)
+    dec = gs.Decoder(B, W=W, max_new=1 << 30, stop=())
+    x = torch.empty((B, cols), dtype=torch.float32, device="cuda")
+    logits = torch.empty((B, V), dtype=torch.float32, device="cuda")
+
+    def reset():
+        dec.init([42])
+        dec.next.fill_(1)
+        torch.cuda.synchronize()
+
+    def steps(n, st=None):
+        for _ in range(n):
+            torch.index_select(E, 0, dec.next.long(), out=x)
+            dec.step(sampler, logits=logits, lm_head=m, x=x, stream=st)
+
+    reset()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        steps(2, side)
+    torch.cuda.current_stream().wait_stream(side)
+    reset()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        steps(K, torch.cuda.current_stream())
+    st = torch.cuda.current_stream()
+    reset()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(reps):
+        e0.record(st)
+        graph.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / K)
+    us_graph = float(np.median(times))
+    # eager launches of the same steps
+    reset()
+    steps(4, st)
+    e0.record(st)
+    steps(K, st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    us_eager = e0.elapsed_time(e1) * 1e3 / K
+    # the sampler alone, batch entry, on the step's logits
+    tok = torch.empty(1, dtype=torch.int32, device="cuda")
+    for _ in range(5):
+        sampler.sample_batch(logits, tok, recent=dec.window, recent_len=dec.window_len, u=dec.u, stream=st)
+    e0.record(st)
+    for _ in range(50):
+        sampler.sample_batch(logits, tok, recent=dec.window, recent_len=dec.window_len, u=dec.u, stream=st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    us_sample = e0.elapsed_time(e1) * 1e3 / 50
+    out = {"workload": "Qwen2.5-7B lm_head Q6_K [152064 x 3584] + sampler T=0.7 k=40 p=0.9 rep=1.1 W=64, B=1",
+           "steps_per_graph": K, "us_per_step_graph": us_graph, "us_per_step_eager": us_eager,
+           "us_sample_batch_entry": us_sample,
+           "bytes_out_per_step": 4,
+           "data": "synthetic Q6_K blocks; x = E[token] with E ~ N(0, 0.05^2) on the device"}
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        h = torch.empty(V, dtype=torch.float32).pin_memory()
+        d2h = []
+        for _ in range(20):
+            t0 = time.perf_counter()
+            h.copy_(logits[0], non_blocking=True)
+            torch.cuda.synchronize()
+            d2h.append((time.perf_counter() - t0) * 1e6)
+        lg = h.numpy().copy()
+        rec = dec.window[0].cpu().numpy().view(np.uint32)
+        t0 = oracle.now()
+        n = 20
+        for _ in range(n):
+            oracle.sample(lg.copy(), 0.7, 40, 0.9, 1.1, rec, r=0.25)
+        cpu_us = (oracle.now() - t0) / n * 1e6
+        out["reference_flow"] = {
+            "us_per_step": gemv_us + float(np.median(d2h)) + cpu_us,
+            "d2h_us": float(np.median(d2h)), "cpu_sample_us": cpu_us, "cores": 1, "kind": "port",
+            "sample": "GEMV on the GPU, 608 KB logits copied to pinned host memory, the oracle's "
+                      "sample (src/sampler.rs restated, full sort) on one thread, 20 calls"}
+    m.close()
+    return out
+
+
 def calib_copy(torch, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of a known size: its FETCH_SIZE and
     WRITE_SIZE per dispatch give the scale factor of those counters."""
@@ -282,6 +387,8 @@ def main():
                     help="only isolated single-row launches of the c1 kernels (for profiling)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the Q6_K logits projection (for profiling)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the graph-captured decode step (for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 1 GiB device copy 5x (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -299,6 +406,10 @@ def main():
     if args.c1_kernel:
         c1_isolated(gs, torch)
         return
+    if args.decode_only:
+        d = bench_decode(gs, torch, cpu=False)
+        log("decode step: %.1f us (graph), %.1f us (eager)" % (d["us_per_step_graph"], d["us_per_step_eager"]))
+        return
     if args.gemv_only:
         g = bench_gemv(gs, torch, steps=args.steps, warmup=args.warmup, cpu=False)
         log("gemv: %.1f us, %.0f GB/s" % (g["us"], g["roofline"]["achieved"]))
@@ -314,6 +425,9 @@ def main():
     gemv = bench_gemv(gs, torch, cpu=not args.no_cpu)
     log("lm_head gemv: %.1f us, %.0f GB/s (%.1f%% of peak)" % (
         gemv["us"], gemv["roofline"]["achieved"], 100 * gemv["roofline"]["frac"]))
+    dstep = bench_decode(gs, torch, cpu=not args.no_cpu, gemv_us=gemv["us"])
+    log("decode step: %.1f us (graph), %.1f us (eager), sampler alone %.1f us" % (
+        dstep["us_per_step_graph"], dstep["us_per_step_eager"], dstep["us_sample_batch_entry"]))
     value = c3["B"] / (c3["ms"] / 1e3)
     achieved = c3["bytes"] / (c3["ms"] / 1e3) / 1e9
     out = {
@@ -339,6 +453,7 @@ def main():
                        "kernel_us_batch_entry": c1k,
                        "V": 32000, "B": 1, "steps": 256},
         "lm_head_gemv": gemv,
+        "decode_step": dstep,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(c3)

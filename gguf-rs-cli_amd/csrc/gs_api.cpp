@@ -33,6 +33,8 @@ struct gs_sampler {
     size_t scratch_elems;
     int32_t *fb;                 // per-row fallback flags of the full-vocabulary path
     size_t fb_cap;
+    void *split;                 // split top-k path: virtual rows (f32), then their ids (u32)
+    size_t split_cap;
 };
 
 namespace {
@@ -73,6 +75,21 @@ bool needs_full_path(const gs_params &p, size_t V)
     if (!(p.temperature > 0.0f) || V <= 1) return false;
     size_t keep = (p.top_k > 0 && p.top_k < V) ? p.top_k : V;
     return keep >= V || keep > (size_t)gs::kMaxTopK;
+}
+
+// Buffer of the split top-k path for `rows` rows of width `width`: the
+// virtual rows' values, then their ids.
+size_t split_bytes(size_t rows, size_t width) { return rows * width * 8; }
+
+int reserve_split(gs_sampler *s, size_t rows, size_t width)
+{
+    return grow(&s->split, &s->split_cap, split_bytes(rows, width));
+}
+
+hipError_t launch_split(gs_sampler *s, const gs::RowArgs &a, size_t B, size_t width, hipStream_t st)
+{
+    float *vrow = (float *)s->split;
+    return gs::launch_split(a, (int)B, vrow, (uint32_t *)(vrow + B * width), st);
 }
 
 int reserve_scratch(gs_sampler *s, size_t rows, size_t V)
@@ -136,6 +153,7 @@ int gs_sampler_destroy(gs_sampler *s)
     if (s->h_rec) (void)hipHostFree(s->h_rec);
     if (s->scratch) (void)hipFree(s->scratch);
     if (s->fb) (void)hipFree(s->fb);
+    if (s->split) (void)hipFree(s->split);
     if (s->h_tok) (void)hipHostFree(s->h_tok);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     (void)hipSetDevice(dev);
@@ -147,6 +165,13 @@ int gs_sampler_set_params(gs_sampler *s, const gs_params *params)
 {
     if (!s || !params) return GS_ERR_INVALID;
     s->params = *params;
+    return GS_OK;
+}
+
+int gs_sampler_get_params(const gs_sampler *s, gs_params *params)
+{
+    if (!s || !params) return GS_ERR_INVALID;
+    *params = s->params;
     return GS_OK;
 }
 
@@ -174,6 +199,11 @@ int gs_sampler_set_state(gs_sampler *s, uint64_t state)
 int gs_sampler_reserve(gs_sampler *s, size_t B, size_t V)
 {
     if (!s || V > GS_MAX_VOCAB) return GS_ERR_INVALID;
+    if (V > gs::kRegMaxV) {               // rows the split top-k path may take, any k
+        const size_t rows = B < (size_t)gs::kSplitMaxRows ? B : (size_t)gs::kSplitMaxRows;
+        int rc = reserve_split(s, rows ? rows : 1, gs::kSplitMaxWidth);
+        if (rc) return rc;
+    }
     return reserve_scratch(s, B, V);
 }
 
@@ -244,10 +274,13 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
         // cannot finish is run again by the general one.
         a.done = s->d_done_map;
         bool reg = gs::reg_row_fits(s->params, V, a.logits);
+        const bool split = !reg && gs::split_fits(s->params, V) &&
+                           reserve_split(s, 1, gs::split_width(s->params, V)) == GS_OK;
         for (;;) {
             a.done_val = ++s->seq;
-            const hipError_t le = reg ? gs::launch_reg_row(a, s->stream)
-                                      : gs::launch_sample_rows(a, 1, true, false, s->stream);
+            const hipError_t le = reg     ? gs::launch_reg_row(a, s->stream)
+                                  : split ? launch_split(s, a, 1, gs::split_width(s->params, V), s->stream)
+                                          : gs::launch_sample_rows(a, 1, true, false, s->stream);
             if (le != hipSuccess) return GS_ERR_HIP;
             volatile uint64_t *f = s->h_done;
             uint64_t w = *f;
@@ -306,7 +339,22 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, si
     a.fb = s->fb;
     const bool full = d_params || needs_full_path(s->params, V);
     const bool small = d_params || !needs_full_path(s->params, V);
-    if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+    bool split = !d_params && B <= (size_t)gs::kSplitMaxRows && gs::split_fits(s->params, V);
+    if (split && s->split_cap < split_bytes(B, gs::split_width(s->params, V))) {
+        // the buffers must grow: not under stream capture (no allocation
+        // there), where the rows take the one-workgroup-per-row path instead
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) { (void)hipGetLastError(); return GS_ERR_HIP; }
+        if (cs != hipStreamCaptureStatusNone) split = false;
+    }
+    if (split) {
+        // a few rows of a large vocabulary: spread each row over the chip
+        const size_t wd = gs::split_width(s->params, V);
+        if ((rc = reserve_split(s, B, wd))) return rc;
+        if (launch_split(s, a, B, wd, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+    } else if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) {
+        return GS_ERR_HIP;
+    }
     if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
     return GS_OK;
 }

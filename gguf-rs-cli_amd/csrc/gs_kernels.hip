@@ -1347,9 +1347,10 @@ reg_row_kernel(RowArgs a)
 {
     __shared__ RowSmem sm;
     const int t = threadIdx.x;
+    const int b = blockIdx.x;
     const int V = a.V;
     const gs_params p = a.uparams;
-    const float *row = a.logits;
+    const float *row = a.logits + (size_t)b * a.ld;
     GS_STAMP(0);
     if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
     const bool has_pen = (p.rep_penalty != 1.0f) && (a.recent != nullptr || a.kwin_n);
@@ -1362,7 +1363,7 @@ reg_row_kernel(RowArgs a)
                 (const char __attribute__((address_space(4))) *)__builtin_amdgcn_kernarg_segment_ptr();
             wsrc = reinterpret_cast<const uint32_t *>((uintptr_t)(ka + offsetof(RowArgs, kwin)));
         } else {
-            wsrc = a.recent;
+            wsrc = a.recent + (size_t)b * a.ld_recent;
         }
     }
     uint32_t rid = kEmpty;
@@ -1383,7 +1384,7 @@ reg_row_kernel(RowArgs a)
     if (p.temperature <= 0.0f) {
         tok = greedy_row_reg(sm, row, rv, pl, V, has_pen, p.rep_penalty, &status);
     } else {
-        const float r = a.u ? a.u[0] : lcg_value(a.lcg_state);
+        const float r = a.u ? a.u[b] : lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
         const int keep = (int)p.top_k;
         bool ok;
         tok = topk_row_reg(sm, row, rv, pl, V, keep, p.temperature, p.top_p, has_pen, p.rep_penalty, r,
@@ -1397,8 +1398,8 @@ reg_row_kernel(RowArgs a)
                                   (uint64_t)((uint32_t)tok & 0xffffffu);
             __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         } else {
-            a.tokens[0] = (uint32_t)tok;
-            if (a.status) a.status[0] = status;
+            a.tokens[b] = (uint32_t)tok;
+            if (a.status) a.status[b] = status;
         }
     }
 }
@@ -1446,6 +1447,180 @@ extern "C" int gs_debug_clear(const uint64_t *zeros)
 
 // Launch wrappers (host side of this translation unit).
 namespace gs {
+
+// --------------------------------------------------------------------------
+// Split top-k for a few rows of a large vocabulary.  Pass 1: workgroup
+// (c, b) takes elements [c0, c0 + L) of row b, applies the penalty
+// (src/sampler.rs:23-30: the window's occurrences of each id in the chunk,
+// one op per occurrence), scales by T, and keeps the kp largest under the
+// sampler's order (y descending, index ascending).  It writes their
+// penalized logits and ids to slots [c kp, (c + 1) kp) of row b's virtual
+// row, in index order.  The global top-k is among the kept elements, and the
+// virtual row lists them in index order, so sampling it (same penalized
+// values, same division by T, no penalty) gives the same token.  A NaN in
+// the chunk goes to the chunk's first slot, so the sampling reports it.
+// Pass 2 samples the virtual rows.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitPer = 2 * kSplitL / kSplitThreads;   // elements per thread, last chunk included
+static_assert(kRegMaxV == (size_t)kThreads * 4 * kRegF4, "register row width");
+
+struct SplitSmem {
+    uint32_t cnt[2 * kSplitL];          // window occurrences per chunk element
+    uint64_t tmax[kSplitThreads];
+    uint64_t cand[kSplitPer * kSplitMaxKp];
+    float candx[kSplitPer * kSplitMaxKp];
+    uint64_t top[kSplitMaxKp];
+    float topx[kSplitMaxKp];
+    uint64_t tau;
+    int ncand;
+    int nan;
+};
+static_assert(kSplitMaxKp <= kSplitThreads, "one thread per kept element");
+
+__global__ void __launch_bounds__(kSplitThreads)
+split_select_kernel(RowArgs a, int nch, int kp, float *vrow, uint32_t *vidx, size_t vld)
+{
+    __shared__ SplitSmem sm;
+    const int t = threadIdx.x;
+    const int c = blockIdx.x, b = blockIdx.y;
+    const gs_params p = a.uparams;
+    const int V = a.V;
+    const int c0 = c * kSplitL;
+    const int L = c == nch - 1 ? V - c0 : kSplitL;
+    const float *row = a.logits + (size_t)b * a.ld + c0;
+    const bool has_pen = p.rep_penalty != 1.0f && a.recent != nullptr;
+    int W = 0;
+    if (has_pen) {
+        W = a.recent_len ? (int)a.recent_len[b] : a.W;
+        if (W > a.W) W = a.W;
+    }
+    float x[kSplitPer];
+#pragma unroll
+    for (int u = 0; u < kSplitPer; u++) {
+        const int i = u * kSplitThreads + t;
+        x[u] = i < L ? ldg(row + i) : -INFINITY;
+    }
+    if (has_pen)
+        for (int i = t; i < L; i += kSplitThreads) sm.cnt[i] = 0u;
+    if (t == 0) { sm.ncand = 0; sm.nan = 0; }
+    __syncthreads();
+    if (has_pen) {
+        const uint32_t *rec = a.recent + (size_t)b * a.ld_recent;
+        for (int j = t; j < W; j += kSplitThreads) {
+            const uint32_t d = ldg(rec + j) - (uint32_t)c0;   // ids >= V never fall in a chunk
+            if (d < (uint32_t)L) atomicAdd(&sm.cnt[d], 1u);
+        }
+        __syncthreads();
+    }
+    uint64_t key[kSplitPer];
+    uint64_t best = 0ull;
+    bool nan = false;
+#pragma unroll
+    for (int u = 0; u < kSplitPer; u++) {
+        const int i = u * kSplitThreads + t;
+        key[u] = 0ull;
+        if (i < L) {
+            float xv = x[u];
+            if (has_pen) {
+                const uint32_t n = sm.cnt[i];
+                if (n) xv = penalize(xv, n, p.rep_penalty);
+            }
+            x[u] = xv;
+            const float y = xv / p.temperature;
+            nan |= isnan(y);
+            key[u] = cand_of(f2key(y), (uint32_t)(c0 + i));
+            best = key[u] > best ? key[u] : best;
+        }
+    }
+    sm.tmax[t] = best;
+    if (__any(nan) && lane_id() == 0) sm.nan = 1;
+    __syncthreads();
+    // Every thread holds at least L / kSplitThreads >= 4 elements, so the
+    // kp-th largest thread maximum (keys are distinct: they carry the id)
+    // bounds the kp-th largest element: at least kp elements reach it, at
+    // most kp * kSplitPer.
+    {
+        int rk = 0;
+        const ulonglong2 *t2 = reinterpret_cast<const ulonglong2 *>(sm.tmax);
+#pragma unroll 8
+        for (int j = 0; j < kSplitThreads / 2; j++) {
+            const ulonglong2 v = t2[j];
+            rk += (v.x > best) + (v.y > best);
+        }
+        if (rk == kp - 1) sm.tau = best;
+    }
+    __syncthreads();
+    const uint64_t tau = sm.tau;
+#pragma unroll
+    for (int u = 0; u < kSplitPer; u++) {
+        if (key[u] >= tau && key[u] != 0ull) {
+            const int pos = atomicAdd(&sm.ncand, 1);
+            sm.cand[pos] = key[u];
+            sm.candx[pos] = x[u];
+        }
+    }
+    __syncthreads();
+    const int nc = sm.ncand;
+    for (int i = t; i < nc; i += kSplitThreads) {
+        const uint64_t me = sm.cand[i];
+        int rk = 0;
+        for (int j = 0; j < nc; j++) rk += sm.cand[j] > me;
+        if (rk < kp) { sm.top[rk] = me; sm.topx[rk] = sm.candx[i]; }
+    }
+    __syncthreads();
+    if (t < kp) {
+        const uint32_t id = ~(uint32_t)sm.top[t];
+        int pos = 0;
+        for (int j = 0; j < kp; j++) pos += (~(uint32_t)sm.top[j]) < id;
+        const size_t o = (size_t)b * vld + (size_t)c * kp + pos;
+        vrow[o] = (sm.nan && pos == 0) ? __builtin_nanf("") : sm.topx[t];
+        vidx[o] = id;
+    }
+}
+
+// Pass 2: sample virtual row b (width vld, a multiple of 4, 16-byte aligned;
+// no penalty): the register path, else the general top-k paths; the token
+// is mapped back through vidx.
+__global__ void __launch_bounds__(kThreads)
+split_finish_kernel(RowArgs a, const float *vrow, const uint32_t *vidx, size_t vld)
+{
+    __shared__ RowSmem sm;
+    const int t = threadIdx.x;
+    const int b = blockIdx.x;
+    const gs_params p = a.uparams;
+    const float *vr = vrow + (size_t)b * vld;
+    const int V2 = (int)vld;
+    float4 rv[kRegF4];
+    {
+        const float4 *r4 = reinterpret_cast<const float4 *>(vr);
+        const int n4 = V2 >> 2;
+#pragma unroll
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+    }
+    reg_clear(sm, false);
+    if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
+    __syncthreads();
+    const PenLoad pl{kEmpty, 0.0f};
+    const float r = a.u ? a.u[b] : lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
+    const int k = (int)p.top_k;
+    int status = GS_OK;
+    bool ok;
+    int tok = topk_row_reg(sm, vr, rv, pl, V2, k, p.temperature, p.top_p, false, 1.0f, r, &status, &ok);
+    if (!ok) tok = topk_row<true>(sm, vr, V2, k, p.temperature, p.top_p, false, r, true, &status, &ok);
+    if (!ok) tok = topk_row<false>(sm, vr, V2, k, p.temperature, p.top_p, false, r, true, &status, &ok);
+    if (t == 0) {
+        tok = status == GS_OK ? (int)ldg(vidx + (size_t)b * vld + tok) : 0;
+        if (a.done) {
+            const uint64_t word = ((uint64_t)a.done_val << 32) | ((uint64_t)((uint32_t)status & 0xffu) << 24) |
+                                  (uint64_t)((uint32_t)tok & 0xffffffu);
+            __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else {
+            a.tokens[b] = (uint32_t)tok;
+            if (a.status) a.status[b] = status;
+        }
+    }
+}
+
 hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st)
 {
     if (small) hipLaunchKernelGGL(sample_rows_kernel<kModeSmall>, dim3(B), dim3(kThreads), 0, st, a);
@@ -1466,6 +1641,28 @@ bool reg_row_fits(const gs_params &p, size_t V, const void *row)
     if (p.temperature <= 0.0f) return true;                  // greedy (a NaN T is not <= 0)
     return p.temperature > 0.0f && p.temperature < INFINITY && p.top_k > 0 && (size_t)p.top_k < V &&
            p.top_k <= (uint32_t)kMaxTopK;
+}
+bool split_fits(const gs_params &p, size_t V)
+{
+    if (!(p.temperature > 0.0f && p.temperature < INFINITY)) return false;
+    if (V <= kRegMaxV || V > (size_t)0x7fffffff) return false;
+    if (p.top_k == 0 || (size_t)p.top_k >= V) return false;
+    const size_t kp = ((size_t)p.top_k + 3) & ~(size_t)3;
+    return kp <= (size_t)kSplitMaxKp && (V / kSplitL) * kp <= kSplitMaxWidth;
+}
+size_t split_width(const gs_params &p, size_t V)
+{
+    return (V / kSplitL) * (((size_t)p.top_k + 3) & ~(size_t)3);
+}
+hipError_t launch_split(const RowArgs &a, int B, float *vrow, uint32_t *vidx, hipStream_t st)
+{
+    const int nch = a.V / kSplitL;
+    const int kp = ((int)a.uparams.top_k + 3) & ~3;
+    const size_t vld = (size_t)nch * kp;
+    hipLaunchKernelGGL(split_select_kernel, dim3(nch, B), dim3(kSplitThreads), 0, st, a, nch, kp, vrow, vidx, vld);
+    hipLaunchKernelGGL(split_finish_kernel, dim3(B), dim3(kThreads), 0, st, a, (const float *)vrow,
+                       (const uint32_t *)vidx, vld);
+    return hipGetLastError();
 }
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st)

@@ -49,6 +49,19 @@ hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hi
 constexpr int kStatusRetryHost = 0x7f;
 bool reg_row_fits(const gs_params &p, size_t V, const void *row);
 hipError_t launch_reg_row(const RowArgs &a, hipStream_t st);
+// Split top-k path for a few rows of a large vocabulary: pass 1 spreads each
+// row over V / kSplitL workgroups, each keeping its chunk's best kp =
+// round_up(k, 4) elements (penalized) in index order in a virtual row of
+// split_width(p, V) entries; pass 2 samples the virtual rows and maps the
+// token back.
+constexpr size_t kRegMaxV = 32768;   // widest row the register kernel holds (1024 threads x 8 float4)
+constexpr int kSplitL = 1024;          // elements per chunk; the last chunk takes the rest (< 2 kSplitL)
+constexpr int kSplitMaxKp = 128;
+constexpr int kSplitMaxRows = 32;      // more rows fill the chip one workgroup per row
+constexpr size_t kSplitMaxWidth = 32768;
+bool split_fits(const gs_params &p, size_t V);
+size_t split_width(const gs_params &p, size_t V);
+hipError_t launch_split(const RowArgs &a, int B, float *vrow, uint32_t *vidx, hipStream_t st);
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st);
 hipError_t launch_synth(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0,

@@ -45,6 +45,8 @@ EXPORTS = [
     "gs_synth_logits", "gs_limits", "gs_version",
     # include/gs_gemv.h
     "gs_qmatrix_upload", "gs_qmatrix_destroy", "gs_qmatrix_shape", "gs_gemv",
+    # include/gs_decode.h
+    "gs_sampler_get_params", "gs_decode_init", "gs_decode_draw", "gs_decode_commit", "gs_decode_step",
 ]
 
 
@@ -57,6 +59,16 @@ class SamplerError(RuntimeError):
 class GsParams(ctypes.Structure):
     _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_uint32),
                 ("top_p", ctypes.c_float), ("rep_penalty", ctypes.c_float)]
+
+
+class DecodeCtx(ctypes.Structure):
+    """gs_decode_ctx (include/gs_decode.h)."""
+    _fields_ = [("B", ctypes.c_size_t), ("rows", ctypes.c_void_p), ("window", ctypes.c_void_p),
+                ("ld_window", ctypes.c_size_t), ("W", ctypes.c_size_t), ("window_len", ctypes.c_void_p),
+                ("stop", ctypes.c_void_p), ("n_stop", ctypes.c_size_t), ("max_new", ctypes.c_uint32),
+                ("generated", ctypes.c_void_p), ("ld_generated", ctypes.c_size_t), ("next", ctypes.c_void_p),
+                ("u", ctypes.c_void_p), ("tokens", ctypes.c_void_p), ("status", ctypes.c_void_p),
+                ("n_active", ctypes.c_void_p)]
 
 
 _lib = None
@@ -89,6 +101,11 @@ def load_library(path=LIB_PATH):
         "gs_qmatrix_destroy": ([P], I),
         "gs_qmatrix_shape": ([P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(SZ), ctypes.POINTER(SZ)], I),
         "gs_gemv": ([P, P, SZ, P, P], I),
+        "gs_sampler_get_params": ([P, ctypes.POINTER(GsParams)], I),
+        "gs_decode_init": ([ctypes.POINTER(DecodeCtx), P, P, P], I),
+        "gs_decode_draw": ([P, P, ctypes.POINTER(DecodeCtx), P], I),
+        "gs_decode_commit": ([ctypes.POINTER(DecodeCtx), P], I),
+        "gs_decode_step": ([P, P, P, P, SZ, SZ, P, ctypes.POINTER(DecodeCtx), P], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -350,3 +367,85 @@ class QMatrix:
             self.close()
         except Exception:
             pass
+
+
+# ---- device-resident decode loop (include/gs_decode.h) ------------------------
+DONE_RUNNING, DONE_STOP, DONE_MAX = 0, 1, 2
+
+
+def decode_row_dtype():
+    """numpy dtype of gs_decode_row (24 bytes)."""
+    import numpy as np
+    return np.dtype([("rng", "<u8"), ("n_gen", "<u4"), ("wpos", "<u4"), ("done", "<u4"), ("last", "<u4")])
+
+
+class Decoder:
+    """Device buffers of B decoding rows and the step of generate_collect
+    (src/main.rs:279-311) over them: sample, stop check, max-length check,
+    window push, generated push.  Buffers are torch tensors on cuda; every
+    method is stream-ordered and, apart from init() and the read-outs,
+    asynchronous."""
+
+    def __init__(self, B, W=64, max_new=256, stop=(), device="cuda"):
+        import torch
+        self._lib = load_library()
+        self.B, self.W, self.max_new = B, W, max_new
+        dev = torch.device(device)
+        u32 = torch.int32
+        self.rows = torch.zeros(B * 24, dtype=torch.uint8, device=dev)
+        self.window = torch.zeros((B, max(W, 1)), dtype=u32, device=dev)
+        self.window_len = torch.zeros(B, dtype=u32, device=dev)
+        stop = [int(s) for s in stop]
+        self.stop = torch.tensor(stop if stop else [0], dtype=torch.int64).to(u32).to(dev)
+        self.generated = torch.zeros((B, max(max_new, 1)), dtype=u32, device=dev)
+        self.next = torch.zeros(B, dtype=u32, device=dev)
+        self.u = torch.zeros(B, dtype=torch.float32, device=dev)
+        self.tokens = torch.zeros(B, dtype=u32, device=dev)
+        self.status = torch.zeros(B, dtype=u32, device=dev)
+        self.n_active = torch.zeros(1, dtype=u32, device=dev)
+        self.ctx = DecodeCtx(B, self.rows.data_ptr(), self.window.data_ptr() if W else None,
+                             self.window.stride(0), W, self.window_len.data_ptr() if W else None,
+                             self.stop.data_ptr() if stop else None, len(stop), max_new,
+                             self.generated.data_ptr(), self.generated.stride(0), self.next.data_ptr(),
+                             self.u.data_ptr(), self.tokens.data_ptr(), self.status.data_ptr(),
+                             self.n_active.data_ptr())
+
+    def init(self, seeds, init_recent=None, stream=None):
+        """Reset every row: LCG state = seeds[b] (set_seed, src/sampler.rs:5)
+        and the window holding init_recent[b] (the reference's `recent` at
+        the start of a turn, oldest first; at most W ids)."""
+        import numpy as np
+        import torch
+        sd = np.ascontiguousarray(np.asarray(seeds, dtype=np.uint64).reshape(self.B))
+        ln = np.zeros(self.B, np.uint32)
+        if init_recent is not None:
+            for b, r in enumerate(init_recent):
+                r = np.asarray(r, dtype=np.uint32)
+                if r.size > self.W:
+                    raise ValueError("init_recent row %d longer than W" % b)
+                ln[b] = r.size
+                if r.size:
+                    self.window[b, :r.size] = torch.from_numpy(r.view(np.int32)).to(self.window.device)
+        _check(self._lib.gs_decode_init(ctypes.byref(self.ctx), sd.ctypes.data, ln.ctypes.data,
+                                        _stream_handle(stream)), "gs_decode_init")
+
+    def step(self, sampler, logits=None, lm_head=None, x=None, params=None, stream=None):
+        """One step.  Either lm_head (a QMatrix) and x [B, cols] f32 with
+        `logits` a [B, rows] f32 output buffer, or logits [B, ld] holding
+        this step's logits."""
+        V = lm_head.rows if lm_head is not None else int(logits.shape[1])
+        ld = V if lm_head is not None else (int(logits.stride(0)) if self.B > 1 else V)
+        _check(self._lib.gs_decode_step(sampler._h, lm_head._h if lm_head is not None else None,
+                                        _ptr(x), _ptr(logits), V, ld, _ptr(params), ctypes.byref(self.ctx),
+                                        _stream_handle(stream)), "gs_decode_step")
+
+    def row_state(self):
+        """The B gs_decode_row records, copied to the host (synchronises)."""
+        import numpy as np
+        return self.rows.cpu().numpy().view(decode_row_dtype()).copy()
+
+    def generated_ids(self):
+        """Per row, the generated ids (list of numpy uint32 arrays)."""
+        st = self.row_state()
+        g = self.generated.cpu().numpy().view("<u4")
+        return [g[b, :min(int(st["n_gen"][b]), g.shape[1])].copy() for b in range(self.B)]

@@ -60,6 +60,7 @@ typedef struct gs_sampler gs_sampler;
 int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out);
 int gs_sampler_destroy(gs_sampler *s);
 int gs_sampler_set_params(gs_sampler *s, const gs_params *params);
+int gs_sampler_get_params(const gs_sampler *s, gs_params *params);
 /* set_seed (src/sampler.rs:5) for this sampler's stream. */
 int gs_sampler_set_seed(gs_sampler *s, uint64_t seed);
 /* Raw LCG state, so a decode trace can be checkpointed and resumed. */
@@ -67,8 +68,11 @@ int gs_sampler_get_state(const gs_sampler *s, uint64_t *state);
 int gs_sampler_set_state(gs_sampler *s, uint64_t state);
 
 /* Pre-allocate the full-vocabulary scratch (16*V bytes per row) for batches
- * of up to B rows, e.g. before capturing gs_sample_batch into a HIP graph
- * (the batch call otherwise allocates on first use). */
+ * of up to B rows, and for V > 32768 the buffers of the split top-k path
+ * (256 KB per row, at most 32 rows), e.g. before capturing gs_sample_batch
+ * into a HIP graph (the batch call otherwise allocates on first use; under
+ * capture, rows whose split buffers are missing take the one-workgroup-per-row
+ * path instead). */
 int gs_sampler_reserve(gs_sampler *s, size_t B, size_t V);
 
 /* ---- single row: sample(logits, recent) -> token -------------------------

@@ -55,6 +55,7 @@ def load(build_if_missing=True):
     lib.oracle_sample.restype = ctypes.c_int64
     lib.oracle_sample_batch.argtypes = [P, SZ, SZ, SZ, P, P, SZ, P, SZ, P, P, ctypes.c_int, ctypes.c_int]
     lib.oracle_decode_trace.argtypes = [P, SZ, SZ, F, SZ, F, F, SZ, P, SZ, U64, P, ctypes.c_int]
+    lib.oracle_generate.argtypes = [P, SZ, SZ, F, SZ, F, F, SZ, P, SZ, P, SZ, SZ, P, P, P, P, P, P, P]
     lib.oracle_synth_logit.argtypes = [U64, U64, F]
     lib.oracle_synth_logit.restype = F
     lib.oracle_synth_logits.argtypes = [P, SZ, U64, U64, F]
@@ -171,6 +172,34 @@ def decode_trace(logits, temperature, top_k, top_p, rep_penalty, window, init_re
     if st:
         raise RuntimeError("oracle_decode_trace failed: %d" % st)
     return tok
+
+
+def generate(logits, params, window, init_recent, stops, max_new, seed):
+    """generate_collect (src/main.rs:258-313) for one row over per-step
+    logits [steps, V].  Returns a dict: sampled (tokens of the steps taken),
+    generated, done (0 out of steps, 1 stop, 2 max), state (final LCG state),
+    recent (final FIFO, oldest first)."""
+    lib = load()
+    lg = _f32(logits)
+    steps, V = lg.shape
+    T, k, p, rep = params
+    ir = _u32(init_recent)
+    sp = _u32(stops)
+    st = ctypes.c_uint64(seed)
+    sampled = np.zeros(steps, np.int64)
+    n_steps, n_gen, rl = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    done = ctypes.c_int()
+    rec = np.zeros(max(window, 1), np.uint32)
+    rc = lib.oracle_generate(lg.ctypes.data, steps, V, T, k, p, rep, window,
+                             ir.ctypes.data if ir.size else None, ir.size,
+                             sp.ctypes.data if sp.size else None, sp.size, max_new,
+                             ctypes.byref(st), sampled.ctypes.data, ctypes.byref(n_steps),
+                             ctypes.byref(n_gen), ctypes.byref(done), rec.ctypes.data, ctypes.byref(rl))
+    if rc:
+        raise RuntimeError("oracle_generate failed: %d" % rc)
+    s = sampled[:n_steps.value]
+    return {"sampled": s, "generated": s[:n_gen.value].astype(np.uint32), "done": done.value,
+            "state": st.value, "recent": rec[:rl.value].copy()}
 
 
 def synth_logits(n, seed, counter0, sigma):

@@ -11,6 +11,7 @@
  *   - apply_rep_penalty        : src/sampler.rs:23-30
  *   - sample                   : src/sampler.rs:35-79
  *   - decode-loop recent FIFO  : src/main.rs:98, 280-281, 302-303
+ *   - generate_collect step    : src/main.rs:279-304 (stop / max checks)
  * Build with -O2 -ffp-contract=off and no fast-math, so that every f32
  * operation is one IEEE op in the same order as the Rust code.  f32::exp
  * lowers to the platform libm expf (glibc on linux-gnu), which is what this
@@ -302,6 +303,53 @@ int oracle_decode_trace(const float *logits, size_t steps, size_t V,
         recent[w++] = (uint32_t)tok;                 /* recent.push(next) */
         if (w > window) { memmove(recent, recent + 1, sizeof(uint32_t) * window); w = window; } /* remove(0) */
     }
+    free(row); free(recent);
+    return 0;
+}
+
+/* generate_collect (src/main.rs:258-313) for one row over given per-step
+ * logits: sample (:280), stop check (:281), max check (:282), recent FIFO
+ * push of the last `window` ids (:302-303), generated push (:304).  The
+ * smart-context branch (:284-296) is not part of it.  logits[t*V..] are the
+ * logits the row sees at step t; `steps` bounds the loop.  Outputs: sampled[t]
+ * for every step taken, *n_steps, *n_gen, *done (0 = ran out of steps, 1 =
+ * stop token, 2 = max), the LCG state after the loop in *state (in: the seed)
+ * and the final FIFO in recent_out[0..*recent_len), oldest first. */
+int oracle_generate(const float *logits, size_t steps, size_t V, float temperature,
+                    size_t top_k, float top_p, float rep_penalty, size_t window,
+                    const uint32_t *init_recent, size_t init_len, const uint32_t *stops,
+                    size_t n_stop, size_t max_new, uint64_t *state, int64_t *sampled,
+                    size_t *n_steps, size_t *n_gen, int *done, uint32_t *recent_out,
+                    size_t *recent_len)
+{
+    float *row = (float *)malloc(sizeof(float) * (V ? V : 1));
+    uint32_t *recent = (uint32_t *)malloc(sizeof(uint32_t) * (window + 1));
+    if (!row || !recent) { free(row); free(recent); return ORACLE_ERR_NOMEM; }
+    size_t w = init_len < window ? init_len : window;
+    if (w) memcpy(recent, init_recent + (init_len - w), sizeof(uint32_t) * w);
+    size_t gen = 0, t = 0;
+    int why = 0;
+    for (; t < steps; t++) {
+        memcpy(row, logits + t * V, sizeof(float) * V);
+        const int64_t tok = oracle_sample_ex(row, V, temperature, top_k, top_p, rep_penalty,
+                                             recent, w, 0.0f, temperature > 0.0f ? state : NULL, 0, NULL);
+        sampled[t] = tok;
+        if (tok < 0) { free(row); free(recent); return (int)tok; }
+        int is_stop = 0;
+        for (size_t i = 0; i < n_stop; i++) is_stop |= stops[i] == (uint32_t)tok;
+        if (is_stop) { why = 1; t++; break; }
+        if (gen >= max_new) { why = 2; t++; break; }
+        if (window) {
+            recent[w++] = (uint32_t)tok;
+            if (w > window) { memmove(recent, recent + 1, sizeof(uint32_t) * window); w = window; }
+        }
+        gen++;
+    }
+    *n_steps = t;
+    *n_gen = gen;
+    *done = why;
+    if (recent_out && w) memcpy(recent_out, recent, sizeof(uint32_t) * w);
+    *recent_len = w;
     free(row); free(recent);
     return 0;
 }

@@ -515,3 +515,73 @@ def test_c5_hip_graph(gpu, torch, oracle):
         torch.cuda.synchronize()
         check_tokens("c5 graph replay %d" % rep, d_toks.cpu().numpy().astype(np.int64), want)
         assert (d_win.cpu().numpy().view(np.uint32) == win).all()
+
+
+# --- split top-k rows (a few rows of a large vocabulary over many workgroups) ---
+def _split_rows(rng, B, V, shape):
+    if shape == "normal":
+        x = rng.standard_normal((B, V)) * 2.0
+    elif shape == "grid":        # many exact ties, before and after the division by T
+        x = rng.integers(-40, 40, size=(B, V)) / 4.0
+    elif shape == "equal":       # every logit equal: the top k are the k lowest ids
+        x = np.full((B, V), 1.5)
+    else:                        # spikes on a flat floor
+        x = rng.standard_normal((B, V)) * 0.5
+        for b in range(B):
+            x[b, rng.integers(0, V, 30)] += rng.uniform(6, 12, 30)
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("V,B,k,shape,T", [
+    (152064, 1, 40, "normal", 0.7),
+    (152064, 8, 1, "normal", 0.7),
+    (40000, 3, 100, "grid", 0.7),
+    (262144, 2, 128, "grid", 1.3),
+    (33000, 32, 40, "spike", 0.7),
+    (200001, 5, 7, "normal", 0.9),
+    (152064, 4, 40, "equal", 0.7),
+    (837999, 1, 40, "spike", 1.0),
+])
+def test_split_rows(gpu, torch, oracle, V, B, k, shape, T):
+    """Rows of V > 32768 with 0 < k <= 128 and at most 32 rows take the split
+    path: every chunk keeps its best round_up(k, 4) elements.  Penalty window
+    with duplicates, ids on chunk edges and ids >= V."""
+    rng = np.random.default_rng(V + B + k)
+    x = _split_rows(rng, B, V, shape)
+    W = 64
+    rec = rng.integers(0, V, size=(B, W)).astype(np.uint32)
+    rec[:, :6] = [1023, 1024, 1024, V - 1, V + 5, 0]
+    rec[:, 6:10] = rec[:, 10:14]                       # duplicates
+    u = rng.random(B).astype(np.float32)
+    u[0] = 0.0
+    for rep in (1.0, 1.3):
+        _say("split V", V, "B", B, "k", k, shape, "rep", rep)
+        params = [(T, k, 0.9, rep)] * B
+        tok, st, _ = run_batch(gpu, torch, x, u=u, recent=rec, uniform=(T, k, 0.9, rep))
+        want = oracle.sample_batch(x, params, u, recent=rec, nthreads=8, fast_topk=True)
+        check_tokens("split %s rep %s" % (shape, rep), tok, want, st)
+
+
+def test_split_rows_nan_and_single_call(gpu, torch, oracle):
+    """A NaN anywhere in a split row is an error for that row only; the
+    single-row call (gs_sample) takes the same path and draws from the LCG."""
+    rng = np.random.default_rng(5)
+    V, B = 152064, 3
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    x[1, 77777] = np.nan
+    u = rng.random(B).astype(np.float32)
+    tok, st, _ = run_batch(gpu, torch, x, u=u, uniform=(0.7, 40, 0.9, 1.0))
+    assert list(st) == [0, gpu.GS_ERR_NAN, 0], st
+    want = oracle.sample_batch(x[[0, 2]], [(0.7, 40, 0.9, 1.0)] * 2, u[[0, 2]], nthreads=4, fast_topk=True)
+    assert tok[0] == want[0] and tok[2] == want[1]
+    s = gpu.Sampler(0.7, 40, 0.9, 1.1, seed=42)
+    recent = np.array([3, 3, 9, V - 1, 1024], np.uint32)
+    d = torch.from_numpy(x[0]).cuda()
+    state = 42
+    for i in range(5):
+        got = s.sample(d, recent)
+        r, state = oracle.lcg_draws(state, 1)
+        w = oracle.sample(x[0], 0.7, 40, 0.9, 1.1, recent, r=float(r[0]))
+        assert got == w, (i, got, w)
+    with pytest.raises(gpu.SamplerError):
+        s.sample(torch.from_numpy(x[1]).cuda())
