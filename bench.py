@@ -252,13 +252,13 @@ def bench_decode(gs, torch, K=32, reps=5, cpu=True, gemv_us=0.0):
     logits = torch.empty((B, V), dtype=torch.float32, device="cuda")
 
     def reset():
-        dec.init([42])
+        dec.init(sampler, [42])
         dec.next.fill_(1)
         torch.cuda.synchronize()
 
     def steps(n, st=None):
         for _ in range(n):
-            torch.index_select(E, 0, dec.next.long(), out=x)
+            torch.index_select(E, 0, dec.next, out=x)
             dec.step(sampler, logits=logits, lm_head=m, x=x, stream=st)
 
     reset()

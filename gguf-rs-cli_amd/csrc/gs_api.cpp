@@ -86,7 +86,7 @@ int reserve_split(gs_sampler *s, size_t rows, size_t width)
     return grow(&s->split, &s->split_cap, split_bytes(rows, width));
 }
 
-hipError_t launch_split(gs_sampler *s, const gs::RowArgs &a, size_t B, size_t width, hipStream_t st)
+hipError_t launch_split_rows(gs_sampler *s, const gs::RowArgs &a, size_t B, size_t width, hipStream_t st)
 {
     float *vrow = (float *)s->split;
     return gs::launch_split(a, (int)B, vrow, (uint32_t *)(vrow + B * width), st);
@@ -279,7 +279,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
         for (;;) {
             a.done_val = ++s->seq;
             const hipError_t le = reg     ? gs::launch_reg_row(a, s->stream)
-                                  : split ? launch_split(s, a, 1, gs::split_width(s->params, V), s->stream)
+                                  : split ? launch_split_rows(s, a, 1, gs::split_width(s->params, V), s->stream)
                                           : gs::launch_sample_rows(a, 1, true, false, s->stream);
             if (le != hipSuccess) return GS_ERR_HIP;
             volatile uint64_t *f = s->h_done;
@@ -311,6 +311,18 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, si
                     const uint32_t *d_recent_len, size_t W, const float *d_u,
                     uint32_t *d_tokens, int32_t *d_status, void *stream)
 {
+    return gs::sample_batch(s, d_logits, B, V, ld, d_params, d_recent, ld_recent, d_recent_len, W, d_u, d_tokens,
+                            d_status, nullptr, stream);
+}
+
+} // extern "C"
+
+namespace gs {
+
+int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld, const gs_params *d_params,
+                 const uint32_t *d_recent, size_t ld_recent, const uint32_t *d_recent_len, size_t W,
+                 const float *d_u, uint32_t *d_tokens, int32_t *d_status, const DecodeHook *hook, void *stream)
+{
     if (!s || !d_tokens || (B > 0 && V > 0 && !d_logits) || ld < V) return GS_ERR_INVALID;
     if (d_recent && ld_recent < W) return GS_ERR_INVALID;
     if (!d_u && d_params) return GS_ERR_INVALID;   // LCG draws need host-known T per row
@@ -337,6 +349,7 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, si
     a.scratch = s->scratch;
     a.scratch_stride = gs::scratch_u32_per_row(V);
     a.fb = s->fb;
+    if (hook) a.hook = *hook;
     const bool full = d_params || needs_full_path(s->params, V);
     const bool small = d_params || !needs_full_path(s->params, V);
     bool split = !d_params && B <= (size_t)gs::kSplitMaxRows && gs::split_fits(s->params, V);
@@ -351,13 +364,17 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, si
         // a few rows of a large vocabulary: spread each row over the chip
         const size_t wd = gs::split_width(s->params, V);
         if ((rc = reserve_split(s, B, wd))) return rc;
-        if (launch_split(s, a, B, wd, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+        if (launch_split_rows(s, a, B, wd, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
     } else if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) {
         return GS_ERR_HIP;
     }
     if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
     return GS_OK;
 }
+
+} // namespace gs
+
+extern "C" {
 
 int gs_window_push(uint32_t *d_window, size_t B, size_t ld, size_t W, size_t pos,
                    const uint32_t *d_tokens, void *stream)

@@ -1178,6 +1178,24 @@ __device__ int full_row(RowSmem &sm, const float *row, int V, int keep, float T,
     return finish_sorted(sm, keep, yv, ix, top_p, r);
 }
 
+// The token and status of row b, written by thread 0 of the kernel that
+// finishes the row: into the mapped completion word (single-row calls), or
+// into tokens / status, followed by the decode step's commit of the row.
+__device__ __forceinline__ void store_row(const RowArgs &a, int b, int tok, int status)
+{
+    if (a.done) {
+        // Token, status and the call's sequence number in one 64-bit store:
+        // the host sees all three or none, so no fence is needed.
+        const uint64_t word = ((uint64_t)a.done_val << 32) | ((uint64_t)((uint32_t)status & 0xffu) << 24) |
+                              (uint64_t)((uint32_t)tok & 0xffffffu);
+        __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    } else {
+        a.tokens[b] = (uint32_t)tok;
+        if (a.status) a.status[b] = status;
+        if (a.hook.rows) decode_commit_row(a.hook, b, (uint32_t)tok, status);
+    }
+}
+
 // --------------------------------------------------------------------------
 // Row paths: the small kernel serves greedy, degenerate and top-k rows; the
 // full-vocabulary rows go to the binned kernel and, when its checks fail, to
@@ -1322,18 +1340,7 @@ sample_rows_kernel(RowArgs a)
 #ifdef GS_TIMING
     if (t == 0 && b < 256 && MODE == kModeBins) g_fails[256 + b] = (int)(__builtin_amdgcn_s_memrealtime() - t_begin);
 #endif
-    if (t == 0) {
-        if (a.done) {
-            // Token, status and the call's sequence number in one 64-bit
-            // store: the host sees all three or none, so no fence is needed.
-            const uint64_t word = ((uint64_t)a.done_val << 32) | ((uint64_t)((uint32_t)status & 0xffu) << 24) |
-                                  (uint64_t)((uint32_t)tok & 0xffffffu);
-            __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        } else {
-            a.tokens[b] = (uint32_t)tok;
-            if (a.status) a.status[b] = status;
-        }
-    }
+    if (t == 0) store_row(a, b, tok, status);
 }
 
 // Single-row register path as a kernel of its own (B = 1): only the code of
@@ -1392,16 +1399,7 @@ reg_row_kernel(RowArgs a)
         if (!ok) { tok = 0; status = kStatusRetry; }
     }
     GS_STAMP(7);
-    if (t == 0) {
-        if (a.done) {
-            const uint64_t word = ((uint64_t)a.done_val << 32) | ((uint64_t)((uint32_t)status & 0xffu) << 24) |
-                                  (uint64_t)((uint32_t)tok & 0xffffffu);
-            __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        } else {
-            a.tokens[b] = (uint32_t)tok;
-            if (a.status) a.status[b] = status;
-        }
-    }
+    if (t == 0) store_row(a, b, tok, status);
 }
 
 __global__ void window_push_kernel(uint32_t *win, int B, size_t ld, int W, size_t pos,
@@ -1608,17 +1606,7 @@ split_finish_kernel(RowArgs a, const float *vrow, const uint32_t *vidx, size_t v
     int tok = topk_row_reg(sm, vr, rv, pl, V2, k, p.temperature, p.top_p, false, 1.0f, r, &status, &ok);
     if (!ok) tok = topk_row<true>(sm, vr, V2, k, p.temperature, p.top_p, false, r, true, &status, &ok);
     if (!ok) tok = topk_row<false>(sm, vr, V2, k, p.temperature, p.top_p, false, r, true, &status, &ok);
-    if (t == 0) {
-        tok = status == GS_OK ? (int)ldg(vidx + (size_t)b * vld + tok) : 0;
-        if (a.done) {
-            const uint64_t word = ((uint64_t)a.done_val << 32) | ((uint64_t)((uint32_t)status & 0xffu) << 24) |
-                                  (uint64_t)((uint32_t)tok & 0xffffffu);
-            __hip_atomic_store(a.done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        } else {
-            a.tokens[b] = (uint32_t)tok;
-            if (a.status) a.status[b] = status;
-        }
-    }
+    if (t == 0) store_row(a, b, status == GS_OK ? (int)ldg(vidx + (size_t)b * vld + tok) : 0, status);
 }
 
 hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st)

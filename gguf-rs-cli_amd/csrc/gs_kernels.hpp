@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "../../include/gs_sampler.h"
+#include "gs_decode_dev.hpp"
 
 namespace gs {
 
@@ -30,6 +31,7 @@ struct RowArgs {
     uint64_t *done;                // optional (single-row calls, B = 1): receives
     uint32_t done_val;             // (done_val << 32) | (status & 0xff) << 24 | token in one store,
                                    // instead of tokens/status, for host polling
+    DecodeHook hook;               // decode step: the kernel that stores a row's token commits it
     int kwin_n;                    // single-row calls: a host window of W <= kKernWin ids passed
     uint32_t kwin[kKernWin];       // by value here (used instead of `recent` when kwin_n != 0)
 };
@@ -62,6 +64,11 @@ constexpr size_t kSplitMaxWidth = 32768;
 bool split_fits(const gs_params &p, size_t V);
 size_t split_width(const gs_params &p, size_t V);
 hipError_t launch_split(const RowArgs &a, int B, float *vrow, uint32_t *vidx, hipStream_t st);
+// gs_sample_batch with an optional decode hook (the sampler's last kernel
+// commits each row into it).
+int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld, const gs_params *d_params,
+                 const uint32_t *d_recent, size_t ld_recent, const uint32_t *d_recent_len, size_t W,
+                 const float *d_u, uint32_t *d_tokens, int32_t *d_status, const DecodeHook *hook, void *stream);
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st);
 hipError_t launch_synth(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0,

@@ -46,7 +46,7 @@ EXPORTS = [
     # include/gs_gemv.h
     "gs_qmatrix_upload", "gs_qmatrix_destroy", "gs_qmatrix_shape", "gs_gemv",
     # include/gs_decode.h
-    "gs_sampler_get_params", "gs_decode_init", "gs_decode_draw", "gs_decode_commit", "gs_decode_step",
+    "gs_sampler_get_params", "gs_decode_init", "gs_decode_commit", "gs_decode_step",
 ]
 
 
@@ -102,9 +102,8 @@ def load_library(path=LIB_PATH):
         "gs_qmatrix_shape": ([P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(SZ), ctypes.POINTER(SZ)], I),
         "gs_gemv": ([P, P, SZ, P, P], I),
         "gs_sampler_get_params": ([P, ctypes.POINTER(GsParams)], I),
-        "gs_decode_init": ([ctypes.POINTER(DecodeCtx), P, P, P], I),
-        "gs_decode_draw": ([P, P, ctypes.POINTER(DecodeCtx), P], I),
-        "gs_decode_commit": ([ctypes.POINTER(DecodeCtx), P], I),
+        "gs_decode_init": ([P, P, ctypes.POINTER(DecodeCtx), P, P, P], I),
+        "gs_decode_commit": ([P, P, ctypes.POINTER(DecodeCtx), P], I),
         "gs_decode_step": ([P, P, P, P, SZ, SZ, P, ctypes.POINTER(DecodeCtx), P], I),
     }
     for name, (args, res) in sig.items():
@@ -370,7 +369,7 @@ class QMatrix:
 
 
 # ---- device-resident decode loop (include/gs_decode.h) ------------------------
-DONE_RUNNING, DONE_STOP, DONE_MAX = 0, 1, 2
+DONE_RUNNING, DONE_STOP, DONE_MAX, DONE_ERROR = 0, 1, 2, 3
 
 
 def decode_row_dtype():
@@ -401,7 +400,7 @@ class Decoder:
         self.next = torch.zeros(B, dtype=u32, device=dev)
         self.u = torch.zeros(B, dtype=torch.float32, device=dev)
         self.tokens = torch.zeros(B, dtype=u32, device=dev)
-        self.status = torch.zeros(B, dtype=u32, device=dev)
+        self.status = torch.zeros(B, dtype=torch.int32, device=dev)
         self.n_active = torch.zeros(1, dtype=u32, device=dev)
         self.ctx = DecodeCtx(B, self.rows.data_ptr(), self.window.data_ptr() if W else None,
                              self.window.stride(0), W, self.window_len.data_ptr() if W else None,
@@ -410,10 +409,12 @@ class Decoder:
                              self.u.data_ptr(), self.tokens.data_ptr(), self.status.data_ptr(),
                              self.n_active.data_ptr())
 
-    def init(self, seeds, init_recent=None, stream=None):
+    def init(self, sampler, seeds, init_recent=None, params=None, stream=None):
         """Reset every row: LCG state = seeds[b] (set_seed, src/sampler.rs:5)
         and the window holding init_recent[b] (the reference's `recent` at
-        the start of a turn, oldest first; at most W ids)."""
+        the start of a turn, oldest first; at most W ids); then the first
+        step's draws with the rows' temperatures (params: device gs_params
+        per row, or None = the sampler's)."""
         import numpy as np
         import torch
         sd = np.ascontiguousarray(np.asarray(seeds, dtype=np.uint64).reshape(self.B))
@@ -426,8 +427,8 @@ class Decoder:
                 ln[b] = r.size
                 if r.size:
                     self.window[b, :r.size] = torch.from_numpy(r.view(np.int32)).to(self.window.device)
-        _check(self._lib.gs_decode_init(ctypes.byref(self.ctx), sd.ctypes.data, ln.ctypes.data,
-                                        _stream_handle(stream)), "gs_decode_init")
+        _check(self._lib.gs_decode_init(sampler._h, _ptr(params), ctypes.byref(self.ctx), sd.ctypes.data,
+                                        ln.ctypes.data, _stream_handle(stream)), "gs_decode_init")
 
     def step(self, sampler, logits=None, lm_head=None, x=None, params=None, stream=None):
         """One step.  Either lm_head (a QMatrix) and x [B, cols] f32 with
@@ -438,6 +439,12 @@ class Decoder:
         _check(self._lib.gs_decode_step(sampler._h, lm_head._h if lm_head is not None else None,
                                         _ptr(x), _ptr(logits), V, ld, _ptr(params), ctypes.byref(self.ctx),
                                         _stream_handle(stream)), "gs_decode_step")
+
+    def commit(self, sampler, params=None, stream=None):
+        """gs_decode_commit: commit self.tokens (sampled by the caller) and
+        draw the next step's u."""
+        _check(self._lib.gs_decode_commit(sampler._h, _ptr(params), ctypes.byref(self.ctx),
+                                          _stream_handle(stream)), "gs_decode_commit")
 
     def row_state(self):
         """The B gs_decode_row records, copied to the host (synchronises)."""

@@ -26,7 +26,11 @@
  * (src/sampler.rs:3-12), seeded like set_seed (src/sampler.rs:5).  A row
  * with B = 1 and the CLI's seed reproduces the reference's token stream
  * exactly (one draw per step iff T > 0; the step that samples a stop token
- * consumes its draw, as at src/main.rs:280-281).
+ * consumes its draw, as at src/main.rs:280-281).  Each step's draw is made
+ * ahead of it: by gs_decode_init for the first step, then by the commit of
+ * the step before, for rows that go on (ctx->u holds it).  So a finished
+ * row's rng is the reference's final state; a running row's is one draw
+ * ahead of the steps it has taken.
  *
  * The window is a ring of W slots per row (W = 64 in the reference): the
  * penalty depends only on how often each id occurs in it, so the ring equals
@@ -49,6 +53,7 @@ extern "C" {
 #define GS_DONE_RUNNING 0u
 #define GS_DONE_STOP    1u   /* sampled a stop token (src/main.rs:281) */
 #define GS_DONE_MAX     2u   /* generated max_new tokens (src/main.rs:282) */
+#define GS_DONE_ERROR   3u   /* the sampler failed on the row (a NaN logit: the reference panics) */
 
 /* Most stop ids one call accepts (the reference's set is the EOS ids plus a
  * template's extras, src/tokenizer/chat.rs:57-72). */
@@ -79,38 +84,38 @@ typedef struct gs_decode_ctx {
     uint32_t *generated;        /* [B][ld_generated] generated ids, or NULL */
     size_t ld_generated;        /* ids past ld_generated are not stored */
     uint32_t *next;             /* [B] the token each running row feeds to its next forward, or NULL */
-    float *u;                   /* [B] scratch: this step's draws */
+    float *u;                   /* [B] the next step's draws */
     uint32_t *tokens;           /* [B] scratch: this step's sampled tokens */
     int32_t *status;            /* [B] per-row sampler statuses, or NULL */
-    uint32_t *n_active;         /* [1] rows still running after the step, or NULL */
+    uint32_t *n_active;         /* [1] rows still running (set by init, decremented as rows end), or NULL */
 } gs_decode_ctx;
 
 /* Reset B rows: rng = seeds[b] (host array), n_gen = 0, done = running,
  * wpos = window_len[b] = init_len[b] (host array or NULL = 0; the caller has
  * written those ids to window slots 0..init_len-1, the reference's `recent`
- * at the start of a turn, oldest first, src/main.rs:98, 198).  Asynchronous
- * on `stream`; the host arrays are consumed before return. */
-int gs_decode_init(const gs_decode_ctx *ctx, const uint64_t *seeds, const uint32_t *init_len, void *stream);
+ * at the start of a turn, oldest first, src/main.rs:98, 198), *n_active = B;
+ * then the first step's draws: u[b] = rand_f32() of row b's LCG
+ * (src/sampler.rs:7-12) iff the row's temperature (d_params[b], or the
+ * sampler's when d_params is NULL) is > 0.  Synchronous. */
+int gs_decode_init(gs_sampler *s, const gs_params *d_params, const gs_decode_ctx *ctx, const uint64_t *seeds,
+                   const uint32_t *init_len, void *stream);
 
-/* Draw this step's u for every running row: u[b] = rand_f32() of the row's
- * LCG (src/sampler.rs:7-12), the state advanced by one, iff the row's
- * temperature is > 0 (d_params[b], or the sampler's params when d_params is
- * NULL); finished rows and rows with T <= 0 draw nothing. */
-int gs_decode_draw(gs_sampler *s, const gs_params *d_params, const gs_decode_ctx *ctx, void *stream);
-
-/* Commit this step's tokens (ctx->tokens) for every running row, in the
- * reference's order: a stop token ends the row (GS_DONE_STOP); else a row
- * with n_gen >= max_new ends (GS_DONE_MAX); else the token goes to the
- * window ring, to generated[n_gen] and to next[b], and n_gen grows by one.
- * Writes *n_active.  One workgroup; the stop ids are staged in LDS. */
-int gs_decode_commit(const gs_decode_ctx *ctx, void *stream);
+/* Commit this step's tokens (ctx->tokens, statuses ctx->status or all OK)
+ * for every running row, in the reference's order: a failed sample ends the
+ * row (GS_DONE_ERROR); a stop token ends it (GS_DONE_STOP); else a row with
+ * n_gen >= max_new ends (GS_DONE_MAX); else the token goes to the window
+ * ring, to generated[n_gen] and to next[b], n_gen grows by one, and the
+ * next step's u[b] is drawn (T > 0).  For callers that sample on their own;
+ * gs_decode_step does this inside the sampler's last kernel. */
+int gs_decode_commit(gs_sampler *s, const gs_params *d_params, const gs_decode_ctx *ctx, void *stream);
 
 /* One whole decode step, stream-ordered and free of host synchronisation
  * and allocation (call gs_sampler_reserve(s, B, V) first when the rows take
- * the full-vocabulary path):
+ * the full-vocabulary or split paths):
  *   lm_head != NULL: d_logits[b*V + r] = gs_gemv(lm_head, d_x)   (V = rows of lm_head, ld = V)
  *   lm_head == NULL: the caller's logits are already in d_logits (row stride ld)
- *   gs_decode_draw; gs_sample_batch with the ring window; gs_decode_commit.
+ *   then gs_sample_batch with the ring window and ctx->u, whose last kernel
+ *   commits each row as gs_decode_commit does.
  * Rows that have finished are still sampled (their tokens are discarded);
  * a serving loop compacts its batch instead. */
 int gs_decode_step(gs_sampler *s, const gs_qmatrix *lm_head, const float *d_x,

@@ -67,13 +67,16 @@ def test_decode_arguments_rejected_without_gpu():
     import gs_sampler
     lib = gs_sampler.load_library()
     ctx = gs_sampler.DecodeCtx()
-    assert lib.gs_decode_commit(None, None) == gs_sampler.GS_ERR_INVALID
-    assert lib.gs_decode_commit(ctypes.byref(ctx), None) == gs_sampler.GS_ERR_INVALID
+    assert lib.gs_decode_commit(None, None, None, None) == gs_sampler.GS_ERR_INVALID
+    assert lib.gs_decode_commit(None, None, ctypes.byref(ctx), None) == gs_sampler.GS_ERR_INVALID
     ctx.B, ctx.rows, ctx.u, ctx.tokens = 4, 0x1000, 0x2000, 0x3000
     ctx.n_stop, ctx.stop = 1000, 0x4000
-    assert lib.gs_decode_commit(ctypes.byref(ctx), None) == gs_sampler.GS_ERR_UNSUPPORTED
+    assert lib.gs_decode_commit(None, None, ctypes.byref(ctx), None) == gs_sampler.GS_ERR_UNSUPPORTED
     ctx.n_stop, ctx.W, ctx.window = 0, 8, None
-    assert lib.gs_decode_commit(ctypes.byref(ctx), None) == gs_sampler.GS_ERR_INVALID
+    assert lib.gs_decode_commit(None, None, ctypes.byref(ctx), None) == gs_sampler.GS_ERR_INVALID
+    ctx.W = 0
+    assert lib.gs_decode_commit(None, None, ctypes.byref(ctx), None) == gs_sampler.GS_ERR_INVALID   # no sampler
+    assert lib.gs_decode_init(None, None, ctypes.byref(ctx), None, None, None) == gs_sampler.GS_ERR_INVALID
     ctx.W = 0
     assert lib.gs_decode_step(None, None, None, None, 0, 0, None, ctypes.byref(ctx), None) == gs_sampler.GS_ERR_INVALID
 
@@ -91,7 +94,7 @@ class _Toy:
         self.V, self.cols = V, cols
 
     def embed(self, torch, tokens, x):
-        torch.index_select(self.E, 0, tokens.long(), out=x)
+        torch.index_select(self.E, 0, tokens, out=x)
 
 
 def _run_eager(gpu, torch, toy, dec, sampler, first, steps, params=None):
@@ -150,13 +153,13 @@ def test_decode_step_matches_reference_loop(gpu, torch, oracle):
     sampler.reserve(B, V)
     # run 1: no stops, to learn the streams; then stop on ids seen mid-run
     dec = gpu.Decoder(B, W=W, max_new=max_new, stop=())
-    dec.init(seeds, init)
+    dec.init(sampler, seeds, init, params=d_params)
     hist = _run_eager(gpu, torch, toy, dec, sampler, first, max_new + 1, d_params)
     _check_rows(oracle, dec, hist, row_params, W, init, [], max_new, seeds)
     g1 = dec.generated_ids()
     stops = [int(g1[0][9]), int(g1[2][4]), V + 5]
     dec2 = gpu.Decoder(B, W=W, max_new=max_new, stop=stops)
-    dec2.init(seeds, init)
+    dec2.init(sampler, seeds, init, params=d_params)
     hist2 = _run_eager(gpu, torch, toy, dec2, sampler, first, max_new + 1, d_params)
     st = _check_rows(oracle, dec2, hist2, row_params, W, init, stops, max_new, seeds)
     assert st["done"][0] == gpu.DONE_STOP and st["done"][2] == gpu.DONE_STOP
@@ -178,7 +181,7 @@ def test_decode_single_row_reference_defaults(gpu, torch, oracle):
     stops = [int(oracle.decode_trace(lg, *DEFAULTS, W, init[0], 42)[33])]
     sampler = gpu.Sampler(*DEFAULTS, seed=42)
     dec = gpu.Decoder(1, W=W, max_new=50, stop=stops)
-    dec.init([42], init)
+    dec.init(sampler, [42], init)
     d_lg = torch.from_numpy(lg).cuda()
     for t in range(steps):
         dec.step(sampler, logits=d_lg[t:t + 1])
@@ -202,7 +205,7 @@ def test_decode_graph_replays(gpu, torch, oracle):
 
     def fresh():
         d = gpu.Decoder(B, W=W, max_new=K * R + 5, stop=())
-        d.init(seeds)
+        d.init(sampler, seeds)
         d.next.copy_(torch.tensor(first, dtype=torch.int32).cuda())
         return d
 
@@ -225,7 +228,7 @@ def test_decode_graph_replays(gpu, torch, oracle):
         toy.embed(torch, dec.next, x)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    dec.init(seeds)
+    dec.init(sampler, seeds)
     dec.next.copy_(torch.tensor(first, dtype=torch.int32).cuda())
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -250,3 +253,34 @@ def test_decode_graph_replays(gpu, torch, oracle):
         torch.cuda.synchronize()
     # and the eager run itself is the reference loop
     toy.m.close()
+
+
+@pytest.mark.gpu
+def test_decode_commit_entry_and_errors(gpu, torch, oracle):
+    """gs_decode_commit after the caller's own gs_sample_batch gives the same
+    state as gs_decode_step; a NaN logit ends its row with GS_DONE_ERROR and
+    n_active counts the rows still running."""
+    V, B, W, steps = 50000, 2, 64, 12
+    rng = np.random.default_rng(9)
+    lg = (rng.standard_normal((steps, B, V)) * 3).astype(np.float32)
+    lg[5, 1, 1234] = np.nan
+    d_lg = torch.from_numpy(lg).cuda()
+    sampler = gpu.Sampler(*DEFAULTS, seed=1)
+    sampler.reserve(B, V)
+    a = gpu.Decoder(B, W=W, max_new=100)
+    b = gpu.Decoder(B, W=W, max_new=100)
+    a.init(sampler, [42, 43])
+    b.init(sampler, [42, 43])
+    lib = gpu.load_library()
+    for t in range(steps):
+        a.step(sampler, logits=d_lg[t])
+        sampler.sample_batch(d_lg[t], b.tokens, recent=b.window, recent_len=b.window_len, u=b.u, status=b.status)
+        assert lib.gs_decode_commit(sampler._h, None, ctypes.byref(b.ctx), None) == 0
+    torch.cuda.synchronize()
+    sa, sb = a.row_state(), b.row_state()
+    assert np.array_equal(sa, sb)
+    assert sa["done"][1] == gpu.DONE_ERROR and sa["n_gen"][1] == 5 and sa["done"][0] == gpu.DONE_RUNNING
+    assert int(a.n_active.cpu()[0]) == 1 and int(b.n_active.cpu()[0]) == 1
+    assert np.array_equal(a.generated.cpu().numpy(), b.generated.cpu().numpy())
+    o = oracle.generate(lg[:, 0], DEFAULTS, W, [], [], 100, 42)
+    assert np.array_equal(a.generated_ids()[0], o["sampled"].astype(np.uint32))
