@@ -333,6 +333,36 @@ def bench_decode(gs, torch, K=32, reps=5, cpu=True, gemv_us=0.0):
     return out
 
 
+def bench_token_decode(gs):
+    """The host text step after the sampler (include/gs_tokens.h): a
+    Qwen2.5-sized GPT-2 vocabulary (151936 tokens of 1-8 random bytes,
+    synthetic), 200000 random ids decoded through gs_tokens_decode (the
+    reference's Tokenizer::decode, src/tokenizer/bpe.rs:180-197, per printed
+    token); the oracle's restatement timed on 20000 ids as the baseline."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import tokens_oracle
+    rng = np.random.default_rng(3)
+    enc = tokens_oracle.byte_encoder()
+    vocab = ["".join(enc[b] for b in rng.integers(0, 256, int(n))) for n in rng.integers(1, 9, 151936)]
+    t0 = time.perf_counter()
+    v = gs.Vocab(vocab, [1] * len(vocab), gs.TOK_GPT2)
+    t_build = time.perf_counter() - t0
+    ids = rng.integers(0, len(vocab), 200000).astype(np.uint32)
+    v.decode_bytes(ids[:1000])
+    t0 = time.perf_counter()
+    out = v.decode_bytes(ids)
+    t_dec = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    ref = "".join(tokens_oracle.decode(vocab, [], tokens_oracle.GPT2, int(i)) for i in ids[:20000])
+    t_ref = time.perf_counter() - t0
+    ok = out.decode("utf-8").startswith(ref)
+    v.close()
+    return {"vocab": len(vocab), "ids": int(ids.size), "ns_per_token": t_dec / ids.size * 1e9,
+            "vocab_build_ms": t_build * 1e3, "matches_oracle": bool(ok),
+            "cpu_baseline": {"value": t_ref / 20000 * 1e9, "unit": "ns per token", "cores": 1, "kind": "port",
+                             "sample": "oracle/tokens_oracle.py decode on the first 20000 ids"}}
+
+
 def calib_copy(torch, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of a known size: its FETCH_SIZE and
     WRITE_SIZE per dispatch give the scale factor of those counters."""
@@ -454,6 +484,7 @@ def main():
                        "V": 32000, "B": 1, "steps": 256},
         "lm_head_gemv": gemv,
         "decode_step": dstep,
+        "token_decode": bench_token_decode(gs),
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(c3)

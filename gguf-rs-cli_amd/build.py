@@ -25,7 +25,7 @@ HIP_FLAGS = [
     "-mllvm", "-amdgpu-function-calls=false",
     "-Wall", "-Wno-unused-function",
 ]
-SOURCES = ["gs_kernels.hip", "gs_api.cpp", "gs_gemv.hip", "gs_decode.hip"]
+SOURCES = ["gs_kernels.hip", "gs_api.cpp", "gs_gemv.hip", "gs_decode.hip", "gs_tokens.cpp"]
 
 
 def _run(cmd, cwd=None):

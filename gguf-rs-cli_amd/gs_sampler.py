@@ -47,6 +47,9 @@ EXPORTS = [
     "gs_qmatrix_upload", "gs_qmatrix_destroy", "gs_qmatrix_shape", "gs_gemv",
     # include/gs_decode.h
     "gs_sampler_get_params", "gs_decode_init", "gs_decode_commit", "gs_decode_step",
+    # include/gs_tokens.h
+    "gs_vocab_create", "gs_vocab_destroy", "gs_vocab_find", "gs_token_decode", "gs_tokens_decode",
+    "gs_chat_template_detect", "gs_stop_tokens",
 ]
 
 
@@ -105,6 +108,13 @@ def load_library(path=LIB_PATH):
         "gs_decode_init": ([P, P, ctypes.POINTER(DecodeCtx), P, P, P], I),
         "gs_decode_commit": ([P, P, ctypes.POINTER(DecodeCtx), P], I),
         "gs_decode_step": ([P, P, P, P, SZ, SZ, P, ctypes.POINTER(DecodeCtx), P], I),
+        "gs_vocab_create": ([P, P, SZ, P, SZ, ctypes.c_uint32, ctypes.POINTER(P)], I),
+        "gs_vocab_destroy": ([P], I),
+        "gs_vocab_find": ([P, ctypes.c_char_p, SZ, ctypes.POINTER(ctypes.c_uint32)], I),
+        "gs_token_decode": ([P, ctypes.c_uint32, P, SZ, ctypes.POINTER(SZ)], I),
+        "gs_tokens_decode": ([P, P, SZ, P, SZ, ctypes.POINTER(SZ)], I),
+        "gs_chat_template_detect": ([P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)], I),
+        "gs_stop_tokens": ([P, ctypes.c_uint32, P, SZ, P, SZ, ctypes.POINTER(SZ)], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -456,3 +466,78 @@ class Decoder:
         st = self.row_state()
         g = self.generated.cpu().numpy().view("<u4")
         return [g[b, :min(int(st["n_gen"][b]), g.shape[1])].copy() for b in range(self.B)]
+
+
+# ---- token text and stop set (include/gs_tokens.h) -----------------------------
+TOK_LLAMA, TOK_GPT2 = 0, 1
+TMPL_CHATML, TMPL_LLAMA3, TMPL_LLAMA2, TMPL_GEMMA, TMPL_PHI3, TMPL_SIMPLE = range(6)
+
+
+class Vocab:
+    """The tokenizer's vocabulary for the text step after the sampler:
+    decode(id) is Tokenizer::decode (src/tokenizer/bpe.rs:180-197),
+    detect / stop_tokens are ChatTemplate's (src/tokenizer/chat.rs:9-72).
+    `tokens` are str or bytes; `types` the GGUF token types; `model` is
+    TOK_LLAMA or TOK_GPT2.  Host-only."""
+
+    def __init__(self, tokens, types=(), model=TOK_LLAMA):
+        import numpy as np
+        self._lib = load_library()
+        raw = [t.encode("utf-8") if isinstance(t, str) else bytes(t) for t in tokens]
+        off = np.zeros(len(raw) + 1, np.uint64)
+        off[1:] = np.cumsum([len(r) for r in raw], dtype=np.uint64)
+        data = b"".join(raw)
+        ty = np.ascontiguousarray(np.asarray(types, dtype=np.uint32))
+        self._data = ctypes.create_string_buffer(data, max(len(data), 1))
+        h = ctypes.c_void_p()
+        _check(self._lib.gs_vocab_create(self._data, off.ctypes.data, len(raw),
+                                         ty.ctypes.data if ty.size else None, ty.size, model,
+                                         ctypes.byref(h)), "gs_vocab_create")
+        self._h = h
+
+    def find(self, s):
+        b = s.encode("utf-8") if isinstance(s, str) else bytes(s)
+        out = ctypes.c_uint32()
+        _check(self._lib.gs_vocab_find(self._h, b, len(b), ctypes.byref(out)), "gs_vocab_find")
+        return None if out.value == 0xFFFFFFFF else int(out.value)
+
+    def decode_bytes(self, ids):
+        """The UTF-8 bytes of decode(id) concatenated over ids (an int or a sequence)."""
+        import numpy as np
+        a = np.ascontiguousarray(np.atleast_1d(np.asarray(ids, dtype=np.uint32)))
+        n = ctypes.c_size_t()
+        _check(self._lib.gs_tokens_decode(self._h, a.ctypes.data, a.size, None, 0, ctypes.byref(n)),
+               "gs_tokens_decode")
+        buf = ctypes.create_string_buffer(max(n.value, 1))
+        _check(self._lib.gs_tokens_decode(self._h, a.ctypes.data, a.size, buf, n.value, ctypes.byref(n)),
+               "gs_tokens_decode")
+        return buf.raw[:n.value]
+
+    def decode(self, ids):
+        return self.decode_bytes(ids).decode("utf-8")
+
+    def detect(self, tmpl=None):
+        out = ctypes.c_uint32()
+        _check(self._lib.gs_chat_template_detect(self._h, None if tmpl is None else tmpl.encode("utf-8"),
+                                                 ctypes.byref(out)), "gs_chat_template_detect")
+        return int(out.value)
+
+    def stop_tokens(self, kind, eos_ids):
+        import numpy as np
+        e = np.ascontiguousarray(np.asarray(eos_ids, dtype=np.uint32))
+        n = ctypes.c_size_t()
+        out = np.zeros(len(eos_ids) + 8, np.uint32)
+        _check(self._lib.gs_stop_tokens(self._h, kind, e.ctypes.data if e.size else None, e.size,
+                                        out.ctypes.data, out.size, ctypes.byref(n)), "gs_stop_tokens")
+        return [int(x) for x in out[:n.value]]
+
+    def close(self):
+        if self._h:
+            self._lib.gs_vocab_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
