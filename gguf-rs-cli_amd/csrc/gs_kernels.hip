@@ -15,6 +15,7 @@
 #include "gs_block.hpp"
 #include "gs_kernels.hpp"
 #include "gs_bins_smem.hpp"
+#include "gs_select.hpp"
 
 namespace gs {
 
@@ -1460,120 +1461,28 @@ namespace gs {
 // Pass 2 samples the virtual rows.
 constexpr int kSplitThreads = 256;
 constexpr int kSplitPer = 2 * kSplitL / kSplitThreads;   // elements per thread, last chunk included
-static_assert(kRegMaxV == (size_t)kThreads * 4 * kRegF4, "register row width");
-
-struct SplitSmem {
-    uint32_t cnt[2 * kSplitL];          // window occurrences per chunk element
-    uint64_t tmax[kSplitThreads];
-    uint64_t cand[kSplitPer * kSplitMaxKp];
-    float candx[kSplitPer * kSplitMaxKp];
-    uint64_t top[kSplitMaxKp];
-    float topx[kSplitMaxKp];
-    uint64_t tau;
-    int ncand;
-    int nan;
-};
-static_assert(kSplitMaxKp <= kSplitThreads, "one thread per kept element");
+static_assert(kSplitMaxKp == kSelMaxKp, "split kp bound");
 
 __global__ void __launch_bounds__(kSplitThreads)
 split_select_kernel(RowArgs a, int nch, int kp, float *vrow, uint32_t *vidx, size_t vld)
 {
-    __shared__ SplitSmem sm;
-    const int t = threadIdx.x;
+    __shared__ SelSmem<kSplitThreads, kSplitPer> sm;
     const int c = blockIdx.x, b = blockIdx.y;
-    const gs_params p = a.uparams;
-    const int V = a.V;
     const int c0 = c * kSplitL;
-    const int L = c == nch - 1 ? V - c0 : kSplitL;
+    const int L = c == nch - 1 ? a.V - c0 : kSplitL;
     const float *row = a.logits + (size_t)b * a.ld + c0;
-    const bool has_pen = p.rep_penalty != 1.0f && a.recent != nullptr;
-    int W = 0;
-    if (has_pen) {
-        W = a.recent_len ? (int)a.recent_len[b] : a.W;
-        if (W > a.W) W = a.W;
-    }
-    float x[kSplitPer];
-#pragma unroll
-    for (int u = 0; u < kSplitPer; u++) {
-        const int i = u * kSplitThreads + t;
-        x[u] = i < L ? ldg(row + i) : -INFINITY;
-    }
-    if (has_pen)
-        for (int i = t; i < L; i += kSplitThreads) sm.cnt[i] = 0u;
-    if (t == 0) { sm.ncand = 0; sm.nan = 0; }
-    __syncthreads();
-    if (has_pen) {
-        const uint32_t *rec = a.recent + (size_t)b * a.ld_recent;
-        for (int j = t; j < W; j += kSplitThreads) {
-            const uint32_t d = ldg(rec + j) - (uint32_t)c0;   // ids >= V never fall in a chunk
-            if (d < (uint32_t)L) atomicAdd(&sm.cnt[d], 1u);
-        }
-        __syncthreads();
-    }
-    uint64_t key[kSplitPer];
-    uint64_t best = 0ull;
-    bool nan = false;
-#pragma unroll
-    for (int u = 0; u < kSplitPer; u++) {
-        const int i = u * kSplitThreads + t;
-        key[u] = 0ull;
-        if (i < L) {
-            float xv = x[u];
-            if (has_pen) {
-                const uint32_t n = sm.cnt[i];
-                if (n) xv = penalize(xv, n, p.rep_penalty);
-            }
-            x[u] = xv;
-            const float y = xv / p.temperature;
-            nan |= isnan(y);
-            key[u] = cand_of(f2key(y), (uint32_t)(c0 + i));
-            best = key[u] > best ? key[u] : best;
-        }
-    }
-    sm.tmax[t] = best;
-    if (__any(nan) && lane_id() == 0) sm.nan = 1;
-    __syncthreads();
-    // Every thread holds at least L / kSplitThreads >= 4 elements, so the
-    // kp-th largest thread maximum (keys are distinct: they carry the id)
-    // bounds the kp-th largest element: at least kp elements reach it, at
-    // most kp * kSplitPer.
-    {
-        int rk = 0;
-        const ulonglong2 *t2 = reinterpret_cast<const ulonglong2 *>(sm.tmax);
-#pragma unroll 8
-        for (int j = 0; j < kSplitThreads / 2; j++) {
-            const ulonglong2 v = t2[j];
-            rk += (v.x > best) + (v.y > best);
-        }
-        if (rk == kp - 1) sm.tau = best;
-    }
-    __syncthreads();
-    const uint64_t tau = sm.tau;
-#pragma unroll
-    for (int u = 0; u < kSplitPer; u++) {
-        if (key[u] >= tau && key[u] != 0ull) {
-            const int pos = atomicAdd(&sm.ncand, 1);
-            sm.cand[pos] = key[u];
-            sm.candx[pos] = x[u];
-        }
-    }
-    __syncthreads();
-    const int nc = sm.ncand;
-    for (int i = t; i < nc; i += kSplitThreads) {
-        const uint64_t me = sm.cand[i];
-        int rk = 0;
-        for (int j = 0; j < nc; j++) rk += sm.cand[j] > me;
-        if (rk < kp) { sm.top[rk] = me; sm.topx[rk] = sm.candx[i]; }
-    }
-    __syncthreads();
-    if (t < kp) {
-        const uint32_t id = ~(uint32_t)sm.top[t];
-        int pos = 0;
-        for (int j = 0; j < kp; j++) pos += (~(uint32_t)sm.top[j]) < id;
-        const size_t o = (size_t)b * vld + (size_t)c * kp + pos;
-        vrow[o] = (sm.nan && pos == 0) ? __builtin_nanf("") : sm.topx[t];
-        vidx[o] = id;
-    }
+    SelArgs s;
+    s.T = a.uparams.temperature;
+    s.rep = a.uparams.rep_penalty;
+    s.kp = kp;
+    s.recent = a.recent;
+    s.ld_recent = a.ld_recent;
+    s.recent_len = a.recent_len;
+    s.W = a.W;
+    s.vrow = vrow;
+    s.vidx = vidx;
+    s.vld = vld;
+    chunk_select<kSplitThreads, kSplitPer>(sm, s, b, c, c0, L, [row](int i) { return ldg(row + i); });
 }
 
 // Pass 2: sample virtual row b (width vld, a multiple of 4, 16-byte aligned;

@@ -284,3 +284,70 @@ def test_decode_commit_entry_and_errors(gpu, torch, oracle):
     assert np.array_equal(a.generated.cpu().numpy(), b.generated.cpu().numpy())
     o = oracle.generate(lg[:, 0], DEFAULTS, W, [], [], 100, 42)
     assert np.array_equal(a.generated_ids()[0], o["sampled"].astype(np.uint32))
+
+
+@pytest.mark.gpu
+def test_decode_large_vocab_split_rows(gpu, torch, oracle):
+    """A large vocabulary (V = 152064), a few rows, uniform params: the
+    decode step's sampler takes the split top-k path (chunk selection over
+    the chip, then the virtual row).  Tokens, stop reasons, LCG states and
+    windows must equal the oracle's loop over the same logits; a captured
+    graph of the same steps must reproduce the eager run."""
+    V, cols, B, W, max_new, steps = 152064, 256, 3, 64, 14, 16
+    import workloads
+    blocks = workloads.synth_qblocks(gpu.QTYPE_Q6_K, V, cols, seed=31)
+    m = gpu.QMatrix(gpu.QTYPE_Q6_K, blocks, V, cols)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    E = torch.randn((V, cols), generator=g, device="cuda") * 0.2
+    sampler = gpu.Sampler(*DEFAULTS, seed=1)
+    sampler.reserve(B, V)
+    seeds = [42, 5, 77]
+    rng = np.random.default_rng(8)
+    init = [np.concatenate([[1023, 1024, 1024, V - 1], rng.integers(0, V, 20)]).astype(np.uint32),
+            np.zeros(0, np.uint32), rng.integers(0, V, 64).astype(np.uint32)]
+    x = torch.empty((B, cols), dtype=torch.float32, device="cuda")
+    logits = torch.empty((B, V), dtype=torch.float32, device="cuda")
+
+    def run(dec, stops, capture=False):
+        dec.init(sampler, seeds, init)
+        dec.next.copy_(torch.tensor([3, 4, 5], dtype=torch.int32).cuda())
+        hist = torch.empty((steps, B, V), dtype=torch.float32, device="cuda")
+        for t in range(steps):
+            torch.index_select(E, 0, dec.next, out=x)
+            dec.step(sampler, logits=logits, lm_head=m, x=x)
+            hist[t].copy_(logits)
+        torch.cuda.synchronize()
+        return hist.cpu().numpy()
+
+    dec = gpu.Decoder(B, W=W, max_new=max_new)
+    hist = run(dec, [])
+    _check_rows(oracle, dec, hist, [DEFAULTS] * B, W, init, [], max_new, seeds)
+    g1 = dec.generated_ids()
+    stops = [int(g1[1][6]), V + 1]
+    dec2 = gpu.Decoder(B, W=W, max_new=max_new, stop=stops)
+    hist2 = run(dec2, stops)
+    st = _check_rows(oracle, dec2, hist2, [DEFAULTS] * B, W, init, stops, max_new, seeds)
+    assert st["done"][1] == gpu.DONE_STOP
+    # the same steps in a graph, replayed twice
+    dec3 = gpu.Decoder(B, W=W, max_new=max_new, stop=stops)
+    s_ = torch.cuda.Stream()
+    s_.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_):
+        torch.index_select(E, 0, dec3.next, out=x)
+    torch.cuda.current_stream().wait_stream(s_)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cs = torch.cuda.current_stream()
+        for t in range(steps):
+            torch.index_select(E, 0, dec3.next, out=x)
+            dec3.step(sampler, logits=logits, lm_head=m, x=x, stream=cs)
+    for rep in range(2):
+        dec3.init(sampler, seeds, init)
+        dec3.next.copy_(torch.tensor([3, 4, 5], dtype=torch.int32).cuda())
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dec3.row_state(), dec2.row_state()), rep
+        assert np.array_equal(dec3.generated.cpu().numpy(), dec2.generated.cpu().numpy()), rep
+    m.close()
