@@ -351,3 +351,36 @@ def test_decode_large_vocab_split_rows(gpu, torch, oracle):
         assert np.array_equal(dec3.row_state(), dec2.row_state()), rep
         assert np.array_equal(dec3.generated.cpu().numpy(), dec2.generated.cpu().numpy()), rep
     m.close()
+
+
+@pytest.mark.gpu
+def test_decode_optional_buffers(gpu, torch, oracle):
+    """gs_decode_step with no window (W = 0), no generated ids, no next
+    tokens, no statuses and no active count; rows on the full-vocabulary path
+    (top_k = 0) and on the split path (V > 32768, k = 40)."""
+    lib = gpu.load_library()
+    for V, params in ((40000, (1.0, 0, 0.9, 1.0)), (50000, (0.8, 40, 0.95, 1.0))):
+        B, steps = 2, 6
+        rng = np.random.default_rng(V)
+        lg = (rng.standard_normal((steps, B, V)) * 2).astype(np.float32)
+        d_lg = torch.from_numpy(lg).cuda()
+        sampler = gpu.Sampler(*params, seed=1)
+        sampler.reserve(B, V)
+        rows = torch.zeros(B * 24, dtype=torch.uint8, device="cuda")
+        u = torch.zeros(B, dtype=torch.float32, device="cuda")
+        tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+        ctx = gpu.DecodeCtx(B, rows.data_ptr(), None, 0, 0, None, None, 0, 1000, None, 0, None,
+                            u.data_ptr(), tok.data_ptr(), None, None)
+        seeds = np.array([42, 9], np.uint64)
+        assert lib.gs_decode_init(sampler._h, None, ctypes.byref(ctx), seeds.ctypes.data, None, None) == 0
+        toks = []
+        for t in range(steps):
+            assert lib.gs_decode_step(sampler._h, None, None, d_lg[t].data_ptr(), V, V, None,
+                                      ctypes.byref(ctx), None) == 0
+            torch.cuda.synchronize()
+            toks.append(tok.cpu().numpy().astype(np.int64).copy())
+        st = rows.cpu().numpy().view(gpu.decode_row_dtype())
+        for b in range(B):
+            o = oracle.generate(lg[:, b], params, 0, [], [], 1000, int(seeds[b]))
+            assert [int(x[b]) for x in toks] == o["sampled"].tolist(), (V, b)
+            assert int(st["n_gen"][b]) == steps and int(st["wpos"][b]) == 0
