@@ -352,7 +352,10 @@ int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_
     if (hook) a.hook = *hook;
     const bool full = d_params || needs_full_path(s->params, V);
     const bool small = d_params || !needs_full_path(s->params, V);
-    bool split = !d_params && B <= (size_t)gs::kSplitMaxRows && gs::split_fits(s->params, V);
+    // measured on MI355X: at V = 152064 the split path wins up to B = 16
+    // (2368 chunks) and loses at B = 32; at V = 40000 it wins up to B = 32
+    bool split = !d_params && B <= (size_t)gs::kSplitMaxRows && B * (V / gs::kSplitL) <= gs::kSplitMaxChunks &&
+                 gs::split_fits(s->params, V);
     if (split && s->split_cap < split_bytes(B, gs::split_width(s->params, V))) {
         // the buffers must grow: not under stream capture (no allocation
         // there), where the rows take the one-workgroup-per-row path instead

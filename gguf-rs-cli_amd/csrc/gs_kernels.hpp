@@ -60,6 +60,7 @@ constexpr size_t kRegMaxV = 32768;   // widest row the register kernel holds (10
 constexpr int kSplitL = 1024;          // elements per chunk; the last chunk takes the rest (< 2 kSplitL)
 constexpr int kSplitMaxKp = 128;
 constexpr int kSplitMaxRows = 32;      // more rows fill the chip one workgroup per row
+constexpr size_t kSplitMaxChunks = 2560; // B * V / kSplitL above this: one workgroup per row is faster
 constexpr size_t kSplitMaxWidth = 32768;
 bool split_fits(const gs_params &p, size_t V);
 size_t split_width(const gs_params &p, size_t V);
