@@ -363,6 +363,52 @@ def bench_token_decode(gs):
                              "sample": "oracle/tokens_oracle.py decode on the first 20000 ids"}}
 
 
+def bench_configs(gs, torch, reps=20):
+    """The sampler alone on the survey's other configurations (parity-test
+    shapes, reported for reference): C2 (Llama-3, B=64, V=128256, W=128, k=40),
+    C4 (Gemma, B=512, V=256000, W=256, per-row params) and one step of C5
+    (B=1024, V=152064, W=1024, the on-device generator's logits).  Per batch:
+    microseconds (HIP events on the launch stream) and algorithmic GB/s."""
+    import workloads
+    out = {}
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for name in ("c2", "c4", "c5"):
+        w = workloads.make(name)
+        B, V, W = w["B"], w["V"], w["W"]
+        s = gs.Sampler(w.get("T", 0.7), w.get("k", 40), w.get("p", 0.9), w.get("rep", 1.1), seed=42)
+        s.reserve(B, V)
+        tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+        if name == "c5":
+            d_lg = torch.empty((B, V), dtype=torch.float32, device="cuda")
+            gs.synth_logits(d_lg, w["synth_seed"], 0, w["sigma"], stream=st)
+            d_rec = torch.from_numpy(w["window"].view(np.int32)).cuda()
+            call = lambda: s.sample_batch(d_lg, tok, recent=d_rec, stream=st)
+            hetero = False
+        else:
+            d_lg = torch.from_numpy(w["logits"]).cuda()
+            d_rec = torch.from_numpy(w["recent"].view(np.int32)).cuda() if w["recent"] is not None else None
+            d_u = torch.from_numpy(w["u"]).cuda()
+            d_pr = torch.from_numpy(np.ascontiguousarray(w["params"]).view(np.uint8)).cuda()
+            call = lambda: s.sample_batch(d_lg, tok, params=d_pr, recent=d_rec, u=d_u, stream=st)
+            hetero = name == "c4"
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(reps):
+            call()
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = B * workloads.algorithmic_bytes_per_row(V, W, hetero=hetero)
+        out[name] = {"B": B, "V": V, "W": W, "us_per_batch": us, "rows_per_s": B / us * 1e6,
+                     "GB_per_s": nbytes / us / 1e3, "frac_of_hbm_peak": nbytes / us / 1e3 / PEAK_HBM_GBS}
+        log("%s: %.1f us per batch of %d rows (%.0f GB/s)" % (name, us, B, nbytes / us / 1e3))
+        del d_lg
+    return out
+
+
 def calib_copy(torch, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of a known size: its FETCH_SIZE and
     WRITE_SIZE per dispatch give the scale factor of those counters."""
@@ -485,6 +531,7 @@ def main():
         "lm_head_gemv": gemv,
         "decode_step": dstep,
         "token_decode": bench_token_decode(gs),
+        "other_configs": bench_configs(gs, torch),
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(c3)

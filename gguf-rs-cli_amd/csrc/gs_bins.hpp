@@ -1179,6 +1179,19 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
         for (int s = t; s < kHashSlots; s += kThreads) {
             const uint32_t id = sm.hkey[s];
             if (id == kEmpty) continue;
+            // the raw value leaves the plan's mass: its exact mass (added in
+            // pass 1) from a mass bin; from a bulk bin, one element of the
+            // count the mass is estimated from (mass64 of bulk bins counts
+            // them).  Counts stay: segment sizes are upper bounds.
+            {
+                const float xr = ldg(row + id);
+                const float dr = (t_one ? xr : xr / T) - m0;
+                if (dr <= kDUp && dr >= -kDLo) {
+                    const int b = bin_of(dr);
+                    if (b < kMassBins) atomicAdd((unsigned long long *)&mass64[b], 0ull - (unsigned long long)(fast_exp(dr) * kMassScale));
+                    else atomicAdd((unsigned long long *)&mass64[b], 1ull);
+                }
+            }
             const float yp = t_one ? __uint_as_float(sm.hval[s]) : __uint_as_float(sm.hval[s]) / T;
             const float dq = yp - m0;
             if (dq > kDUp) {
@@ -1223,7 +1236,8 @@ __device__ bool full_bins_row(RowSmem &sm, const float *row, int V, float T, flo
         for (int c = 0; c < kPer; c++) {
             const int b = kPer * t + c;
             cntv[c] = bn.cnt[b];
-            eb[c] = b < kMassBins ? (double)mass64[b] * mscale : (double)cntv[c] * e_at((float)b + 0.5f);
+            eb[c] = b < kMassBins ? (double)mass64[b] * mscale
+                                  : (double)(cntv[c] - (uint32_t)mass64[b]) * e_at((float)b + 0.5f);
             loc += eb[c];
             ctot += cntv[c];
         }
