@@ -6,7 +6,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
+
 #include <new>
+#include <vector>
 
 #include "../../include/gs_sampler.h"
 #include "gs_kernels.hpp"
@@ -33,6 +35,7 @@ struct gs_sampler {
     size_t scratch_elems;
     int32_t *fb;                 // per-row fallback flags of the full-vocabulary path
     size_t fb_cap;
+    size_t fb_rows;              // rows of the last call that launched that path (0: none)
     void *split;                 // split top-k path: virtual rows (f32), then their ids (u32)
     size_t split_cap;
 };
@@ -182,6 +185,20 @@ int gs_sampler_set_seed(gs_sampler *s, uint64_t seed)
     return GS_OK;
 }
 
+int gs_sampler_fallback_rows(gs_sampler *s, void *stream, size_t *n)
+{
+    if (!s || !n) return GS_ERR_INVALID;
+    *n = 0;
+    if (!s->fb_rows) return GS_OK;
+    std::vector<int32_t> h(s->fb_rows);
+    hipStream_t st = (hipStream_t)stream;
+    if (hipMemcpyAsync(h.data(), s->fb, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return GS_ERR_HIP;
+    for (int32_t f : h) *n += f != 0;
+    return GS_OK;
+}
+
 int gs_sampler_get_state(const gs_sampler *s, uint64_t *state)
 {
     if (!s || !state) return GS_ERR_INVALID;
@@ -211,6 +228,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
               uint32_t *out_token)
 {
     if (!s || !out_token || (V > 0 && !logits) || (W > 0 && !recent)) return GS_ERR_INVALID;
+    s->fb_rows = 0;
     if (V > GS_MAX_VOCAB) return GS_ERR_UNSUPPORTED;
     if (W > (size_t)gs::kMaxWindow) return GS_ERR_UNSUPPORTED;
     int rc;
@@ -263,6 +281,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     uint32_t tok;
     if (full) {
         // the full-vocabulary path (several kernels) synchronises the stream
+        s->fb_rows = 1;
         if (gs::launch_sample_rows(a, 1, false, true, s->stream) != hipSuccess) return GS_ERR_HIP;
         if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
         st = *(volatile int32_t *)s->h_status;
@@ -324,6 +343,7 @@ int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_
                  const float *d_u, uint32_t *d_tokens, int32_t *d_status, const DecodeHook *hook, void *stream)
 {
     if (!s || !d_tokens || (B > 0 && V > 0 && !d_logits) || ld < V) return GS_ERR_INVALID;
+    s->fb_rows = 0;
     if (d_recent && ld_recent < W) return GS_ERR_INVALID;
     if (!d_u && d_params) return GS_ERR_INVALID;   // LCG draws need host-known T per row
     if (V > GS_MAX_VOCAB || B > 0x7fffffff) return GS_ERR_UNSUPPORTED;
@@ -368,8 +388,9 @@ int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_
         const size_t wd = gs::split_width(s->params, V);
         if ((rc = reserve_split(s, B, wd))) return rc;
         if (launch_split_rows(s, a, B, wd, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
-    } else if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) {
-        return GS_ERR_HIP;
+    } else {
+        if (full) s->fb_rows = B;
+        if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
     }
     if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
     return GS_OK;

@@ -961,6 +961,7 @@ __device__ bool finish_now(RowSmem &sm, uint64_t *gl, uint64_t *tmp)
             atomicMin(&bn.gbeg[r], bn.off[b]);
             atomicMax(&bn.gend[r], bn.off[b + 1]);
         }
+        if (starts[c]) bn.runt[r] = (uint32_t)b;      // the run's first bin
     }
     __threadfence_block();
     __syncthreads();
@@ -1004,8 +1005,9 @@ __device__ bool finish_now(RowSmem &sm, uint64_t *gl, uint64_t *tmp)
     __syncthreads();
     // run r: nonzero prefix at its first bin (runt[r])
     if (t < (int)nruns) {
-        const uint64_t en0 = ldg(gl + bn.gbeg[t]);       // the first entry of a run is its largest
-        bn.runt[t] = en0 ? bn.nzc[bin_of_entry(en0)] : 0u;
+        // (not from the run's first entry: that slot may hold a zero, such as
+        // a penalized id's raw value taken out of the list)
+        bn.runt[t] = bn.nzc[bn.runt[t]];
     }
     __syncthreads();
     for (uint32_t it = wave_id(); it < tot; it += kWaves) {

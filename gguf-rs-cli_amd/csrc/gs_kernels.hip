@@ -1221,7 +1221,10 @@ sample_rows_kernel(RowArgs a)
     const gs_params p = a.params ? a.params[b] : a.uparams;
     const bool full = is_full_path(p, V);
     if (MODE == kModeSmall && full) return;
-    if (MODE != kModeSmall && !full) return;
+    if (MODE != kModeSmall && !full) {
+        if (MODE == kModeBins && t == 0 && a.fb != nullptr) a.fb[b] = 0;
+        return;
+    }
     if (MODE == kModeSort && a.fb != nullptr && a.fb[b] == 0) return;
     GS_STAMP(8 * MODE);
 #ifdef GS_TIMING

@@ -46,7 +46,7 @@ EXPORTS = [
     # include/gs_gemv.h
     "gs_qmatrix_upload", "gs_qmatrix_destroy", "gs_qmatrix_shape", "gs_gemv",
     # include/gs_decode.h
-    "gs_sampler_get_params", "gs_decode_init", "gs_decode_commit", "gs_decode_step",
+    "gs_sampler_get_params", "gs_sampler_fallback_rows", "gs_decode_init", "gs_decode_commit", "gs_decode_step",
     # include/gs_tokens.h
     "gs_vocab_create", "gs_vocab_destroy", "gs_vocab_find", "gs_token_decode", "gs_tokens_decode",
     "gs_chat_template_detect", "gs_stop_tokens",
@@ -105,6 +105,7 @@ def load_library(path=LIB_PATH):
         "gs_qmatrix_shape": ([P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(SZ), ctypes.POINTER(SZ)], I),
         "gs_gemv": ([P, P, SZ, P, P], I),
         "gs_sampler_get_params": ([P, ctypes.POINTER(GsParams)], I),
+        "gs_sampler_fallback_rows": ([P, P, ctypes.POINTER(ctypes.c_size_t)], I),
         "gs_decode_init": ([P, P, ctypes.POINTER(DecodeCtx), P, P, P], I),
         "gs_decode_commit": ([P, P, ctypes.POINTER(DecodeCtx), P], I),
         "gs_decode_step": ([P, P, P, P, SZ, SZ, P, ctypes.POINTER(DecodeCtx), P], I),
@@ -209,6 +210,13 @@ class Sampler:
     def set_params(self, temperature, top_k, top_p, rep_penalty):
         self.params = GsParams(temperature, top_k, top_p, rep_penalty)
         _check(self._lib.gs_sampler_set_params(self._h, ctypes.byref(self.params)), "set_params")
+
+    def fallback_rows(self, stream=None):
+        """Rows of the last full-vocabulary call finished by the sort-based
+        path instead of the binned one (waits for the stream)."""
+        n = ctypes.c_size_t()
+        _check(self._lib.gs_sampler_fallback_rows(self._h, _stream_handle(stream), ctypes.byref(n)), "fallback_rows")
+        return n.value
 
     def set_seed(self, seed):
         _check(self._lib.gs_sampler_set_seed(self._h, seed), "set_seed")

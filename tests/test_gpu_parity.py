@@ -100,6 +100,25 @@ def test_c4_gemma_hetero(gpu, torch, oracle):
         assert tok[b] == want[b]
 
 
+def test_c4_rows_with_zero_at_run_head(gpu, torch, oracle):
+    """Rows 312-319 of the full C4 batch.  In row 315 a bin collected late
+    starts a run of collected bins whose first list slot holds a zero (a
+    penalized id's raw value, taken out); the run's compaction must not take
+    its base from that slot, or an entry is listed twice and the sums drift."""
+    import workloads
+    w = workloads.make("c4")
+    sl = slice(312, 320)
+    lg = np.ascontiguousarray(w["logits"][sl])
+    pr, u, rec = w["params"][sl], w["u"][sl], np.ascontiguousarray(w["recent"][sl])
+    del w
+    _say("c4 rows 312-319 V", lg.shape[1])
+    tok, st, s = run_batch(gpu, torch, lg, params=pr, u=u, recent=rec)
+    assert (pr["top_k"] == 0).any()        # rows on the full-vocabulary path
+    assert s.fallback_rows() == 0          # every full-vocabulary row stayed on the binned path
+    want = oracle.sample_batch(lg, pr, u, recent=rec, nthreads=8)
+    check_tokens("c4 rows 312-319", tok, want, st)
+
+
 def test_c1_decode_trace(gpu, torch, oracle):
     """Sequential single-row calls on the sampler's own LCG stream (seed 42)."""
     import workloads
