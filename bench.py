@@ -59,6 +59,7 @@ def bench_c3(gs, torch, steps, warmup):
         s.sample_batch(d_lg, d_tok, u=d_u, status=d_st, stream=stream)
     torch.cuda.synchronize()
     assert int((d_st != 0).sum()) == 0, "sampler reported row errors"
+    sort_rows = s.fallback_rows(stream)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -70,7 +71,7 @@ def bench_c3(gs, torch, steps, warmup):
     ms = e0.elapsed_time(e1) / steps
     per_row = workloads.algorithmic_bytes_per_row(V, 0)
     tokens = d_tok.cpu().numpy().astype(np.int64)
-    return dict(B=B, V=V, ms=ms, bytes=per_row * B, tokens=tokens, w=w)
+    return dict(B=B, V=V, ms=ms, bytes=per_row * B, tokens=tokens, w=w, sort_rows=sort_rows)
 
 
 def bench_c1_latency(gs, torch, steps=256):
@@ -395,6 +396,7 @@ def bench_configs(gs, torch, reps=20):
         for _ in range(3):
             call()
         torch.cuda.synchronize()
+        sort_rows = s.fallback_rows(st)
         e0.record(st)
         for _ in range(reps):
             call()
@@ -403,7 +405,8 @@ def bench_configs(gs, torch, reps=20):
         us = e0.elapsed_time(e1) * 1e3 / reps
         nbytes = B * workloads.algorithmic_bytes_per_row(V, W, hetero=hetero)
         out[name] = {"B": B, "V": V, "W": W, "us_per_batch": us, "rows_per_s": B / us * 1e6,
-                     "GB_per_s": nbytes / us / 1e3, "frac_of_hbm_peak": nbytes / us / 1e3 / PEAK_HBM_GBS}
+                     "GB_per_s": nbytes / us / 1e3, "frac_of_hbm_peak": nbytes / us / 1e3 / PEAK_HBM_GBS,
+                     "sort_path_rows": sort_rows}
         log("%s: %.1f us per batch of %d rows (%.0f GB/s)" % (name, us, B, nbytes / us / 1e3))
         del d_lg
     return out
@@ -520,7 +523,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded numpy N(0,2^2) logits resident in HBM)",
         "config": {"workload": "c3 Qwen2.5 V=152064 B=256 top_k=0 top_p=0.95 T=1.0 rep=1.0",
-                   "global_batch": c3["B"], "vocab": c3["V"], "parallelism": "none (1 GPU)"},
+                   "global_batch": c3["B"], "vocab": c3["V"], "parallelism": "none (1 GPU)",
+                   "sort_path_rows": c3["sort_rows"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": profiled_traffic(),
                      "kernel": "gs::sample_rows_kernel", "bytes_per_launch": c3["bytes"]},

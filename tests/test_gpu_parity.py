@@ -100,6 +100,22 @@ def test_c4_gemma_hetero(gpu, torch, oracle):
         assert tok[b] == want[b]
 
 
+
+@pytest.mark.parametrize("name", ["c2", "c4"])
+def test_full_batch(gpu, torch, oracle, name):
+    """Every row of the configuration at its full size (C2 B=64 V=128256, C4
+    B=512 V=256000): identical tokens, and no full-vocabulary row handed to
+    the sort-based path.  (C3 at full size: test_c3_full_batch_256.)"""
+    import workloads
+    w = workloads.make(name)
+    rec = w.get("recent")
+    _say(name, "full batch B", w["B"], "V", w["V"])
+    tok, st, s = run_batch(gpu, torch, w["logits"], params=w["params"], u=w["u"], recent=rec)
+    assert s.fallback_rows() == 0
+    want = oracle.sample_batch(w["logits"], w["params"], w["u"], recent=rec, nthreads=8,
+                               fast_topk=name == "c2")
+    check_tokens(name + " full", tok, want, st)
+
 def test_c4_rows_with_zero_at_run_head(gpu, torch, oracle):
     """Rows 312-319 of the full C4 batch.  In row 315 a bin collected late
     starts a run of collected bins whose first list slot holds a zero (a
@@ -447,11 +463,12 @@ def test_reference_free_function_api(gpu, oracle):
 
 # --- full-vocabulary path (binned exact sums) -------------------------------
 def test_c3_full_batch_256(gpu, torch, oracle):
-    """All 256 rows of the benchmark batch, bit-exact."""
+    """All 256 rows of the benchmark batch, bit-exact, none on the sort path."""
     import workloads
     w = workloads.make("c3")
     _say("c3 B=256 V", w["V"])
-    tok, st, _ = run_batch(gpu, torch, w["logits"], params=w["params"], u=w["u"])
+    tok, st, s = run_batch(gpu, torch, w["logits"], params=w["params"], u=w["u"])
+    assert s.fallback_rows() == 0
     want = oracle.sample_batch(w["logits"], w["params"], w["u"], nthreads=16)
     check_tokens("c3 B=256", tok, want, st)
 
