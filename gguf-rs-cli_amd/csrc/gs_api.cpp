@@ -5,8 +5,10 @@
 // single-row call and the scratch of the full-vocabulary path.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -38,6 +40,10 @@ struct gs_sampler {
     size_t fb_rows;              // rows of the last call that launched that path (0: none)
     void *split;                 // split top-k path: virtual rows (f32), then their ids (u32)
     size_t split_cap;
+    const int32_t *fb_last;      // fallback flags of the last call (own buffer or the static scratch)
+    bool captured;               // a call was recorded into a graph: buffers are never freed before destroy
+    void **retired;              // buffers replaced after a capture, freed by gs_sampler_destroy
+    size_t n_retired, cap_retired;
 };
 
 namespace {
@@ -64,9 +70,24 @@ bool is_device_ptr(gs_sampler *s, const void *p)
     return dev;
 }
 
-int grow(void **buf, size_t *cap, size_t need_bytes)
+// Grow a sampler-owned device buffer.  Once a call of this sampler has been
+// captured into a HIP graph the old buffer may still be referenced by that
+// graph, so it is kept (freed by gs_sampler_destroy) instead of freed.
+int grow(gs_sampler *s, void **buf, size_t *cap, size_t need_bytes)
 {
     if (*cap >= need_bytes) return GS_OK;
+    if (*buf && s->captured) {
+        if (s->n_retired == s->cap_retired) {
+            const size_t nc = s->cap_retired ? 2 * s->cap_retired : 8;
+            void **r = (void **)realloc(s->retired, nc * sizeof(void *));
+            if (!r) return GS_ERR_NOMEM;
+            s->retired = r;
+            s->cap_retired = nc;
+        }
+        s->retired[s->n_retired++] = *buf;
+        *buf = nullptr;
+        *cap = 0;
+    }
     if (*buf) { (void)hipFree(*buf); *buf = nullptr; *cap = 0; }
     if (hipMalloc(buf, need_bytes) != hipSuccess) { (void)hipGetLastError(); *buf = nullptr; return GS_ERR_NOMEM; }
     *cap = need_bytes;
@@ -86,25 +107,25 @@ size_t split_bytes(size_t rows, size_t width) { return rows * width * 8; }
 
 int reserve_split(gs_sampler *s, size_t rows, size_t width)
 {
-    return grow(&s->split, &s->split_cap, split_bytes(rows, width));
+    return grow(s, &s->split, &s->split_cap, split_bytes(rows, width));
 }
 
-hipError_t launch_split_rows(gs_sampler *s, const gs::RowArgs &a, size_t B, size_t width, hipStream_t st)
+hipError_t launch_split_rows(void *buf, const gs::RowArgs &a, size_t B, size_t width, hipStream_t st)
 {
-    float *vrow = (float *)s->split;
+    float *vrow = (float *)buf;
     return gs::launch_split(a, (int)B, vrow, (uint32_t *)(vrow + B * width), st);
 }
 
 int reserve_scratch(gs_sampler *s, size_t rows, size_t V)
 {
     void *f = s->fb;
-    int rcf = grow(&f, &s->fb_cap, (rows ? rows : 1) * sizeof(int32_t));
+    int rcf = grow(s, &f, &s->fb_cap, (rows ? rows : 1) * sizeof(int32_t));
     s->fb = (int32_t *)f;
     if (rcf) return rcf;
     size_t elems = rows * gs::scratch_u32_per_row(V);
     size_t cap = s->scratch_elems * sizeof(uint32_t);
     void *p = s->scratch;
-    int rc = grow(&p, &cap, elems * sizeof(uint32_t));
+    int rc = grow(s, &p, &cap, elems * sizeof(uint32_t));
     s->scratch = (uint32_t *)p;
     s->scratch_elems = cap / sizeof(uint32_t);
     return rc;
@@ -157,6 +178,8 @@ int gs_sampler_destroy(gs_sampler *s)
     if (s->scratch) (void)hipFree(s->scratch);
     if (s->fb) (void)hipFree(s->fb);
     if (s->split) (void)hipFree(s->split);
+    for (size_t i = 0; i < s->n_retired; i++) (void)hipFree(s->retired[i]);
+    free(s->retired);
     if (s->h_tok) (void)hipHostFree(s->h_tok);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     (void)hipSetDevice(dev);
@@ -192,7 +215,7 @@ int gs_sampler_fallback_rows(gs_sampler *s, void *stream, size_t *n)
     if (!s->fb_rows) return GS_OK;
     std::vector<int32_t> h(s->fb_rows);
     hipStream_t st = (hipStream_t)stream;
-    if (hipMemcpyAsync(h.data(), s->fb, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st) != hipSuccess ||
+    if (hipMemcpyAsync(h.data(), s->fb_last, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess)
         return GS_ERR_HIP;
     for (int32_t f : h) *n += f != 0;
@@ -235,7 +258,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     const float *d_logits = logits;
     if (V > 0 && !is_device_ptr(s, logits)) {
         void *p = s->d_row;
-        rc = grow(&p, &s->row_cap, V * sizeof(float));
+        rc = grow(s, &p, &s->row_cap, V * sizeof(float));
         s->d_row = (float *)p;
         if (rc) return rc;
         if (hipMemcpyAsync(s->d_row, logits, V * sizeof(float), hipMemcpyHostToDevice, s->stream) != hipSuccess)
@@ -282,6 +305,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     if (full) {
         // the full-vocabulary path (several kernels) synchronises the stream
         s->fb_rows = 1;
+        s->fb_last = s->fb;
         if (gs::launch_sample_rows(a, 1, false, true, s->stream) != hipSuccess) return GS_ERR_HIP;
         if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
         st = *(volatile int32_t *)s->h_status;
@@ -298,7 +322,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
         for (;;) {
             a.done_val = ++s->seq;
             const hipError_t le = reg     ? gs::launch_reg_row(a, s->stream)
-                                  : split ? launch_split_rows(s, a, 1, gs::split_width(s->params, V), s->stream)
+                                  : split ? launch_split_rows(s->split, a, 1, gs::split_width(s->params, V), s->stream)
                                           : gs::launch_sample_rows(a, 1, true, false, s->stream);
             if (le != hipSuccess) return GS_ERR_HIP;
             volatile uint64_t *f = s->h_done;
@@ -338,9 +362,33 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, si
 
 namespace gs {
 
-int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld, const gs_params *d_params,
-                 const uint32_t *d_recent, size_t ld_recent, const uint32_t *d_recent_len, size_t W,
-                 const float *d_u, uint32_t *d_tokens, int32_t *d_status, const DecodeHook *hook, void *stream)
+namespace {
+
+// Is `stream` being captured into a HIP graph?
+int capturing(hipStream_t stream, bool *cap)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) { (void)hipGetLastError(); return GS_ERR_HIP; }
+    *cap = cs != hipStreamCaptureStatusNone;
+    return GS_OK;
+}
+
+// Device buffers of one batched call.  `fixed` buffers come from the caller
+// (the static scratch of gs_sample_batch_noalloc) and never grow.
+struct CallBufs {
+    bool fixed;
+    uint32_t *scratch;           // full-vocabulary path, B * scratch_u32_per_row(V) words
+    int32_t *fb;                 // B fallback flags
+    void *split;                 // split top-k path
+    size_t split_cap;            // bytes
+};
+
+} // namespace
+
+int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld, const gs_params *d_params,
+                      const uint32_t *d_recent, size_t ld_recent, const uint32_t *d_recent_len, size_t W,
+                      const float *d_u, uint32_t *d_tokens, int32_t *d_status, const DecodeHook *hook,
+                      void *stream, const CallBufs *fixed)
 {
     if (!s || !d_tokens || (B > 0 && V > 0 && !d_logits) || ld < V) return GS_ERR_INVALID;
     s->fb_rows = 0;
@@ -350,7 +398,25 @@ int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_
     if (d_recent && W > (size_t)gs::kMaxWindow) return GS_ERR_UNSUPPORTED;
     if (B == 0) return GS_OK;
     int rc;
-    if ((d_params || needs_full_path(s->params, V)) && (rc = reserve_scratch(s, B, V))) return rc;
+    bool cap = false;
+    if ((rc = capturing((hipStream_t)stream, &cap))) return rc;
+    // The sampler's own LCG is host state: a graph would replay the draws it
+    // held at capture time, so under capture the draws must come from d_u.
+    if (cap && !d_u && s->params.temperature > 0.0f) return GS_ERR_UNSUPPORTED;
+    if (cap) s->captured = true;
+    const bool full = d_params || needs_full_path(s->params, V);
+    const bool small = d_params || !needs_full_path(s->params, V);
+    CallBufs bf;
+    if (fixed) {
+        bf = *fixed;
+    } else {
+        if (full && (s->fb_cap < B * sizeof(int32_t) ||
+                     s->scratch_elems < B * gs::scratch_u32_per_row(V))) {
+            if (cap) return GS_ERR_UNSUPPORTED;      // no allocation under capture: reserve first
+            if ((rc = reserve_scratch(s, B, V))) return rc;
+        }
+        bf = CallBufs{false, s->scratch, s->fb, s->split, s->split_cap};
+    }
     gs::RowArgs a;
     memset(&a, 0, sizeof(a));
     a.logits = d_logits;
@@ -366,34 +432,40 @@ int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_
     a.lcg_state = s->state;
     a.tokens = d_tokens;
     a.status = d_status;
-    a.scratch = s->scratch;
+    a.scratch = bf.scratch;
     a.scratch_stride = gs::scratch_u32_per_row(V);
-    a.fb = s->fb;
+    a.fb = bf.fb;
     if (hook) a.hook = *hook;
-    const bool full = d_params || needs_full_path(s->params, V);
-    const bool small = d_params || !needs_full_path(s->params, V);
     // measured on MI355X: at V = 152064 the split path wins up to B = 16
     // (2368 chunks) and loses at B = 32; at V = 40000 it wins up to B = 32
     bool split = !d_params && B <= (size_t)gs::kSplitMaxRows && B * (V / gs::kSplitL) <= gs::kSplitMaxChunks &&
                  gs::split_fits(s->params, V);
-    if (split && s->split_cap < split_bytes(B, gs::split_width(s->params, V))) {
-        // the buffers must grow: not under stream capture (no allocation
-        // there), where the rows take the one-workgroup-per-row path instead
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) { (void)hipGetLastError(); return GS_ERR_HIP; }
-        if (cs != hipStreamCaptureStatusNone) split = false;
+    const size_t wd = split ? gs::split_width(s->params, V) : 0;
+    if (split && bf.split_cap < split_bytes(B, wd)) {
+        // the buffers must grow: not with fixed buffers or under stream
+        // capture (no allocation there); the rows then take the
+        // one-workgroup-per-row path instead
+        if (bf.fixed || cap) split = false;
+        else if ((rc = reserve_split(s, B, wd))) return rc;
+        else bf.split = s->split;
     }
     if (split) {
         // a few rows of a large vocabulary: spread each row over the chip
-        const size_t wd = gs::split_width(s->params, V);
-        if ((rc = reserve_split(s, B, wd))) return rc;
-        if (launch_split_rows(s, a, B, wd, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+        if (launch_split_rows(bf.split, a, B, wd, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
     } else {
-        if (full) s->fb_rows = B;
+        if (full) { s->fb_rows = B; s->fb_last = bf.fb; }
         if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
     }
     if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
     return GS_OK;
+}
+
+int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld, const gs_params *d_params,
+                 const uint32_t *d_recent, size_t ld_recent, const uint32_t *d_recent_len, size_t W,
+                 const float *d_u, uint32_t *d_tokens, int32_t *d_status, const DecodeHook *hook, void *stream)
+{
+    return sample_batch_bufs(s, d_logits, B, V, ld, d_params, d_recent, ld_recent, d_recent_len, W, d_u, d_tokens,
+                             d_status, hook, stream, nullptr);
 }
 
 } // namespace gs

@@ -239,6 +239,12 @@ class Sampler:
         torch f32 tensor (host or device).  Synchronous."""
         fast = _torch_fast_args(logits, recent)
         if fast is not None:
+            if logits.is_cuda or (recent is not None and getattr(recent, "is_cuda", False)):
+                # gs_sample runs on the sampler's own non-blocking stream:
+                # wait for torch's current stream, which may still be writing
+                # the logits (or the window)
+                import torch
+                torch.cuda.current_stream(logits.device if logits.is_cuda else None).synchronize()
             rc = self._lib.gs_sample(self._h, fast[0], fast[1], fast[2], fast[3], self._outref)
             if rc != GS_OK:
                 raise SamplerError(rc, "gs_sample")

@@ -106,7 +106,16 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V,
  * stream     : hipStream_t (NULL = default stream).
  * Scratch for rows that need the full-vocabulary path is owned by the
  * sampler and grows on demand (allocation happens outside kernels, before
- * the launch). */
+ * the launch).
+ * One sampler serves one stream at a time: its scratch is shared by all its
+ * calls, so calls of one sampler on two streams may race.
+ * HIP graph capture: call gs_sampler_reserve(s, B, V) before capturing (a
+ * call that would have to allocate under capture returns
+ * GS_ERR_UNSUPPORTED), and pass d_u (a captured call with d_u == NULL and
+ * T > 0 returns GS_ERR_UNSUPPORTED: the host LCG state would be frozen into
+ * the graph and every replay would repeat the same draws).  Once a call has
+ * been captured, buffers the sampler replaces later are kept until
+ * gs_sampler_destroy, so earlier graphs never touch freed memory. */
 int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V,
                     size_t ld, const gs_params *d_params,
                     const uint32_t *d_recent, size_t ld_recent,

@@ -385,6 +385,36 @@ void oracle_synth_logits(float *out, size_t n, uint64_t seed, uint64_t counter0,
  * counter (t*B + b)*V + col.  Each row keeps a ring window of W ids
  * (initial contents given); the sampled token overwrites slot t % W.
  * Draw for (t, b) is u[t*B + b]. */
+/* Rows [row0, row1) of one step's synthetic logits, for the threads of
+ * oracle_device_loop. */
+struct synth_job { float *out; size_t n; uint64_t seed, c0; float sigma; };
+static void *synth_worker(void *arg)
+{
+    struct synth_job *j = (struct synth_job *)arg;
+    oracle_synth_logits(j->out, j->n, j->seed, j->c0, j->sigma);
+    return NULL;
+}
+
+static void synth_rows(float *lg, size_t B, size_t V, uint64_t seed, uint64_t c0, float sigma, int nthreads)
+{
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    if ((size_t)nthreads > B) nthreads = (int)(B ? B : 1);
+    pthread_t th[256];
+    struct synth_job jobs[256];
+    for (int t = 0; t < nthreads; t++) {
+        const size_t r0 = B * (size_t)t / (size_t)nthreads, r1 = B * (size_t)(t + 1) / (size_t)nthreads;
+        jobs[t].out = lg + r0 * V;
+        jobs[t].n = (r1 - r0) * V;
+        jobs[t].seed = seed;
+        jobs[t].c0 = c0 + r0 * V;
+        jobs[t].sigma = sigma;
+    }
+    if (nthreads == 1) { synth_worker(&jobs[0]); return; }
+    for (int t = 0; t < nthreads; t++) pthread_create(&th[t], NULL, synth_worker, &jobs[t]);
+    for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
+}
+
 int oracle_device_loop(size_t B, size_t V, size_t steps, uint64_t seed, float sigma,
                        const oracle_params *p, uint32_t *window, size_t W,
                        const float *u, int64_t *tokens, int nthreads, int fast_topk)
@@ -395,7 +425,7 @@ int oracle_device_loop(size_t B, size_t V, size_t steps, uint64_t seed, float si
     for (size_t b = 0; b < B; b++) pp[b] = *p;
     int st = 0;
     for (size_t t = 0; t < steps && !st; t++) {
-        oracle_synth_logits(lg, B * V, seed, (uint64_t)t * B * V, sigma);
+        synth_rows(lg, B, V, seed, (uint64_t)t * B * V, sigma, nthreads);
         st = oracle_sample_batch(lg, B, V, V, pp, window, W, NULL, W, u + t * B,
                                  tokens + t * B, nthreads, fast_topk);
         for (size_t b = 0; b < B && !st; b++) {

@@ -136,9 +136,11 @@ def test_c4_rows_with_zero_at_run_head(gpu, torch, oracle):
 
 
 def test_c1_decode_trace(gpu, torch, oracle):
-    """Sequential single-row calls on the sampler's own LCG stream (seed 42)."""
+    """Config C1 as specified: 256 sequential single-row calls on the
+    sampler's own LCG stream (seed 42), against the reference loop."""
     import workloads
-    w = workloads.make("c1", steps=64)
+    w = workloads.make("c1")
+    assert w["steps"] == 256
     _say("c1 steps", w["steps"])
     s = gpu.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
     recent = list(w["init_recent"])
@@ -518,39 +520,60 @@ def test_full_vocab_sweep(gpu, torch, oracle, V, shape):
     check_tokens("sweep V=%d %s" % (V, shape), tok, want, st)
 
 
+def lcg_draw_table(seeds, steps):
+    """u[t, b] = the t-th draw of an LCG seeded seeds[b] (src/sampler.rs:7-12),
+    vectorised over rows with wrapping u64 arithmetic."""
+    a, c = np.uint64(6364136223846793005), np.uint64(1442695040888963407)
+    st = np.asarray(seeds, dtype=np.uint64).copy()
+    u = np.empty((steps, st.size), np.float32)
+    with np.errstate(over="ignore"):
+        for t in range(steps):
+            u[t] = (st >> np.uint64(33)).astype(np.float32) / np.float32(4294967295.0)
+            st = st * a + c
+    return u, st
+
+
 def test_c5_hip_graph(gpu, torch, oracle):
-    """Config C5 as a captured HIP graph: every step (on-device logits, batched
-    sample, window push) recorded once, then replayed; each replay's token
-    trace and final window must equal the oracle's.  The LCG states of the
-    steps are fixed at capture, as the eager loop would draw them."""
+    """Config C5 as specified: B = 1024 rows, V = 152064, 128 steps captured
+    in one HIP graph (on-device logits, then the decode step: sample with
+    the 1024-id ring window and commit), replayed once.  The rows' LCGs live
+    on the device (gs_decode_*), so the draws come from the device state, not
+    from values frozen at capture.  The whole token trace and the final
+    windows must equal the oracle's loop over the same logits and draws."""
     import workloads
-    w = workloads.make("c5", B=4, steps=6)
+    w = workloads.make("c5")
     B, V, W, steps = w["B"], w["V"], w["W"], w["steps"]
-    _say("c5 graph B", B, "steps", steps)
+    assert (B, V, W, steps) == (1024, 152064, 1024, 128)
+    _say("c5 graph B", B, "V", V, "steps", steps)
+    seeds = [w["seed"] + b for b in range(B)]
+    s = gpu.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=1)
+    s.reserve(B, V)
+    dec = gpu.Decoder(B, W=W, max_new=steps + 1, stop=())
+    dec.init(s, seeds, init_recent=w["window"])
     d_lg = torch.empty((B, V), dtype=torch.float32, device="cuda")
-    win0 = torch.from_numpy(w["window"].view(np.int32)).cuda()
-    d_win = win0.clone()
-    d_toks = torch.zeros((steps, B), dtype=torch.int32, device="cuda")
-    s = gpu.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=w["seed"])
-    st = torch.cuda.Stream()
-    g = torch.cuda.CUDAGraph()
     torch.cuda.synchronize()
-    with torch.cuda.graph(g, stream=st):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream()
         for t in range(steps):
             gpu.synth_logits(d_lg, w["synth_seed"], t * B * V, w["sigma"], stream=st)
-            s.sample_batch(d_lg, d_toks[t], recent=d_win, stream=st)
-            gpu.window_push(d_win, d_toks[t], t, stream=st)
-    u, _ = workloads.lcg_stream(w["seed"], steps * B)
-    want, win = oracle.device_loop(B, V, steps, w["synth_seed"], w["sigma"],
-                                   (w["T"], w["k"], w["p"], w["rep"]), w["window"], u, nthreads=4)
-    for rep in range(3):
-        d_win.copy_(win0)          # eager work between replays
-        d_toks.zero_()
-        torch.cuda.synchronize()
-        g.replay()
-        torch.cuda.synchronize()
-        check_tokens("c5 graph replay %d" % rep, d_toks.cpu().numpy().astype(np.int64), want)
-        assert (d_win.cpu().numpy().view(np.uint32) == win).all()
+            dec.step(s, logits=d_lg, stream=st)
+    torch.cuda.synchronize()
+    assert int(dec.row_state()["n_gen"].sum()) == 0     # capture ran nothing
+    g.replay()
+    torch.cuda.synchronize()
+    rows = dec.row_state()
+    gen = dec.generated.cpu().numpy().view(np.uint32)[:, :steps].astype(np.int64)
+    win = dec.window.cpu().numpy().view(np.uint32)
+    u, final = lcg_draw_table(seeds, steps + 1)          # + the draw made after the last step
+    _say("c5 oracle")
+    want, want_win = oracle.device_loop(B, V, steps, w["synth_seed"], w["sigma"],
+                                        (w["T"], w["k"], w["p"], w["rep"]), w["window"],
+                                        np.ascontiguousarray(u[:steps]).reshape(-1), nthreads=16)
+    check_tokens("c5 graph", gen.T, want)
+    assert (rows["n_gen"] == steps).all() and (rows["done"] == gpu.DONE_RUNNING).all()
+    assert np.array_equal(rows["rng"], final)            # one draw ahead, as documented
+    assert np.array_equal(win, want_win)
 
 
 # --- split top-k rows (a few rows of a large vocabulary over many workgroups) ---
