@@ -46,6 +46,8 @@ struct gs_sampler {
     size_t n_retired, cap_retired;
 };
 
+namespace gs { int init_static_scratch(int device); }
+
 namespace {
 
 // Device pointer test with a one-allocation cache: consecutive rows of one
@@ -146,6 +148,8 @@ int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out)
     s->state = seed;
     if (hipGetDevice(&s->device) != hipSuccess) { delete s; return GS_ERR_HIP; }
     if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) { delete s; return GS_ERR_HIP; }
+    // set-up of gs_sample_batch_noalloc's scratch on this device (once per device)
+    if (gs::init_static_scratch(s->device) != GS_OK) { (void)hipStreamDestroy(s->stream); delete s; return GS_ERR_HIP; }
     if (hipHostMalloc((void **)&s->h_tok, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
         hipHostGetDevicePointer((void **)&s->d_tok_map, s->h_tok, 0) != hipSuccess) {
         gs_sampler_destroy(s);
@@ -468,9 +472,73 @@ int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_
                              d_status, hook, stream, nullptr);
 }
 
+// ---- the scratch of gs_sample_batch_noalloc --------------------------------
+// One array per GPU, in the code object: the library holds it until the
+// process ends.  Host code never uses the symbol's name as an address (that
+// is a host-side stand-in); it uses the device address resolved per device
+// by hipGetSymbolAddress.
+constexpr size_t kStaticScratchBytes = (size_t)GS_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint32_t scratch[kStaticScratchBytes / sizeof(uint32_t)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on `device` (made current by the caller).
+int static_scratch(int device, void **out)
+{
+    if (device < 0 || device >= kMaxDevices) return GS_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            return GS_ERR_HIP;
+        }
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return GS_OK;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+} // namespace
+
+// Resolve the static scratch of the current device (sampler set-up).
+int init_static_scratch(int device)
+{
+    void *p;
+    return static_scratch(device, &p);
+}
+
 } // namespace gs
 
 extern "C" {
+
+int gs_sample_batch_noalloc(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld,
+                            const gs_params *d_params, const uint32_t *d_recent, size_t ld_recent,
+                            const uint32_t *d_recent_len, size_t W, const float *d_u,
+                            uint32_t *d_tokens, int32_t *d_status, void *stream)
+{
+    if (!s) return GS_ERR_INVALID;
+    if (V > GS_MAX_VOCAB || B > 0x7fffffff) return GS_ERR_UNSUPPORTED;
+    void *base = nullptr;
+    int rc = gs::static_scratch(s->device, &base);
+    if (rc) return rc;
+    // layout: B fallback flags | split top-k buffers (any k, up to
+    // kSplitMaxRows rows) | full-vocabulary scratch
+    const size_t fb_bytes = gs::align256((B ? B : 1) * sizeof(int32_t));
+    const size_t split_rows = B < (size_t)gs::kSplitMaxRows ? B : (size_t)gs::kSplitMaxRows;
+    const size_t sp_bytes = V > gs::kRegMaxV ? gs::align256(split_bytes(split_rows, gs::kSplitMaxWidth)) : 0;
+    const size_t full_bytes = B * gs::scratch_u32_per_row(V) * sizeof(uint32_t);
+    if (fb_bytes + sp_bytes + full_bytes > gs::kStaticScratchBytes) return GS_ERR_UNSUPPORTED;
+    char *p = (char *)base;
+    gs::CallBufs bf{true, (uint32_t *)(p + fb_bytes + sp_bytes), (int32_t *)p, sp_bytes ? p + fb_bytes : nullptr,
+                    sp_bytes};
+    return gs::sample_batch_bufs(s, d_logits, B, V, ld, d_params, d_recent, ld_recent, d_recent_len, W, d_u,
+                                 d_tokens, d_status, nullptr, stream, &bf);
+}
 
 int gs_window_push(uint32_t *d_window, size_t B, size_t ld, size_t W, size_t pos,
                    const uint32_t *d_tokens, void *stream)

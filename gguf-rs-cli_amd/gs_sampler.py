@@ -41,7 +41,7 @@ _ERRNAMES = {
 EXPORTS = [
     "gs_sampler_create", "gs_sampler_destroy", "gs_sampler_set_params",
     "gs_sampler_set_seed", "gs_sampler_get_state", "gs_sampler_set_state",
-    "gs_sampler_reserve", "gs_sample", "gs_sample_batch", "gs_window_push",
+    "gs_sampler_reserve", "gs_sample", "gs_sample_batch", "gs_sample_batch_noalloc", "gs_window_push",
     "gs_synth_logits", "gs_limits", "gs_version",
     # include/gs_gemv.h
     "gs_qmatrix_upload", "gs_qmatrix_destroy", "gs_qmatrix_shape", "gs_gemv",
@@ -96,6 +96,7 @@ def load_library(path=LIB_PATH):
         "gs_sampler_reserve": ([P, SZ, SZ], I),
         "gs_sample": ([P, P, SZ, P, SZ, ctypes.POINTER(ctypes.c_uint32)], I),
         "gs_sample_batch": ([P, P, SZ, SZ, SZ, P, P, SZ, P, SZ, P, P, P, P], I),
+        "gs_sample_batch_noalloc": ([P, P, SZ, SZ, SZ, P, P, SZ, P, SZ, P, P, P, P], I),
         "gs_window_push": ([P, SZ, SZ, SZ, SZ, P, P], I),
         "gs_synth_logits": ([P, SZ, SZ, SZ, U64, U64, ctypes.c_float, P], I),
         "gs_limits": ([ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)], I),
@@ -275,11 +276,14 @@ class Sampler:
         return int(out.value)
 
     def sample_batch(self, logits, tokens, params=None, recent=None, recent_len=None,
-                     u=None, status=None, stream=None, V=None, ld=None, W=None, ld_recent=None):
+                     u=None, status=None, stream=None, V=None, ld=None, W=None, ld_recent=None,
+                     noalloc=False):
         """Batched sampling over B device rows (torch tensors on cuda).
         logits [B, ld] f32; tokens [B] int32/uint32; params [B, 4]-shaped
         gs_params buffer (or None); recent [B, ld_recent] uint32 ids (or None);
-        u [B] f32 draws (or None = this sampler's LCG stream).  Asynchronous."""
+        u [B] f32 draws (or None = this sampler's LCG stream).  Asynchronous.
+        noalloc=True calls gs_sample_batch_noalloc (static scratch, no
+        device allocation)."""
         B = int(logits.shape[0])
         V = int(logits.shape[1]) if V is None else V
         # a size-1 leading dimension may carry any stride (numpy gives 0)
@@ -290,10 +294,11 @@ class Sampler:
                 ld_recent = int(recent.stride(0)) if recent.shape[0] > 1 else W
         else:
             W, ld_recent = 0, 0
-        _check(self._lib.gs_sample_batch(
+        fn = self._lib.gs_sample_batch_noalloc if noalloc else self._lib.gs_sample_batch
+        _check(fn(
             self._h, _ptr(logits), B, V, ld, _ptr(params), _ptr(recent), ld_recent,
             _ptr(recent_len), W, _ptr(u), _ptr(tokens), _ptr(status),
-            _stream_handle(stream)), "gs_sample_batch")
+            _stream_handle(stream)), "gs_sample_batch_noalloc" if noalloc else "gs_sample_batch")
 
 
 def window_push(window, tokens, pos, W=None, stream=None):

@@ -122,6 +122,29 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V,
                     const uint32_t *d_recent_len, size_t W, const float *d_u,
                     uint32_t *d_tokens, int32_t *d_status, void *stream);
 
+/* ---- batched, allocation-free --------------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, semantics and results as
+ * gs_sample_batch, but every scratch buffer (per-row fallback flags, the
+ * split top-k path's virtual rows, the full-vocabulary path's scratch) lives
+ * in one statically sized device array of GS_NOALLOC_SCRATCH_BYTES per GPU,
+ * part of the library's code object and held until the process ends.  The
+ * call makes no hipMalloc/hipFree and no allocating library call.
+ * Limit: fallback flags (4 B per row, 256-byte aligned) + split buffers
+ * (V > 32768 only: 256 KB per row for up to 32 rows) + B rows of
+ * full-vocabulary scratch must fit; otherwise GS_ERR_UNSUPPORTED.
+ * Every call on one GPU shares that GPU's array (whichever sampler makes
+ * it) and the array keeps the last call's contents: calls that overlap on
+ * one GPU (two streams, or two threads) race and must be serialised by the
+ * caller.  Nothing in the array needs to start at zero. */
+#define GS_NOALLOC_SCRATCH_BYTES (64u << 20)
+int gs_sample_batch_noalloc(gs_sampler *s, const float *d_logits, size_t B, size_t V,
+                            size_t ld, const gs_params *d_params,
+                            const uint32_t *d_recent, size_t ld_recent,
+                            const uint32_t *d_recent_len, size_t W, const float *d_u,
+                            uint32_t *d_tokens, int32_t *d_status, void *stream);
+
 /* ---- device-resident decode helpers (decode loop, src/main.rs:279-311) ---
  * Append each row's token to its ring window: window[b*ld + (pos % W)] =
  * tokens[b].  The penalty only depends on how often each id occurs in the
