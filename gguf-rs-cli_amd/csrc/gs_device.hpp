@@ -35,7 +35,13 @@ __device__ __constant__ uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
+// The same function with the table read from `tab` (e.g. a copy in LDS).
+__device__ __forceinline__ float glibc_expf_tab(float x, const uint64_t *tab);
 __device__ __forceinline__ float glibc_expf(float x)
+{
+    return glibc_expf_tab(x, kExp2Tab);
+}
+__device__ __forceinline__ float glibc_expf_tab(float x, const uint64_t *tab)
 {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -56,7 +62,7 @@ __device__ __forceinline__ float glibc_expf(float x)
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd = kd - Shift;
     const double r = __builtin_fma(InvLn2N, xd, -kd);
-    uint64_t t = kExp2Tab[ki & 31];
+    uint64_t t = tab[ki & 31];
     t += ki << 47;
     const double s = __longlong_as_double((long long)t);
     const double z = __builtin_fma(C0, r, C1);

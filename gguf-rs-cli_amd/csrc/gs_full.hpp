@@ -1,0 +1,1419 @@
+// gs_full.hpp -- exact full-vocabulary sampling without sorting the row.
+// (Included inside namespace gs by gs_kernels.hip, after RowSmem, the block
+// helpers and the penalty table.)
+//
+// The reference (src/sampler.rs:44-78) sorts all V scaled logits y
+// (descending, ties by index here), then runs three sequential f32
+// accumulations in sorted order:
+//   seq 1  S  = sum of a_j = expf(y_j - max)                    (:53-54)
+//   seq 2  cum of p_j = a_j / S until cum >= top_p: cut, s2      (:56, :59-67)
+//   seq 3  cum of q_j = p_j / s2 (or p_j) until r < cum          (:68, :71-78)
+// While a running f32 sum stays inside one binade [2^e, 2^(e+1)) every add
+// is integer arithmetic on multiples of g = 2^(e-23): RN(s + v) = s + g k,
+// k = v / g rounded to nearest, ties to even (the only case where k depends
+// on s: the parity of s / g).  Each summand is a monotone function of y, so
+// inside one bin of y its increment k is a monotone step function of y.
+//
+// The elements are counted into 4096 bins of d' = y - m0.  For each bin and
+// accumulation the plan predicts the binade of the running sum and
+// evaluates the exact increment at the bin's edges:
+//   * one value          : every element of the bin adds lvl (no work);
+//   * two values         : the bin gets a record (thr, up): elements with
+//                          y >= up add lvl + 1, elements with thr <= y < up
+//                          are rounding ties, the rest add lvl; a pass
+//                          counts the first two groups;
+//   * more, or a bin where the sum may change binade, reach top_p or pass
+//     the draw r        : the bin is listed (its elements' keys and ids
+//                          are written to a per-row list and sorted).
+// A bin's contribution is then a function of one parity bit (ties go to
+// even, and the elements above a tie are exactly those with y >= up), so the
+// three accumulations are replayed exactly by a walk over the sorted list
+// entries and the counted bins (f_walk), which checks every prediction.
+//
+// Passes over the row: pass 1 (HBM) counts, pass 2 (cache) serves seq 1,
+// pass 3 (cache) seqs 2 and 3.  For a nucleus row s2 is known before pass 3
+// only to a range [top_p, top_p + the largest summand of the cut's bins]; an
+// element whose seq-3 increment that range leaves open is deferred (its id is
+// written) and counted once s2 is exact.  Any failed check returns false:
+// the row then takes the sort-based path (the same result, slower).
+
+// Failure exits (development builds record the line per row).
+#if defined(GS_TIMING) || defined(GS_DIAG)
+// per row (< 1024): [0] failing line of the row, [1] failing line of a walk,
+// [2..7] statistics (see F_STAT uses)
+__device__ int g_vdiag[1024 * 16];
+#define F_NOTE(k) do { if (threadIdx.x == 0 && blockIdx.x < 1024) g_vdiag[blockIdx.x * 16 + (k)] = __LINE__; } while (0)
+#define F_STAT(k, v) do { if (threadIdx.x == 0 && blockIdx.x < 1024) g_vdiag[blockIdx.x * 16 + (k)] = (int)(v); } while (0)
+#else
+#define F_NOTE(k) do { } while (0)
+#define F_STAT(k, v) do { } while (0)
+#endif
+#define F_FAIL() do { F_NOTE(0); return false; } while (0)
+#define F_WFAIL() do { F_NOTE(1); return -1; } while (0)
+
+constexpr float kFDUp = 3.0f;                 // bins cover d' in [-kFDLo, kFDUp]
+constexpr float kFDLo = 18.5f;                // below: a < 2^-26, adds +0 to every sum
+constexpr float kFInvW = (float)kFBins / (kFDUp + kFDLo);
+constexpr double kFDelta = 1.0 / 4096.0;      // relative margin of every prediction
+constexpr float kFMassScale = 4294967296.0f;  // pass-1 masses in 2^-32 units
+constexpr int kFMaxSeg = 512;                 // largest listed bin (wave sort)
+constexpr uint32_t kFDeferCap = 16384;        // deferred seq-3 elements per row
+constexpr uint32_t kFPen = 0x80000000u;       // deferred entry: the id's penalized value
+
+__device__ __forceinline__ int f_bin(float dp)
+{
+    const int b = (int)((kFDUp - dp) * kFInvW);
+    return min(max(b, 0), kFBins - 1);
+}
+__device__ __forceinline__ uint64_t f_entry(float y, uint32_t i) { return ((uint64_t)f2key(y) << 32) | (uint64_t)(~i); }
+__device__ __forceinline__ float f_entry_y(uint64_t en) { return key2f((uint32_t)(en >> 32)); }
+__device__ __forceinline__ uint32_t f_entry_id(uint64_t en) { return ~(uint32_t)en; }
+// walk items: list entries, or a bin (high word 0, bin index in the low bits)
+__device__ __forceinline__ uint64_t f_bin_item(int b) { return (uint64_t)(uint32_t)b; }
+__device__ __forceinline__ bool f_is_bin(uint64_t it) { return (uint32_t)(it >> 32) == 0u; }
+
+// Binade exponent of a positive normal double.
+__device__ __forceinline__ int f_dexp(double x) { return (int)((__double_as_longlong(x) >> 52) & 0x7ff) - 1023; }
+
+// Constants of the three summands.
+struct FSeq {
+    float m, S;
+    bool nuc;
+    const uint64_t *tab;   // expf's table (a copy in LDS)
+};
+// Exact summand of accumulation sq for scaled logit y (src/sampler.rs:54, :56, :68).
+__device__ __forceinline__ float f_val(const FSeq &c, int sq, float y, float s2)
+{
+    const float a = glibc_expf_tab(y - c.m, c.tab);
+    if (sq == 1) return a;
+    const float p = a / c.S;
+    if (sq == 2 || !c.nuc) return p;
+    return p / s2;
+}
+// Increments of summand v at grid exponent e with a tie rounded down / up.
+__device__ __forceinline__ void f_incs(float v, int e, uint32_t *dn, uint32_t *up)
+{
+    const float w = ldexpf(v, 23 - e);
+    if (!(w < 33554432.0f)) { *dn = *up = kSat; return; }
+    const float fl = floorf(w);
+    const float fr = w - fl;
+    *dn = (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+    *up = (uint32_t)fl + (fr >= 0.5f ? 1u : 0u);
+}
+// Smallest y in [ylo, yhi] whose increment reaches lvl + 1 (ties counted as
+// reaching it if `tie_up`); the increment must reach it at yhi.  The search
+// starts at the y where the real summand crosses lvl + 1/2 grid steps (`est`)
+// and gallops over f32 keys to the exact boundary.
+__device__ float f_first(const FSeq &c, int sq, int e, uint32_t lvl, float ylo, float yhi, float s2, bool tie_up,
+                         double est)
+{
+    auto reach = [&](uint32_t k) {
+        uint32_t dn, up;
+        f_incs(f_val(c, sq, key2f(k), s2), e, &dn, &up);
+        return (tie_up ? up : dn) >= lvl + 1u;
+    };
+    const uint32_t klo = f2key(ylo), khi = f2key(yhi);
+    if (reach(klo)) return ylo;
+    // [lo, hi]: reach(lo) false, reach(hi) true
+    uint32_t lo = klo, hi = khi;
+    const float ye = (float)est;
+    if (ye > ylo && ye < yhi) {
+        const uint32_t k0 = f2key(ye);
+        if (reach(k0)) {
+            hi = k0;
+            for (uint32_t d = 1; hi - d > lo; d <<= 1) {
+                if (!reach(hi - d)) { lo = hi - d; break; }
+                hi = hi - d;
+            }
+        } else {
+            lo = k0;
+            for (uint32_t d = 1; lo + d < hi; d <<= 1) {
+                if (reach(lo + d)) { hi = lo + d; break; }
+                lo = lo + d;
+            }
+        }
+    }
+    while (hi - lo > 1u) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (reach(mid)) hi = mid;
+        else lo = mid;
+    }
+    return key2f(hi);
+}
+// A y-interval holding every element bin b can receive (the bin index is
+// computed in f32; the margin covers its rounding).
+__device__ __forceinline__ void f_range(float m0, int b, float *ylo, float *yhi)
+{
+    const double w = (double)(kFDUp + kFDLo) / kFBins;
+    const double hi = (double)m0 + kFDUp - b * w, lo = (double)m0 + kFDUp - (b + 1) * w;
+    const double tol = 2e-5 + 4e-6 * fmax(fabs(hi), fabs(lo));
+    *yhi = (float)(hi + tol);
+    *ylo = (float)(lo - tol);
+}
+// Increment function of a counted bin: nup elements add lvl + 1, then ntie
+// rounding ties at lvl + 1/2 (the first goes to even from the parity before
+// it, which leaves the sum even, so the others add lvl + (lvl & 1)), then
+// nlo elements add lvl.
+__device__ __forceinline__ ParFn f_binfn(uint32_t lvl, uint32_t nup, uint32_t ntie, uint32_t nlo)
+{
+    ParFn f;
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++) {
+        uint64_t n = p + (uint64_t)(lvl + 1u) * nup;
+        if (ntie) {
+            n += lvl + ((n + lvl) & 1u);
+            n += (uint64_t)(ntie - 1u) * (lvl + (lvl & 1u));
+        }
+        n += (uint64_t)lvl * nlo;
+        const uint64_t d = n - p;
+        const uint32_t v = d > kSat ? kSat : (uint32_t)d;
+        if (p == 0) f.f0 = v;
+        else f.f1 = v;
+    }
+    return f;
+}
+__device__ __forceinline__ ParFn f_fn_id() { return ParFn{0u, 0u}; }
+
+// Classify one bin for accumulation sq at grid exponent e: returns 0 (one
+// increment: *lvl), 1 (two: *lvl, *thr, *up), 2 (more: list it).  For seq 3
+// of a nucleus row s2 lies in [s2lo, s2hi]: lvl is the lowest increment over
+// the range, and (thr, up) bound the deferred elements: y >= up adds lvl + 1
+// for every s2 in the range, y < thr adds lvl for every s2.
+__device__ int f_classify(const FSeq &c, int sq, int e, float ylo, float yhi, float s2lo, float s2hi,
+                          uint32_t *lvl, float *thr, float *up)
+{
+    uint32_t d0, u0, d1, u1;
+    f_incs(f_val(c, sq, ylo, s2hi), e, &d0, &u0);
+    f_incs(f_val(c, sq, yhi, s2lo), e, &d1, &u1);
+    if (u1 - d0 > 1u || u1 < d0) return 2;
+    *lvl = d0;
+    if (u1 == d0) return 0;
+    // the real summand reaches (lvl + 1/2) g at y = m + ln((lvl + 1/2) g S s2)
+    const double a = ldexp((double)d0 + 0.5, e - 23) * (sq >= 2 ? (double)c.S : 1.0);
+    const double elo = (double)c.m + log(a * (sq == 3 && c.nuc ? (double)s2lo : 1.0));
+    const double ehi = (double)c.m + log(a * (sq == 3 && c.nuc ? (double)s2hi : 1.0));
+    *thr = f_first(c, sq, e, d0, ylo, yhi, s2lo, true, elo);
+    uint32_t d2, u2;
+    f_incs(f_val(c, sq, yhi, s2hi), e, &d2, &u2);
+    *up = d2 >= d0 + 1u ? f_first(c, sq, e, d0, ylo, yhi, s2hi, false, ehi) : INFINITY;
+    return 1;
+}
+
+// Fields of the per-bin words.
+__device__ __forceinline__ uint32_t f_cls(uint32_t w1, uint32_t w23, int sq)
+{
+    return sq == 1 ? (w1 & 7u) : (sq == 2 ? (w23 & 7u) : ((w23 >> 3) & 7u));
+}
+__device__ __forceinline__ uint32_t f_recix(uint32_t w1, uint32_t w23, int sq)
+{
+    return sq == 1 ? ((w1 >> 3) & kNoRec) : (sq == 2 ? ((w23 >> 6) & kNoRec) : ((w23 >> 16) & kNoRec));
+}
+constexpr uint32_t kW1Listed = 1u << 13, kW1TieFn = 1u << 14;
+constexpr uint32_t kW3Listed = 1u << 26, kW3Visit = 1u << 27, kW3TieFn2 = 1u << 28, kW3TieFn3 = 1u << 29;
+
+// Increment function of bin item b in accumulation sq (a uniform, record or
+// bag bin); *ok = false if the bin is none of these for that accumulation.
+__device__ __forceinline__ ParFn f_item_fn(const FullSmem &f, int sq, int b, int *eb, bool *ok)
+{
+    const uint32_t w1 = f.w1[b], w23 = f.w23[b];
+    const uint32_t cls = f_cls(w1, w23, sq);
+    *ok = cls == kCUni || cls == kCRec || cls == kCBag;
+    *eb = sq == 1 ? (int)((w1 >> 16) & 255u) - 128 : (int)f.ex[b][sq - 2] - 128;
+    const uint32_t val = sq == 3 ? f.v3[b] : f.v1[b];
+    if (cls == kCBag) {
+        const bool tf = sq == 1 ? (w1 & kW1TieFn) != 0u : (w23 & (sq == 2 ? kW3TieFn2 : kW3TieFn3)) != 0u;
+        if (tf) {
+            const uint32_t key = (uint32_t)b | ((uint32_t)sq << 16);
+            for (int i = 0; i < f.ntiefn; i++)
+                if (f.tiefn[i].key == key) return ParFn{f.tiefn[i].f0, f.tiefn[i].f1};
+            *ok = false;
+        }
+        const uint32_t v = val > kSat ? kSat : val;
+        return ParFn{v, v};
+    }
+    const uint32_t n = f.cnt[b];
+    uint32_t nup = 0u, ntie = 0u;
+    if (cls == kCRec) {
+        const uint32_t rr = f_recix(w1, w23, sq);
+        nup = f.u.rec[rr].hi;
+        ntie = f.u.rec[rr].tie;
+    }
+    return f_binfn(val, nup, ntie, n - nup - ntie);
+}
+
+// ---------------------------------------------------------------------------
+// Block helpers.
+__device__ double f_block_excl_f64(double v, double *tot, RowSmem &sm)
+{
+    const int lane = lane_id(), w = wave_id();
+    double incl = v;
+    for (int d = 1; d < 64; d <<= 1) {
+        const double o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) sm.red_f64[w] = incl;
+    __syncthreads();
+    double pre = 0.0, all = 0.0;
+    for (int i = 0; i < kWaves; i++) { if (i < w) pre += sm.red_f64[i]; all += sm.red_f64[i]; }
+    __syncthreads();
+    *tot = all;
+    return pre + incl - v;
+}
+__device__ float f_block_max(float v, RowSmem &sm)
+{
+    for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+    if (lane_id() == 0) sm.red_f32[wave_id()] = v;
+    __syncthreads();
+    float r = sm.red_f32[0];
+    for (int i = 1; i < kWaves; i++) r = fmaxf(r, sm.red_f32[i]);
+    __syncthreads();
+    return r;
+}
+// Segmented scan element: `st` = a segment starts inside.
+struct SegFn { uint32_t st; ParFn f; };
+__device__ __forceinline__ SegFn seg_op(const SegFn &a, const SegFn &b)
+{
+    SegFn r;
+    r.st = a.st | b.st;
+    r.f = b.st ? b.f : par_compose(a.f, b.f);
+    return r;
+}
+__device__ SegFn f_block_seg_excl(SegFn v, RowSmem &sm, ParFn *wtot, uint32_t *wst)
+{
+    const int lane = lane_id(), w = wave_id();
+    SegFn incl = v;
+    for (int d = 1; d < 64; d <<= 1) {
+        SegFn o;
+        o.st = __shfl_up(incl.st, d, 64);
+        o.f.f0 = __shfl_up(incl.f.f0, d, 64);
+        o.f.f1 = __shfl_up(incl.f.f1, d, 64);
+        if (lane >= d) incl = seg_op(o, incl);
+    }
+    if (lane == 63) { wtot[w] = incl.f; wst[w] = incl.st; }
+    __syncthreads();
+    SegFn pre{0u, f_fn_id()};
+    for (int i = 0; i < w; i++) pre = seg_op(pre, SegFn{wst[i], wtot[i]});
+    __syncthreads();
+    SegFn ex;
+    ex.st = __shfl_up(incl.st, 1, 64);
+    ex.f.f0 = __shfl_up(incl.f.f0, 1, 64);
+    ex.f.f1 = __shfl_up(incl.f.f1, 1, 64);
+    if (lane == 0) ex = SegFn{0u, f_fn_id()};
+    return seg_op(pre, ex);
+}
+
+// ---------------------------------------------------------------------------
+// The walk: exact replay of one accumulation over a sorted item array
+// (list entries and counted bins), stopping at the first item after which
+// the predicate holds.  Items are processed in chunks of kThreads * kWC, each
+// thread owning kWC consecutive items.  Per round: the binade of the sum
+// before every item is predicted (a prefix scan of the items' increments at
+// the predicted grids, refined twice); items of one predicted binade form a
+// segment whose integer increments are composed by a segmented scan; one
+// thread chains the segments (each ends with the item that leaves the
+// binade, added with the reference's own f32 add); then every item checks
+// its prediction.  The first failed check restarts the round from that
+// item with the exact sum before it.  Returns the event item (and the sum
+// after it), N if none (the final sum), -1 on failure.
+constexpr int kWC = 4;
+constexpr int kWMaxRounds = 96;
+enum { kWFailCross = 1, kWFailBin = 2, kWFailRepred = 3 };
+struct WArgs {
+    FSeq c;
+    int sq;
+    float s2;
+    int pk;          // 0 none, 1 s >= thr, 2 thr < s
+    float thr;
+};
+__device__ __forceinline__ bool w_pred(const WArgs &wa, float s)
+{
+    return wa.pk == 1 ? s >= wa.thr : (wa.pk == 2 ? wa.thr < s : false);
+}
+
+// Increment function of walk item q (an element's summand or a bin) at grid e.
+__device__ __forceinline__ ParFn w_fn(const FullSmem &f, const WArgs &wa, bool bin, float v, int e, bool *bad)
+{
+    if (bin) {
+        int eb;
+        bool ok;
+        const ParFn fn = f_item_fn(f, wa.sq, __float_as_int(v), &eb, &ok);
+        *bad = !ok || (eb != e && (fn.f0 | fn.f1));
+        return fn;
+    }
+    *bad = false;
+    return elem_fn(v, e);
+}
+
+__device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa, float *s_out, int slot)
+{
+    int nrounds = 0;
+    FullSmem &f = sm.x.fs;
+    const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+    constexpr int kNone = 0x7fffffff;
+    float s = 0.0f;
+    int pos = 0;
+    // leading items from s == 0 (0 + v == v); every thread does the same
+    while (pos < N && s == 0.0f) {
+        const uint64_t it = ldg(items + pos);
+        if (f_is_bin(it)) {
+            int eb;
+            bool ok;
+            const ParFn fn = f_item_fn(f, wa.sq, (int)(uint32_t)it, &eb, &ok);
+            if (!ok || fn.f0 || fn.f1) { *s_out = s; F_WFAIL(); }
+        } else {
+            s = f_val(wa.c, wa.sq, f_entry_y(it), wa.s2);
+            if (w_pred(wa, s)) { *s_out = s; return pos; }
+        }
+        pos++;
+    }
+    while (pos < N) {
+        const int cend = min(pos + kThreads * kWC, N);
+        const int j0 = pos + t * kWC;
+        float v[kWC];
+        uint32_t isbin = 0u;
+#pragma unroll
+        for (int q = 0; q < kWC; q++) {
+            v[q] = 0.0f;
+            const int j = j0 + q;
+            if (j < cend) {
+                const uint64_t it = ldg(items + j);
+                if (f_is_bin(it)) { isbin |= 1u << q; v[q] = __int_as_float((int)(uint32_t)it); }
+                else v[q] = f_val(wa.c, wa.sq, f_entry_y(it), wa.s2);
+            }
+        }
+        int start = pos;
+        for (int round = 0;; round++) {
+            if (round >= kWMaxRounds) { *s_out = s; F_WFAIL(); }
+            nrounds++;
+            F_STAT(slot, nrounds);
+            // ---- predicted grid of the sum before every item: three scans ----
+            int e[kWC];
+            double tpre = 0.0, tot;
+            for (int it = 0; it < 4; it++) {
+                double loc = 0.0;
+                const double base = (double)s + tpre;
+#pragma unroll
+                for (int q = 0; q < kWC; q++) {
+                    const int j = j0 + q;
+                    if (it == 3) e[q] = 0;
+                    if (j < start || j >= cend) continue;
+                    const int eq = j == start ? grid_exp(s) : f_dexp(base + loc);
+                    if (it == 3) e[q] = eq;
+                    double cq;
+                    if (isbin & (1u << q)) {
+                        int eb;
+                        bool ok;
+                        const ParFn fn = f_item_fn(f, wa.sq, __float_as_int(v[q]), &eb, &ok);
+                        cq = it == 0 ? ldexp(0.5 * ((double)fn.f0 + (double)fn.f1), eb - 23)
+                                     : ldexp((double)fn.f0, eb - 23);
+                    } else if (it == 0) {
+                        cq = (double)v[q];
+                    } else {
+                        uint32_t dn, up;
+                        f_incs(v[q], eq, &dn, &up);
+                        cq = ldexp((double)dn, eq - 23);
+                    }
+                    loc += cq;
+                }
+                if (it < 3) tpre = f_block_excl_f64(loc, &tot, sm);
+            }
+            // ---- segments: an item starts one if its grid differs from the item before ----
+            int prev_e = __shfl_up(e[kWC - 1], 1, 64);
+            if (lane == 63) sm.red_i32[w] = e[kWC - 1];
+            __syncthreads();
+            if (lane == 0) prev_e = w > 0 ? sm.red_i32[w - 1] : 0;
+            uint32_t starts = 0u, nst = 0u;
+            {
+                int ep = prev_e;
+#pragma unroll
+                for (int q = 0; q < kWC; q++) {
+                    const int j = j0 + q;
+                    if (j >= start && j < cend && (j == start || e[q] != ep)) { starts |= 1u << q; nst++; }
+                    ep = e[q];
+                }
+            }
+            uint32_t nseg;
+            const uint32_t ord0 = block_excl_u32(nst, &nseg, sm);   // contains barriers
+            const int nused = (int)min(nseg, (uint32_t)kWSeg);
+            SegFn agg{0u, f_fn_id()};
+#pragma unroll
+            for (int q = 0; q < kWC; q++) {
+                const int j = j0 + q;
+                if (j < start || j >= cend) continue;
+                bool bad;
+                const ParFn fn = w_fn(f, wa, (isbin >> q) & 1u, v[q], e[q], &bad);
+                agg = seg_op(agg, SegFn{(starts >> q) & 1u, fn});
+            }
+            const SegFn carry = f_block_seg_excl(agg, sm, f.wtot, f.wst);   // contains barriers
+            // segment table: first item and grid of each segment; for each
+            // segment followed by another, the prefix before its last item
+            // (the one that leaves the binade) and that item's summand
+            ParFn last_ex = f_fn_id();
+            float last_v = 0.0f;
+            bool last_bin = false;
+            {
+                uint32_t ord = ord0;
+                SegFn run = carry;
+                ParFn pex = f_fn_id();
+                float pv = 0.0f;
+                bool pbin = false;
+#pragma unroll
+                for (int q = 0; q < kWC; q++) {
+                    const int j = j0 + q;
+                    if (j < start || j >= cend) continue;
+                    const bool st = (starts >> q) & 1u;
+                    if (st) {
+                        if (ord <= (uint32_t)kWSeg) { f.sj[ord] = (uint32_t)j; f.se[ord] = e[q]; }
+                        if (q > 0 && ord >= 1u && ord - 1u < (uint32_t)nused) {
+                            f.sF0[ord - 1u] = pex.f0;
+                            f.sF1[ord - 1u] = pex.f1;
+                            f.sv[ord - 1u] = pbin ? __int_as_float(0x7fc00000) : pv;
+                        }
+                        ord++;
+                    }
+                    bool bad;
+                    const ParFn fn = w_fn(f, wa, (isbin >> q) & 1u, v[q], e[q], &bad);
+                    pex = st ? f_fn_id() : run.f;
+                    pv = v[q];
+                    pbin = (isbin >> q) & 1u;
+                    run = st ? SegFn{1u, fn} : SegFn{run.st, par_compose(run.f, fn)};
+                }
+                last_ex = pex;
+                last_v = pv;
+                last_bin = pbin;
+            }
+            // the previous thread's last item, for a segment starting at my first item
+            {
+                ParFn nex;
+                nex.f0 = __shfl_up(last_ex.f0, 1, 64);
+                nex.f1 = __shfl_up(last_ex.f1, 1, 64);
+                float nv = __shfl_up(last_v, 1, 64);
+                int nbin = __shfl_up((int)last_bin, 1, 64);
+                if (lane == 63) { f.nbF0[w] = last_ex.f0; f.nbF1[w] = last_ex.f1; f.nbv[w] = last_v; f.nbb[w] = last_bin; }
+                __syncthreads();
+                if (lane == 0 && w > 0) { nex.f0 = f.nbF0[w - 1]; nex.f1 = f.nbF1[w - 1]; nv = f.nbv[w - 1]; nbin = f.nbb[w - 1]; }
+                if ((starts & 1u) && j0 > start && ord0 >= 1u && ord0 - 1u < (uint32_t)nused) {
+                    f.sF0[ord0 - 1u] = nex.f0;
+                    f.sF1[ord0 - 1u] = nex.f1;
+                    f.sv[ord0 - 1u] = nbin ? __int_as_float(0x7fc00000) : nv;
+                }
+            }
+            if (t == 0) { f.wfail = kNone; f.wev = kNone; }
+            __syncthreads();
+            // ---- chain the segments (one thread) ----
+            if (t == 0) {
+                float cs = s;
+                int nok = nused, rend = nseg > (uint32_t)nused ? (int)f.sj[nused] : cend;
+                for (int k = 0; k < nused; k++) {
+                    f.ss[k] = cs;
+                    const int ek = f.se[k];
+                    if (grid_exp(cs) != ek) {          // never for k = 0 (its grid is the sum's)
+                        nok = k;
+                        rend = (int)f.sj[k];
+                        f.wfail = rend;
+                        f.wfkind = kWFailRepred;
+                        f.wfs = cs;
+                        break;
+                    }
+                    const uint32_t M = (uint32_t)ldexpf(cs, 23 - ek);
+                    f.sM[k] = M;
+                    if (k + 1 < (int)nseg) {
+                        const float vc = f.sv[k];
+                        if (isnan(vc)) {               // a bin cannot leave the binade
+                            nok = k + 1;
+                            rend = (int)f.sj[k + 1] - 1;
+                            f.wfail = rend;
+                            f.wfkind = kWFailBin;
+                            break;
+                        }
+                        const ParFn F{f.sF0[k], f.sF1[k]};
+                        const uint32_t nb = M + par_apply(F, M & 1u);
+                        cs = ldexpf((float)nb, ek - 23) + vc;   // the reference's f32 add
+                        f.ss[k + 1] = cs;
+                    }
+                }
+                f.nseg = nok;
+                f.round_end = rend;
+            }
+            __syncthreads();
+            const int nok = f.nseg, rend = f.round_end;
+            // ---- check every item up to rend, find the event ----
+            int myfail = kNone, mykind = 0, myev = kNone;
+            float myfs = 0.0f, myevs = 0.0f, mylast = 0.0f;
+            {
+                uint32_t ord = ord0;
+                SegFn run = carry;
+                int k = (int)ord0 - 1;
+#pragma unroll
+                for (int q = 0; q < kWC; q++) {
+                    const int j = j0 + q;
+                    if (j < start || j >= rend) continue;
+                    const bool st = (starts >> q) & 1u;
+                    if (st) { k = (int)ord; ord++; }
+                    bool bad;
+                    const bool bin = (isbin >> q) & 1u;
+                    const ParFn fn = w_fn(f, wa, bin, v[q], e[q], &bad);
+                    const ParFn ex = st ? f_fn_id() : run.f;
+                    run = st ? SegFn{1u, fn} : SegFn{run.st, par_compose(run.f, fn)};
+                    if (myfail != kNone || myev != kNone) continue;
+                    const int ek = e[q];
+                    const uint32_t M = f.sM[k];
+                    const uint32_t nb = M + par_apply(ex, M & 1u);
+                    const bool crossing = k + 1 < (int)nseg && k + 1 <= kWSeg && j + 1 == (int)f.sj[k + 1];
+                    float sa;
+                    if (crossing) {
+                        sa = f.ss[k + 1];
+                    } else {
+                        const uint32_t na = nb + par_apply(fn, nb & 1u);
+                        if (bad || (bin && na >= (1u << 24))) { myfail = j; mykind = kWFailBin; continue; }
+                        if (na >= (1u << 24)) {
+                            myfail = j;
+                            mykind = kWFailCross;
+                            myfs = ldexpf((float)nb, ek - 23) + v[q];   // the reference's f32 add
+                            continue;
+                        }
+                        sa = ldexpf((float)na, ek - 23);
+                    }
+                    if (w_pred(wa, sa)) {
+                        if (bin) { myfail = j; mykind = kWFailBin; continue; }
+                        myev = j;
+                        myevs = sa;
+                    }
+                    mylast = sa;
+                }
+            }
+            (void)nok;
+            if (myfail != kNone) atomicMin(&f.wfail, myfail);
+            if (myev != kNone) atomicMin(&f.wev, myev);
+            __syncthreads();
+            const int gfail = f.wfail, gev = f.wev;
+            if (myfail == gfail && myfail != kNone) { f.wfkind = mykind; f.wfs = myfs; }
+            if (myev == gev && myev != kNone) f.wevs = myevs;
+            if (rend - 1 >= j0 && rend - 1 < j0 + kWC && rend - 1 >= start) f.wends = mylast;
+            __syncthreads();
+            const int kind = f.wfkind;
+            const float fs = f.wfs, evs = f.wevs, ends = f.wends;
+            const float snext = (rend < cend && gfail == kNone) ? f.ss[nseg > (uint32_t)nused ? nused : nok] : 0.0f;
+            __syncthreads();
+            if (gev < gfail) { *s_out = evs; return gev; }
+            if (gfail != kNone) {
+                if (kind == kWFailBin) {
+                    F_STAT(14, gfail);
+                    F_STAT(15, (int)(uint32_t)ldg(items + gfail) | ((int)f_is_bin(ldg(items + gfail)) << 31));
+                    F_STAT(13, N);
+                    *s_out = s;
+                    F_WFAIL();
+                }
+                s = fs;
+                if (kind == kWFailCross) {
+                    if (w_pred(wa, s)) { *s_out = s; return gfail; }
+                    start = gfail + 1;
+                } else {
+                    start = gfail;
+                }
+            } else if (rend >= cend) {
+                s = rend > start ? ends : s;
+                start = cend;
+            } else {
+                s = snext;
+                start = rend;
+            }
+            if (start >= cend) break;
+        }
+        pos = cend;
+    }
+    *s_out = s;
+    return N;
+}
+
+// ---------------------------------------------------------------------------
+// Rank of list entry `en` in the list segment [st, end): the number of
+// entries greater than it (the order is key descending, then index
+// ascending; removed entries are 0 and rank below every real one).
+__device__ __forceinline__ uint32_t f_rank(const uint64_t *gl, uint32_t st, uint32_t end, uint64_t en)
+{
+    uint32_t rank = 0u, i = st;
+    for (; i + 4u <= end; i += 4u) {
+        const uint64_t a0 = ldg(gl + i), a1 = ldg(gl + i + 1), a2 = ldg(gl + i + 2), a3 = ldg(gl + i + 3);
+        rank += (a0 > en) + (a1 > en) + (a2 > en) + (a3 > en);
+    }
+    for (; i < end; i++) rank += ldg(gl + i) > en;
+    return rank;
+}
+
+// The walk items of bins [0, nb), in order: the overflow entries, then per
+// bin either its list entries sorted (`lst(b)`: ranked from its list segment
+// [seg, sege)) or one bin item (`item(b)`).  A listed bin's first item
+// offset goes to v1[b].  Returns the item count, -1 if it does not fit.
+template <class Lst, class Item>
+__device__ int f_items(RowSmem &sm, const uint64_t *gl, uint64_t *items, size_t icap, int nb, int nov,
+                       Lst lst, Item item)
+{
+    FullSmem &f = sm.x.fs;
+    const int t = threadIdx.x;
+    constexpr int kPer = kFBins / kThreads;
+    uint32_t n[kPer], loc = 0;
+#pragma unroll
+    for (int c = 0; c < kPer; c++) {
+        const int b = kPer * t + c;
+        n[c] = 0u;
+        if (b < nb && f.cnt[b]) n[c] = lst(b) ? f.cnt[b] : (item(b) ? 1u : 0u);
+        loc += n[c];
+    }
+    uint32_t tot;
+    uint32_t o = block_excl_u32(loc, &tot, sm) + (uint32_t)nov;
+    if ((size_t)tot + nov > icap) return -1;
+#pragma unroll
+    for (int c = 0; c < kPer; c++) {
+        const int b = kPer * t + c;
+        if (n[c]) {
+            if (lst(b)) f.v1[b] = o;
+            else stg(items + o, f_bin_item(b));
+        }
+        o += n[c];
+    }
+    __syncthreads();
+    const int nover = f.nover;
+    for (int p = t; p < nover; p += kThreads) {
+        const uint64_t en = ldg(gl + p);
+        if (en) stg(items + f_rank(gl, 0u, (uint32_t)nover, en), en);
+    }
+    for (uint32_t p = (uint32_t)nover + t; p < f.list_end; p += kThreads) {
+        const uint64_t en = ldg(gl + p);
+        if (!en) continue;
+        const int b = f_bin(f_entry_y(en) - f.m0);
+        if (b >= nb || !lst(b)) continue;
+        const uint32_t rk = f_rank(gl, f.seg[b], f.sege[b], en);
+        if (rk < f.cnt[b]) stg(items + f.v1[b] + rk, en);
+        else f.fail = 1;
+    }
+    __threadfence_block();
+    __syncthreads();
+    return f.fail ? -1 : (int)tot + nov;
+}
+
+// Bag bins of accumulation sq: the exact increments of their list entries
+// are summed into v1 / v3 (zeroed by the caller); rounding ties are set
+// aside, and each bag bin that holds some gets its increment function in the
+// tie table: the ties are visited in order, each after the bin's non-tie
+// elements above it.
+__device__ void f_bags(RowSmem &sm, const uint64_t *gl, const FSeq &c, int sq, float s2)
+{
+    FullSmem &f = sm.x.fs;
+    const int t = threadIdx.x, lane = lane_id();
+    uint32_t *val = sq == 3 ? f.v3 : f.v1;
+    if (t == 0) f.nties = 0;
+    __syncthreads();
+    auto grid = [&](int b) {
+        return sq == 1 ? (int)((f.w1[b] >> 16) & 255u) - 128 : (int)f.ex[b][sq - 2] - 128;
+    };
+    for (uint32_t p = (uint32_t)f.nover + t; p < f.list_end; p += kThreads) {
+        const uint64_t en = ldg(gl + p);
+        if (!en) continue;
+        const float y = f_entry_y(en);
+        const int b = f_bin(y - f.m0);
+        if (f_cls(f.w1[b], f.w23[b], sq) != kCBag) continue;
+        uint32_t dn, up;
+        f_incs(f_val(c, sq, y, s2), grid(b), &dn, &up);
+        if (dn >= (1u << 24)) { f.fail = 1; continue; }
+        if (dn == up) {
+            atomicAdd(&val[b], dn);
+        } else {
+            const int slot = atomicAdd(&f.nties, 1);
+            if (slot < kTieCap) f.ties[slot] = FullTie{en, (uint32_t)b | ((uint32_t)sq << 16), dn};
+            else f.fail = 1;
+        }
+    }
+    __syncthreads();
+    const int nt = min(f.nties, kTieCap);
+    for (int i = wave_id(); i < nt; i += kWaves) {
+        const uint32_t key = f.ties[i].key;
+        bool first = true;
+        for (int j = 0; j < i; j++) first &= f.ties[j].key != key;
+        if (!first) continue;
+        const int b = (int)(key & 0xffffu);
+        const int e = grid(b);
+        const uint32_t st = f.seg[b], end = f.sege[b];
+        // the bin's ties, in the walk's order (entry descending)
+        uint64_t done = ~0ull;           // entries below this one remain
+        uint64_t n0 = 0, n1 = 1;         // the sum in grid units from parity 0 / 1
+        uint32_t acc = 0u;               // non-tie increments added so far
+        for (int k = 0; k < nt; k++) {
+            // next tie of this bin: the largest entry below `done`
+            uint64_t best = 0ull;
+            uint32_t bk = 0u;
+            for (int j = 0; j < nt; j++) {
+                if (f.ties[j].key != key) continue;
+                const uint64_t ej = f.ties[j].en;
+                if (ej < done && ej > best) { best = ej; bk = f.ties[j].k; }
+            }
+            if (!best) break;
+            // non-tie increments of entries above it
+            uint32_t above = 0u;
+            for (uint32_t q = st + lane; q < end; q += 64) {
+                const uint64_t eq = ldg(gl + q);
+                if (!eq || eq <= best) continue;
+                uint32_t dn, up;
+                f_incs(f_val(c, sq, f_entry_y(eq), s2), e, &dn, &up);
+                if (dn == up) above += dn;
+            }
+            for (int d = 32; d > 0; d >>= 1) above += __shfl_xor(above, d, 64);
+            n0 += above - acc;
+            n1 += above - acc;
+            acc = above;
+            n0 += bk + ((n0 + bk) & 1u);
+            n1 += bk + ((n1 + bk) & 1u);
+            done = best;
+        }
+        const uint32_t tot = val[b];
+        n0 += tot - acc;
+        n1 += tot - acc;
+        if (lane == 0) {
+            const int slot = atomicAdd(&f.ntiefn, 1);
+            if (slot < kTieCap) {
+                const uint64_t d0 = n0, d1 = n1 - 1u;
+                f.tiefn[slot] = FullTieFn{key, d0 > kSat ? kSat : (uint32_t)d0, d1 > kSat ? kSat : (uint32_t)d1};
+                if (sq == 1) atomicOr(&f.w1[b], kW1TieFn);
+                else atomicOr(&f.w23[b], sq == 2 ? kW3TieFn2 : kW3TieFn3);
+            } else {
+                f.fail = 1;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// The exact full-vocabulary path.  Returns true with *tok / *status set, or
+// false to hand the row to the sort-based path.  `gl` is the row's scratch
+// (lcap u64 words).
+__device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float top_p, bool has_pen, float r,
+                            uint64_t *gl, size_t lcap, int *tok, int *status)
+{
+    FullSmem &f = sm.x.fs;
+    const int t = threadIdx.x;
+    constexpr int kPer = kFBins / kThreads;
+    static_assert(kPer * kThreads == kFBins, "bins per thread");
+    const bool t_one = (T == 1.0f);
+    const bool nuc = top_p < 1.0f;
+    // scratch: list | seq-1 walk items | seq-2/3 walk items | deferred ids
+    const size_t lsz = (size_t)V + kFOverCap + 2 * kHashSlots;
+    const size_t isz = (size_t)V + kFBins + kFOverCap + 2 * kHashSlots;
+    if (lcap < lsz + 2 * isz + kFDeferCap / 2) F_FAIL();
+    uint64_t *items1 = gl + lsz;
+    uint64_t *items = items1 + isz;
+    uint32_t *defer = reinterpret_cast<uint32_t *>(items + isz);
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+    const int n4 = V >> 2;
+    if (n4 == 0) F_FAIL();
+    auto ydiv = [&](float x) { return t_one ? x : x / T; };
+    auto pen_y = [&](int s) { return ydiv(__uint_as_float(sm.hval[s])); };
+
+    for (int b = t; b < kFBins; b += kThreads) { f.cnt[b] = 0u; f.v1[b] = 0u; }
+    for (int b = t; b < kFMassBins; b += kThreads) f.u.mass64[b] = 0ull;
+    if (t < 32) f.exptab[t] = kExp2Tab[t];
+    if (t == 0) { f.nover = 0; f.nrec = 0; f.fail = 0; f.ndefer = 0; f.ntiefn = 0; }
+
+    // ---- pass 1 (HBM): counts, masses of the top bins, max, NaN -------------
+    float tmax = -INFINITY;
+    int nan = 0;
+    float m0 = 0.0f;
+    auto visit1 = [&](int i, float y) {
+        nan |= (int)isnan(y);
+        if (y > tmax && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) tmax = y;
+        const float dp = y - m0;
+        if (dp > kFDUp) {
+            const int slot = atomicAdd(&f.nover, 1);
+            if (slot < kFOverCap) f.over[slot] = f_entry(y, (uint32_t)i);
+        } else if (dp >= -kFDLo) {
+            const int b = f_bin(dp);
+            atomicAdd(&f.cnt[b], 1u);
+            if (b < kFMassBins)
+                atomicAdd((unsigned long long *)&f.u.mass64[b], (unsigned long long)(fast_exp(dp) * kFMassScale));
+        }
+    };
+    for (int base = 0; base < n4; base += kThreads * kUnroll) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));
+        if (base == 0) {
+            float lm = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++)
+                if (u * kThreads + t < n4) lm = fmaxf(lm, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
+            m0 = ydiv(f_block_max(lm, sm));
+            if (!isfinite(m0)) F_FAIL();
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int q = base + u * kThreads + t;
+            if (q < n4) {
+                visit1(4 * q + 0, ydiv(v[u].x));
+                visit1(4 * q + 1, ydiv(v[u].y));
+                visit1(4 * q + 2, ydiv(v[u].z));
+                visit1(4 * q + 3, ydiv(v[u].w));
+            }
+        }
+    }
+    for (int i = (n4 << 2) + t; i < V; i += kThreads) visit1(i, ydiv(ldg(row + i)));
+    if (has_pen) {
+        for (int s = t; s < kHashSlots; s += kThreads) {
+            if (sm.hkey[s] == kEmpty) continue;
+            const float y = pen_y(s);
+            nan |= (int)isnan(y);
+            tmax = fmaxf(tmax, y);
+        }
+    }
+    if (block_or(nan, sm) || sm.flag_nan) { *status = GS_ERR_NAN; *tok = 0; return true; }
+    const float m = f_block_max(tmax, sm);
+    *status = GS_OK;
+    if (!isfinite(m) || m0 > m || f.nover > kFOverCap) F_FAIL();
+    GS_STAMP(10);
+    if (t == 0) { f.m = m; f.m0 = m0; }
+
+    // ---- penalty: the raw values of penalized ids leave, their penalized
+    // values join (exact counts; v1 counts the raw values per bin, which the
+    // list segments must still hold room for) ----------------------------------
+    if (has_pen) {
+        for (int j = t; j < f.nover; j += kThreads)
+            if (hash_find(sm, f_entry_id(f.over[j])) >= 0) f.over[j] = 0ull;
+        __syncthreads();
+        for (int s = t; s < kHashSlots; s += kThreads) {
+            const uint32_t id = sm.hkey[s];
+            if (id == kEmpty) continue;
+            const float dr = ydiv(ldg(row + id)) - m0;
+            if (dr <= kFDUp && dr >= -kFDLo) {
+                const int b = f_bin(dr);
+                atomicSub(&f.cnt[b], 1u);
+                atomicAdd(&f.v1[b], 1u);
+                if (b < kFMassBins)
+                    atomicAdd((unsigned long long *)&f.u.mass64[b], 0ull - (unsigned long long)(fast_exp(dr) * kFMassScale));
+            }
+            const float yp = pen_y(s);
+            const float dq = yp - m0;
+            if (dq > kFDUp) {
+                const int slot = atomicAdd(&f.nover, 1);
+                if (slot < kFOverCap) f.over[slot] = f_entry(yp, id);
+            } else if (dq >= -kFDLo) {
+                const int b = f_bin(dq);
+                atomicAdd(&f.cnt[b], 1u);
+                if (b < kFMassBins)
+                    atomicAdd((unsigned long long *)&f.u.mass64[b], (unsigned long long)(fast_exp(dq) * kFMassScale));
+            }
+        }
+        __syncthreads();
+        if (f.nover > kFOverCap) F_FAIL();
+    }
+    const int nover = f.nover;
+    const FSeq c{m, 1.0f, nuc, f.exptab};
+    const double wbin = (double)(kFDUp + kFDLo) / kFBins;
+    const double shift = (double)m0 - (double)m;
+    auto e_at = [&](double bpos) { return exp((double)kFDUp - bpos * wbin + shift); };
+    const double dl = 1.0 - kFDelta, dh = 1.0 + kFDelta;
+
+    // ---- plan A (seq 1): the running sum before each bin, predicted from
+    // the masses (top bins) and the counts times the rounded increment of the
+    // bin's centre (the rest), refined twice; then each bin's class:
+    //   listed-and-sorted (the sum may change binade in it, or the top bin),
+    //   uniform, record (two increments), or bag (more) ---------------------
+    {
+        double osum = 0.0;
+        for (int j = t; j < nover; j += kThreads) {
+            const uint64_t en = f.over[j];
+            if (en) osum += (double)glibc_expf_tab(f_entry_y(en) - m, f.exptab);
+        }
+        double otot;
+        f_block_excl_f64(osum, &otot, sm);
+        osum = otot;
+        uint32_t cn[kPer];
+        double mb[kPer], ctr[kPer];
+        const double mscale = exp(shift) / (double)kFMassScale;
+        double loc = 0.0;
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            cn[q] = f.cnt[b];
+            ctr[q] = e_at((double)b + 0.5);
+            mb[q] = b < kFMassBins ? (double)(int64_t)f.u.mass64[b] * mscale : (double)cn[q] * ctr[q];
+            if (mb[q] < 0.0) mb[q] = 0.0;
+            loc += mb[q];
+        }
+        double tot;
+        double pre = f_block_excl_f64(loc, &tot, sm) + osum;
+        double ct[kPer];
+        for (int round = 0; round < 2; round++) {
+            double lo = pre;
+            loc = 0.0;
+#pragma unroll
+            for (int q = 0; q < kPer; q++) {
+                const int b = kPer * t + q;
+                ct[q] = mb[q];
+                if (b >= kFMassBins && cn[q] && lo > 0.0) {
+                    const double g = ldexp(1.0, f_dexp(lo) - 23);
+                    ct[q] = (double)cn[q] * rint(ctr[q] / g) * g;
+                }
+                lo += ct[q];
+                loc += ct[q];
+            }
+            pre = f_block_excl_f64(loc, &tot, sm) + osum;
+        }
+        // classes (records overwrite the masses: every thread has read
+        // them); the predicted sums before / after each bin go through LDS
+        {
+            double lo = pre;
+#pragma unroll
+            for (int q = 0; q < kPer; q++) {
+                const int b = kPer * t + q;
+                f.seg[b] = __float_as_uint((float)lo);
+                lo += ct[q];
+                f.sege[b] = __float_as_uint((float)lo);
+            }
+        }
+        uint32_t capl = 0;
+#pragma unroll 1
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            const double lo = (double)__uint_as_float(f.seg[b]), hi = (double)__uint_as_float(f.sege[b]);
+            const uint32_t n = f.cnt[b];
+            uint32_t cls = kCNone, rec = kNoRec, lvl = 0u;
+            int e = 0;
+            if (n) {
+                if (b == 0 || !(lo > 0.0) || f_dexp(lo * dl) != f_dexp(hi * dh)) {
+                    cls = kCLst;
+                } else {
+                    e = f_dexp(lo);
+                    float ylo, yhi, thr = 0.0f, up = 0.0f;
+                    f_range(m0, b, &ylo, &yhi);
+                    const int k = f_classify(c, 1, e, ylo, yhi, 1.0f, 1.0f, &lvl, &thr, &up);
+                    cls = k == 0 ? kCUni : kCBag;
+                    if (k == 1 && n < 65536u) {
+                        const int rr = atomicAdd(&f.nrec, 1);
+                        if (rr < kRecCap) { f.u.rec[rr] = FullRec{thr, up, 0u, 0u}; rec = (uint32_t)rr; cls = kCRec; }
+                    }
+                }
+            }
+            const bool listed = cls == kCBag || cls == kCLst;
+            f.w1[b] = cls | (rec << 3) | (listed ? kW1Listed : 0u) | ((uint32_t)(e + 128) << 16);
+            const uint32_t cap = listed ? n + f.v1[b] : 0u;
+            if (cls == kCLst && cap > (uint32_t)(16 * kThreads)) f.fail = 1;
+            f.v1[b] = cls == kCBag ? 0u : lvl;
+            f.sege[b] = cap;
+            capl += cap;
+        }
+        uint32_t ltot;
+        uint32_t o = block_excl_u32(capl, &ltot, sm) + (uint32_t)nover;
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            const uint32_t cap = f.sege[b];
+            f.seg[b] = o;
+            f.sege[b] = o;
+            o += cap;
+        }
+        if (t == 0) f.list_end = (uint32_t)nover + ltot;
+    }
+    for (int j = t; j < nover; j += kThreads) stg(gl + j, f.over[j]);
+    __syncthreads();
+    GS_STAMP(11);
+    if (f.fail || f.list_end > lsz) F_FAIL();
+
+    // ---- pass 2 (cache): seq-1 record counts; listed bins written ----------
+    auto visit2 = [&](int i, float y) {
+        const float dp = y - m0;
+        if (!(dp <= kFDUp) || dp < -kFDLo) return;
+        const int b = f_bin(dp);
+        const uint32_t w = f.w1[b];
+        if ((w & 7u) == kCRec) {
+            FullRec &rc = f.u.rec[(w >> 3) & kNoRec];
+            if (y >= rc.up) atomicAdd(&rc.hi, 1u);
+            else if (y >= rc.thr) atomicAdd(&rc.tie, 1u);
+        } else if (w & kW1Listed) {
+            const uint32_t slot = atomicAdd(&f.sege[b], 1u);
+            if (slot < lsz) stg(gl + slot, f_entry(y, (uint32_t)i));
+        }
+    };
+    if (t_one) row_for_each(row, V, true, visit2);
+    else row_for_each(row, V, true, [&](int i, float x) { visit2(i, x / T); });
+    __syncthreads();
+    if (has_pen) {
+        // the raw values of penalized ids leave: listed entries are zeroed,
+        // counted ones uncounted; then the penalized values are visited
+        for (int s = t; s < kHashSlots; s += kThreads) {
+            const uint32_t id = sm.hkey[s];
+            if (id == kEmpty) continue;
+            const float y = ydiv(ldg(row + id));
+            const float dp = y - m0;
+            if (!(dp <= kFDUp) || dp < -kFDLo) continue;
+            const int b = f_bin(dp);
+            const uint32_t w = f.w1[b];
+            if (w & kW1Listed) {
+                for (uint32_t p = f.seg[b]; p < f.sege[b]; p++)
+                    if (ldg(gl + p) != 0ull && f_entry_id(ldg(gl + p)) == id) stg(gl + p, (uint64_t)0);
+            } else if ((w & 7u) == kCRec) {
+                FullRec &rc = f.u.rec[(w >> 3) & kNoRec];
+                if (y >= rc.up) atomicSub(&rc.hi, 1u);
+                else if (y >= rc.thr) atomicSub(&rc.tie, 1u);
+            }
+        }
+        __threadfence_block();
+        __syncthreads();
+        for (int s = t; s < kHashSlots; s += kThreads)
+            if (sm.hkey[s] != kEmpty) visit2((int)sm.hkey[s], pen_y(s));
+        __threadfence_block();
+        __syncthreads();
+    }
+    GS_STAMP(12);
+    int nov = 0;
+    for (int j = 0; j < nover; j++) nov += ldg(gl + j) != 0ull;
+    f_bags(sm, gl, c, 1, 1.0f);
+    if (f.fail) F_FAIL();
+    GS_STAMP(13);
+
+    // ---- walk seq 1: S (src/sampler.rs:54) -----------------------------------
+    int N = f_items(sm, gl, items1, isz, kFBins, nov, [&](int b) { return (f.w1[b] & 7u) == kCLst; },
+                    [&](int b) {
+                        int eb;
+                        bool ok;
+                        const ParFn fn = f_item_fn(f, 1, b, &eb, &ok);
+                        return ok && (fn.f0 | fn.f1) != 0u;
+                    });
+    if (N < 0) F_FAIL();
+    F_STAT(0, 0);
+    F_STAT(1, 0);
+    F_STAT(2, N);
+    F_STAT(3, f.list_end);
+    GS_STAMP(14);
+    float S;
+    {
+        WArgs wa{c, 1, 1.0f, 0, 0.0f};
+        if (f_walk(sm, items1, N, wa, &S, 8) != N) F_FAIL();
+    }
+    if (!(S > 0.0f) || !isfinite(S)) F_FAIL();
+    F_STAT(11, __float_as_int(S));
+    GS_STAMP(16);
+    const FSeq c2{m, S, nuc, f.exptab};
+
+    // ---- plan B (seqs 2, 3): masses per bin, the cut and the draw; classes --
+    {
+        float *mf = reinterpret_cast<float *>(f.v3);
+        for (int b = t; b < kFBins; b += kThreads) mf[b] = 0.0f;
+        __syncthreads();
+        // exact masses of the listed-and-sorted bins, one wave per bin (a
+        // fixed order of the f32 adds, so the plan is reproducible)
+        for (int b = wave_id(); b < kFBins; b += kWaves) {
+            if ((f.w1[b] & 7u) != kCLst) continue;
+            float ms = 0.0f;
+            for (uint32_t p = f.seg[b] + lane_id(); p < f.sege[b]; p += 64) {
+                const uint64_t en = ldg(gl + p);
+                if (en) ms += glibc_expf_tab(f_entry_y(en) - m, f.exptab);
+            }
+            for (int d = 32; d > 0; d >>= 1) ms += __shfl_xor(ms, d, 64);
+            if (lane_id() == 0) mf[b] = ms;
+        }
+        double osum = 0.0;
+        for (int p = t; p < nover; p += kThreads) {
+            const uint64_t en = ldg(gl + p);
+            if (en) osum += (double)glibc_expf_tab(f_entry_y(en) - m, f.exptab);
+        }
+        double otot;
+        f_block_excl_f64(osum, &otot, sm);
+        osum = otot;
+        double mass[kPer], loc = 0.0;
+        uint32_t cn[kPer], w1[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            cn[q] = f.cnt[b];
+            w1[q] = f.w1[b];
+            mass[q] = 0.0;
+            const uint32_t cls = w1[q] & 7u;
+            if (cls == kCLst) {
+                mass[q] = (double)mf[b];
+            } else if (cls != kCNone) {
+                int eb;
+                bool ok;
+                const ParFn fn = f_item_fn(f, 1, b, &eb, &ok);
+                mass[q] = ldexp(0.5 * ((double)fn.f0 + (double)fn.f1), eb - 23);
+            }
+            loc += mass[q];
+        }
+        double tot;
+        const double pre = f_block_excl_f64(loc, &tot, sm) + osum;   // (barriers: masses and records read)
+        tot += osum;
+        const double iS = 1.0 / (double)S;
+        if (t == 0) { f.cutb = kFBins; f.nrec = 0; f.last2 = -1; f.last3 = -1; }
+        __syncthreads();
+        if (nuc) {
+            if (tot * iS < (double)top_p * (1.0 + 2.0 * kFDelta)) F_FAIL();   // the cut may not happen
+            double lo = pre;
+#pragma unroll
+            for (int q = 0; q < kPer; q++) {
+                const double hi = lo + mass[q];
+                if (cn[q] && hi * iS * dh >= (double)top_p) { atomicMin(&f.cutb, kPer * t + q); break; }
+                lo = hi;
+            }
+        }
+        __syncthreads();
+        float s2lo = 1.0f, s2hi = 1.0f;
+        if (nuc) {
+            // s2 = the nucleus sum at the cut: >= top_p, and above it by at
+            // most the cut element's summand (<= the largest of the cut bin,
+            // or of the overflow when that may already reach top_p) plus a
+            // rounding step
+            const double vmax = osum * iS * dh >= (double)top_p ? iS : e_at((double)f.cutb) * 1.001 * iS;
+            s2lo = top_p;
+            s2hi = __double2float_ru((double)top_p + vmax + ldexp((double)top_p, -22));
+        }
+        // the predicted sums before / after each bin go through LDS (w23, v3:
+        // every thread has read the masses)
+        {
+            double lo = pre;
+#pragma unroll
+            for (int q = 0; q < kPer; q++) {
+                const int b = kPer * t + q;
+                f.w23[b] = __float_as_uint((float)lo);
+                lo += mass[q];
+                f.v3[b] = __float_as_uint((float)lo);
+            }
+        }
+        int l23 = -1;
+#pragma unroll 1
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            const double lo = (double)__uint_as_float(f.w23[b]), hi = (double)__uint_as_float(f.v3[b]);
+            const uint32_t n = f.cnt[b];
+            const double c2lo = lo * iS, c2hi = hi * iS;
+            const bool rel2 = nuc && n && c2lo * dl < (double)top_p;
+            // seq 3 over the whole range of s2: the lowest sum before the bin
+            // and the highest after it
+            const double c3lo = c2lo / (double)s2hi, c3hi = c2hi / (double)s2lo;
+            const bool rel3 = n && (nuc ? rel2 : true) && c3lo * dl <= (double)r;
+            const bool listed2 = (f.w1[b] & kW1Listed) != 0u;
+            uint32_t cl2 = kCNone, cl3 = kCNone, r2 = kNoRec, r3 = kNoRec, lvl2 = 0u, lvl3 = 0u;
+            int e2 = 0, e3 = 0;
+            float ylo = 0.0f, yhi = 0.0f;
+            if (rel2 || rel3) f_range(m0, b, &ylo, &yhi);
+            if (rel2) {
+                if (!(c2lo > 0.0) || f_dexp(c2lo * dl) != f_dexp(c2hi * dh) || c2hi * dh >= (double)top_p) {
+                    cl2 = kCLst;
+                } else {
+                    e2 = f_dexp(c2lo);
+                    float thr = 0.0f, up = 0.0f;
+                    const int k = f_classify(c2, 2, e2, ylo, yhi, 1.0f, 1.0f, &lvl2, &thr, &up);
+                    cl2 = k == 0 ? kCUni : kCBag;
+                    if (k == 1 && !listed2 && n < 65536u) {
+                        const int rr = atomicAdd(&f.nrec, 1);
+                        if (rr < kRecCap) { f.u.rec[rr] = FullRec{thr, up, 0u, 0u}; r2 = (uint32_t)rr; cl2 = kCRec; }
+                    }
+                }
+            }
+            if (rel3) {
+                if (!(c3lo > 0.0) || f_dexp(c3lo * dl) != f_dexp(c3hi * dh) || c3hi * dh > (double)r) {
+                    cl3 = kCLst;
+                } else {
+                    e3 = f_dexp(c3lo);
+                    float thr = 0.0f, up = 0.0f;
+                    const int k = f_classify(c2, 3, e3, ylo, yhi, s2lo, s2hi, &lvl3, &thr, &up);
+                    cl3 = k == 0 ? kCUni : kCBag;
+                    if (k == 1 && !listed2 && n < 65536u) {
+                        const int rr = atomicAdd(&f.nrec, 1);
+                        if (rr < kRecCap) { f.u.rec[rr] = FullRec{thr, up, 0u, 0u}; r3 = (uint32_t)rr; cl3 = kCRec; }
+                    }
+                }
+            }
+            const bool need = cl2 == kCBag || cl2 == kCLst || cl3 == kCBag || cl3 == kCLst;
+            const bool listed3 = !listed2 && need;
+            // a listed bin's elements are all in the list: bags instead of records
+            if (listed3 && cl2 == kCRec) { cl2 = kCBag; r2 = kNoRec; }
+            if (listed3 && cl3 == kCRec) { cl3 = kCBag; r3 = kNoRec; }
+            const bool visit = !listed2 && (listed3 || cl2 == kCRec || cl3 == kCRec);
+            if ((cl2 == kCLst || cl3 == kCLst) && n > (uint32_t)(16 * kThreads)) f.fail = 1;
+            f.w23[b] = cl2 | (cl3 << 3) | (r2 << 6) | (r3 << 16) | (listed3 ? kW3Listed : 0u) | (visit ? kW3Visit : 0u);
+            f.ex[b][0] = (uint8_t)(e2 + 128);
+            f.ex[b][1] = (uint8_t)(e3 + 128);
+            f.v1[b] = cl2 == kCBag ? 0u : lvl2;
+            f.v3[b] = cl3 == kCBag ? 0u : lvl3;
+            if (listed3) f.sege[b] = n;        // + the raw values of penalized ids, below
+            if (rel2 || rel3) l23 = b;
+        }
+        if (l23 >= 0) atomicMax(&f.last3, l23);
+        __syncthreads();
+        // list segments of the bins listed in pass 3 (room for raw values of
+        // penalized ids too)
+        if (has_pen) {
+            for (int s = t; s < kHashSlots; s += kThreads) {
+                const uint32_t id = sm.hkey[s];
+                if (id == kEmpty) continue;
+                const float dr = ydiv(ldg(row + id)) - m0;
+                if (dr <= kFDUp && dr >= -kFDLo) {
+                    const int b = f_bin(dr);
+                    if (f.w23[b] & kW3Listed) atomicAdd(&f.sege[b], 1u);
+                }
+            }
+        }
+        __syncthreads();
+        uint32_t capv[kPer], capl = 0;
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            capv[q] = (f.w23[b] & kW3Listed) ? f.sege[b] : 0u;
+            capl += capv[q];
+        }
+        uint32_t ltot;
+        uint32_t o = block_excl_u32(capl, &ltot, sm) + f.list_end;
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            if (capv[q]) { f.seg[b] = o; f.sege[b] = o; }
+            o += capv[q];
+        }
+        __syncthreads();
+        if (t == 0) f.list_end += ltot;
+        __syncthreads();
+        if (f.fail || f.list_end > lsz) F_FAIL();
+    }
+    GS_STAMP(17);
+
+    // ---- pass 3 (cache): seq-2 and seq-3 record counts, bins listed, seq-3
+    // deferrals ---------------------------------------------------------------
+    auto visit3 = [&](int i, float y, uint32_t flag) {
+        const float dp = y - m0;
+        if (!(dp <= kFDUp) || dp < -kFDLo) return;
+        const int b = f_bin(dp);
+        const uint32_t w = f.w23[b];
+        if (!(w & kW3Visit)) return;
+        if (w & kW3Listed) {
+            const uint32_t slot = atomicAdd(&f.sege[b], 1u);
+            if (slot < lsz) stg(gl + slot, f_entry(y, (uint32_t)i));
+            return;
+        }
+        if ((w & 7u) == kCRec) {
+            FullRec &rc = f.u.rec[(w >> 6) & kNoRec];
+            if (y >= rc.up) atomicAdd(&rc.hi, 1u);
+            else if (y >= rc.thr) atomicAdd(&rc.tie, 1u);
+        }
+        if (((w >> 3) & 7u) == kCRec) {
+            FullRec &rc = f.u.rec[(w >> 16) & kNoRec];
+            if (y >= rc.up) atomicAdd(&rc.hi, 1u);
+            else if (y >= rc.thr) {
+                if (!nuc) atomicAdd(&rc.tie, 1u);
+                else {
+                    const uint32_t slot = atomicAdd((uint32_t *)&f.ndefer, 1u);
+                    if (slot < kFDeferCap) stg(defer + slot, (uint32_t)i | flag);
+                }
+            }
+        }
+    };
+    if (t_one) row_for_each(row, V, true, [&](int i, float y) { visit3(i, y, 0u); });
+    else row_for_each(row, V, true, [&](int i, float x) { visit3(i, x / T, 0u); });
+    __syncthreads();
+    if (has_pen) {
+        for (int s = t; s < kHashSlots; s += kThreads) {
+            const uint32_t id = sm.hkey[s];
+            if (id == kEmpty) continue;
+            const float y = ydiv(ldg(row + id));
+            const float dp = y - m0;
+            if (!(dp <= kFDUp) || dp < -kFDLo) continue;
+            const int b = f_bin(dp);
+            const uint32_t w = f.w23[b];
+            if (!(w & kW3Visit)) continue;
+            if (w & kW3Listed) {
+                for (uint32_t p = f.seg[b]; p < f.sege[b]; p++)
+                    if (ldg(gl + p) != 0ull && f_entry_id(ldg(gl + p)) == id) stg(gl + p, (uint64_t)0);
+                continue;
+            }
+            if ((w & 7u) == kCRec) {
+                FullRec &rc = f.u.rec[(w >> 6) & kNoRec];
+                if (y >= rc.up) atomicSub(&rc.hi, 1u);
+                else if (y >= rc.thr) atomicSub(&rc.tie, 1u);
+            }
+            if (((w >> 3) & 7u) == kCRec) {   // a deferred raw value is skipped when the deferrals are resolved
+                FullRec &rc = f.u.rec[(w >> 16) & kNoRec];
+                if (y >= rc.up) atomicSub(&rc.hi, 1u);
+                else if (y >= rc.thr && !nuc) atomicSub(&rc.tie, 1u);
+            }
+        }
+        __threadfence_block();
+        __syncthreads();
+        for (int s = t; s < kHashSlots; s += kThreads)
+            if (sm.hkey[s] != kEmpty) visit3((int)sm.hkey[s], pen_y(s), kFPen);
+        __threadfence_block();
+        __syncthreads();
+    }
+    GS_STAMP(18);
+    if ((uint32_t)f.ndefer > kFDeferCap) F_FAIL();
+    f_bags(sm, gl, c2, 2, 1.0f);
+    if (!nuc) f_bags(sm, gl, c2, 3, 1.0f);
+    if (f.fail) F_FAIL();
+    GS_STAMP(19);
+
+    // ---- walk seq 2: the cut and s2 (src/sampler.rs:59-67) -------------------
+    const int nb23 = f.last3 + 1;
+    auto lst23 = [&](int b) {
+        const uint32_t w = f.w23[b];
+        return (w & 7u) == kCLst || ((w >> 3) & 7u) == kCLst;
+    };
+    N = f_items(sm, gl, items, isz, nb23, nov, lst23, [&](int b) {
+        const uint32_t w = f.w23[b];
+        return (w & 7u) != kCNone || ((w >> 3) & 7u) != kCNone;
+    });
+    GS_STAMP(20);
+    if (N < 0) F_FAIL();
+    F_STAT(4, N);
+    F_STAT(5, f.list_end);
+    F_STAT(6, f.ndefer);
+    F_STAT(7, f.nrec);
+    float s2 = 1.0f;
+    int n3 = N;
+    uint32_t cut_id = 0u;
+    if (nuc) {
+        WArgs wa{c2, 2, 1.0f, 1, top_p};
+        const int jc = f_walk(sm, items, N, wa, &s2, 9);
+        if (jc < 0 || jc >= N) F_FAIL();
+        cut_id = f_entry_id(ldg(items + jc));
+        n3 = jc + 1;
+        F_STAT(12, __float_as_int(s2));
+        F_STAT(13, cut_id);
+        // deferred seq-3 elements: exact increments now that s2 is exact
+        const int nd = f.ndefer;
+        for (int j = t; j < nd; j += kThreads) {
+            const uint32_t en = ldg(defer + j);
+            const uint32_t id = en & ~kFPen;
+            float y;
+            if (en & kFPen) {
+                const int hs = hash_find(sm, id);
+                if (hs < 0) { f.fail = 1; continue; }
+                y = pen_y(hs);
+            } else {
+                if (has_pen && hash_find(sm, id) >= 0) continue;   // its raw value left the row
+                y = ydiv(ldg(row + id));
+            }
+            const int b = f_bin(y - m0);
+            const uint32_t w = f.w23[b];
+            if (((w >> 3) & 7u) != kCRec) { f.fail = 1; continue; }
+            const uint32_t r3 = (w >> 16) & kNoRec;
+            const uint32_t lvl = f.v3[b];
+            uint32_t dn, up;
+            f_incs(f_val(c2, 3, y, s2), (int)f.ex[b][1] - 128, &dn, &up);
+            if (dn == lvl + 1u) atomicAdd(&f.u.rec[r3].hi, 1u);
+            else if (up == lvl + 1u) atomicAdd(&f.u.rec[r3].tie, 1u);
+            else if (dn != lvl || up != lvl) f.fail = 1;
+        }
+        __syncthreads();
+        f_bags(sm, gl, c2, 3, s2);
+        if (f.fail) F_FAIL();
+    }
+    GS_STAMP(21);
+
+    // ---- walk seq 3: the draw (src/sampler.rs:71-78) ---------------------------
+    {
+        WArgs wa{c2, 3, s2, 2, r};
+        float c3;
+        const int jd = f_walk(sm, items, n3, wa, &c3, 10);
+        if (jd < 0) F_FAIL();
+        if (jd < n3) *tok = (int)f_entry_id(ldg(items + jd));
+        else if (nuc) *tok = (int)cut_id;
+        else F_FAIL();   // the last element of the whole order: sort path
+    }
+    GS_STAMP(22);
+    return true;
+}

@@ -1,0 +1,84 @@
+// gs_full_smem.hpp -- LDS layout of the exact full-vocabulary path (gs_full.hpp).
+#pragma once
+#include <stdint.h>
+#include "gs_block.hpp"
+
+namespace gs {
+
+constexpr int kFBins = 4096;        // bins of d' = y - m0 over [-18.5, 3]
+constexpr int kFOverCap = 256;      // elements above the bin range (d' > 3)
+constexpr int kFMassBins = 1143;    // top bins whose mass pass 1 accumulates exactly
+constexpr int kRecCap = 1023;       // threshold records per pass (10-bit index, 1023 = none)
+constexpr uint32_t kNoRec = 0x3ffu;
+constexpr int kTieCap = 64;         // rounding ties inside bag bins, per accumulation
+constexpr int kWSeg = 64;           // walk: binade segments resolved per round
+
+// Bin classes of one accumulation (see gs_full.hpp).
+enum : uint32_t { kCNone = 0, kCUni = 1, kCRec = 2, kCBag = 3, kCLst = 4 };
+
+// A bin whose summands take two integer increments (lvl and lvl + 1):
+// elements with y >= up add lvl + 1, elements with thr <= y < up are rounding
+// ties, the rest add lvl.  Pass counters: hi (y >= up), tie.  For the seq-3
+// records of a nucleus row (s2 known only to a range) thr / up bound the
+// elements whose increment the range leaves open (deferred).
+struct FullRec {
+    float thr, up;
+    uint32_t hi, tie;
+};
+// A rounding tie inside a bag bin, and the increment function of a bag bin
+// that holds ties.
+struct FullTie {
+    uint64_t en;
+    uint32_t key;     // bin | accumulation << 16
+    uint32_t k;       // the lower of the two increments
+};
+struct FullTieFn {
+    uint32_t key;
+    uint32_t f0, f1;
+};
+
+struct FullSmem {
+    uint32_t cnt[kFBins];   // exact element count per bin (penalized values moved)
+    uint32_t seg[kFBins];   // list segment start of a listed bin
+    uint32_t sege[kFBins];  // list cursor of a listed bin: its segment's end after the pass
+    // seq 1: bits 0-2 class, 3-12 record, 13 listed in pass 2, 14 increment
+    // function in the tie table, 16-23 grid exponent + 128
+    uint32_t w1[kFBins];
+    // seqs 2/3: bits 0-2 class of seq 2, 3-5 class of seq 3, 6-15 seq-2
+    // record, 16-25 seq-3 record, 26 listed in pass 3, 27 visited by pass 3,
+    // 28 / 29 seq-2 / seq-3 function in the tie table
+    uint32_t w23[kFBins];
+    // seq 1, then seq 2: the level of a uniform / record bin, the increment
+    // sum of a bag bin; transiently (pass 1) the raw values of penalized ids
+    // per bin and (plan B) f32 masses
+    uint32_t v1[kFBins];
+    uint32_t v3[kFBins];    // seq 3: level or increment sum
+    uint8_t ex[kFBins][2];  // grid exponents of seqs 2 and 3 + 128
+    union {
+        FullRec rec[kRecCap + 1];
+        uint64_t mass64[kFMassBins];
+    } u;
+    uint64_t over[kFOverCap];
+    FullTie ties[kTieCap];
+    FullTieFn tiefn[kTieCap];
+    int nties, ntiefn;
+    uint64_t exptab[32];
+    // walk: per binade segment of the current round
+    uint32_t sj[kWSeg + 1];     // first item
+    int se[kWSeg + 1];          // grid exponent
+    uint32_t sF0[kWSeg + 1], sF1[kWSeg + 1];   // increments before the crossing item (last of the segment)
+    float sv[kWSeg + 1];        // the crossing item's summand
+    uint32_t sM[kWSeg + 1];     // the sum at the segment's start, in grid units
+    float ss[kWSeg + 1];        // the sum at the segment's start
+    ParFn wtot[kWaves];         // segmented scan: per-wave totals
+    uint32_t wst[kWaves];
+    uint32_t nbF0[kWaves], nbF1[kWaves], nbb[kWaves];   // each wave's last item, for the next wave
+    float nbv[kWaves];
+    int wfail, wfkind, wev, nseg, round_end;
+    float wfs, wevs, wends;
+    float m0, m, S;
+    int nover, nrec, fail, ndefer, cutb, last2, last3;
+    uint32_t list_end;
+};
+
+} // namespace gs

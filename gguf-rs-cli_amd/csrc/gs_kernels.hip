@@ -15,6 +15,7 @@
 #include "gs_block.hpp"
 #include "gs_kernels.hpp"
 #include "gs_bins_smem.hpp"
+#include "gs_full_smem.hpp"
 #include "gs_select.hpp"
 
 namespace gs {
@@ -72,6 +73,7 @@ struct RowSmem {
     union {
         TopkSmem tk;
         BinsSmem bn;
+        FullSmem fs;
     } x;
 };
 
@@ -1080,6 +1082,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
 }
 
 #include "gs_bins.hpp"
+#include "gs_full.hpp"
 
 // --------------------------------------------------------------------------
 // Full-vocabulary path: stable LSD radix sort of (~key, index) in scratch.
@@ -1327,7 +1330,11 @@ sample_rows_kernel(RowArgs a)
         else if (aligned && keep == V) {
             uint64_t *gl = reinterpret_cast<uint64_t *>(a.scratch + (size_t)b * a.scratch_stride);
             const uint32_t lcap = (uint32_t)(a.scratch_stride / 2);
+#ifdef GS_FULL_V1
             done = full_bins_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
+#else
+            done = full_v2_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
+#endif
         }
         if (t == 0) a.fb[b] = done ? 0 : 1;
         if (!done) return;
@@ -1437,6 +1444,18 @@ extern "C" int gs_debug_fails(int *out)
 {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_fails), sizeof(int) * 1280) == hipSuccess ? 0 : -5;
 }
+#endif
+#if defined(GS_TIMING) || defined(GS_DIAG)
+extern "C" int gs_debug_vdiag(int *out, int clear)
+{
+    if (clear) {
+        static int zeros[1024 * 16];
+        return hipMemcpyToSymbol(HIP_SYMBOL(gs::g_vdiag), zeros, sizeof(zeros)) == hipSuccess ? 0 : -5;
+    }
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_vdiag), sizeof(int) * 1024 * 16) == hipSuccess ? 0 : -5;
+}
+#endif
+#ifdef GS_TIMING
 extern "C" int gs_debug_row(unsigned row)
 {
     return hipMemcpyToSymbol(HIP_SYMBOL(gs::g_row), &row, sizeof(row)) == hipSuccess ? 0 : -5;

@@ -37,13 +37,12 @@ struct RowArgs {
 };
 
 // Per-row scratch (u32 units) of the full-vocabulary paths: the sort path
-// needs 4V; the binned path needs its element list (V + 4352 u64), the
-// deferred ids (65536 u32), the walk array (65536 f32 + 65536 u32) and the
-// per-bin element indices (V + 4352 u32).
+// needs 4V; the exact path its element list and walk items (each V plus
+// room for the overflow, the bins and penalized values, in u64) and its
+// deferred ids.
 inline size_t scratch_u32_per_row(size_t V)
 {
-    const size_t bins = 2 * (V + 4352) + 65536 + 2 * 65536 + (V + 4352 + 1);
-    return (4 * V > bins ? 4 * V : bins);
+    return 6 * V + 2 * (3 * 256 + 2 * 4096 + 6 * 2048) + 16384;
 }
 
 hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st);
