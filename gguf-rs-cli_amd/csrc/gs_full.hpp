@@ -48,6 +48,13 @@ __device__ int g_vdiag[1024 * 16];
 #define F_NOTE(k) do { } while (0)
 #define F_STAT(k, v) do { } while (0)
 #endif
+#ifdef GS_TIMING
+// sub-phase timestamps per row (< 256): 64 slots
+__device__ uint32_t g_vt[256 * 64];
+#define F_TS(k) do { if (threadIdx.x == 0 && blockIdx.x < 256) g_vt[blockIdx.x * 64 + (k)] = (uint32_t)__builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define F_TS(k) do { } while (0)
+#endif
 #define F_FAIL() do { F_NOTE(0); return false; } while (0)
 #define F_WFAIL() do { F_NOTE(1); return -1; } while (0)
 
@@ -324,7 +331,32 @@ struct WArgs {
     float s2;
     int pk;          // 0 none, 1 s >= thr, 2 thr < s
     float thr;
+    const uint32_t *c0, *c1;   // the bins' cached increment functions (f_cache_fns)
 };
+// Cache the increment functions of accumulation sq's bin items in two LDS
+// arrays: c0[b] = f0, c1[b] = f1 | (grid exponent + 64) << 25, both capped
+// at 2^24 (a bin adding that much leaves its binade anyway); a zero exponent
+// field marks a bin that is not a bin item of sq.
+__device__ void f_cache_fns(RowSmem &sm, int sq, uint32_t *c0, uint32_t *c1)
+{
+    FullSmem &f = sm.x.fs;
+    for (int b = threadIdx.x; b < kFBins; b += kThreads) {
+        int eb;
+        bool ok;
+        const ParFn fn = f_item_fn(f, sq, b, &eb, &ok);
+        ok &= eb > -64 && eb < 64;
+        c0[b] = min(fn.f0, 1u << 24);
+        c1[b] = min(fn.f1, 1u << 24) | (ok ? (uint32_t)(eb + 64) << 25 : 0u);
+    }
+    __syncthreads();
+}
+__device__ __forceinline__ ParFn w_binfn(const WArgs &wa, int b, int *eb, bool *ok)
+{
+    const uint32_t a = wa.c0[b], c = wa.c1[b];
+    *eb = (int)(c >> 25) - 64;
+    *ok = (c >> 25) != 0u;
+    return ParFn{a, c & 0x1ffffffu};
+}
 __device__ __forceinline__ bool w_pred(const WArgs &wa, float s)
 {
     return wa.pk == 1 ? s >= wa.thr : (wa.pk == 2 ? wa.thr < s : false);
@@ -336,7 +368,7 @@ __device__ __forceinline__ ParFn w_fn(const FullSmem &f, const WArgs &wa, bool b
     if (bin) {
         int eb;
         bool ok;
-        const ParFn fn = f_item_fn(f, wa.sq, __float_as_int(v), &eb, &ok);
+        const ParFn fn = w_binfn(wa, __float_as_int(v), &eb, &ok);
         *bad = !ok || (eb != e && (fn.f0 | fn.f1));
         return fn;
     }
@@ -347,6 +379,8 @@ __device__ __forceinline__ ParFn w_fn(const FullSmem &f, const WArgs &wa, bool b
 __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa, float *s_out, int slot)
 {
     int nrounds = 0;
+    const int tsb = 16 + 8 * (slot - 8);
+    F_TS(tsb + 0);
     FullSmem &f = sm.x.fs;
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     constexpr int kNone = 0x7fffffff;
@@ -358,7 +392,7 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
         if (f_is_bin(it)) {
             int eb;
             bool ok;
-            const ParFn fn = f_item_fn(f, wa.sq, (int)(uint32_t)it, &eb, &ok);
+            const ParFn fn = w_binfn(wa, (int)(uint32_t)it, &eb, &ok);
             if (!ok || fn.f0 || fn.f1) { *s_out = s; F_WFAIL(); }
         } else {
             s = f_val(wa.c, wa.sq, f_entry_y(it), wa.s2);
@@ -386,24 +420,25 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
             if (round >= kWMaxRounds) { *s_out = s; F_WFAIL(); }
             nrounds++;
             F_STAT(slot, nrounds);
+            F_TS(tsb + 1);
             // ---- predicted grid of the sum before every item: three scans ----
             int e[kWC];
             double tpre = 0.0, tot;
-            for (int it = 0; it < 4; it++) {
+            for (int it = 0; it < 3; it++) {
                 double loc = 0.0;
                 const double base = (double)s + tpre;
 #pragma unroll
                 for (int q = 0; q < kWC; q++) {
                     const int j = j0 + q;
-                    if (it == 3) e[q] = 0;
+                    if (it == 2) e[q] = 0;
                     if (j < start || j >= cend) continue;
                     const int eq = j == start ? grid_exp(s) : f_dexp(base + loc);
-                    if (it == 3) e[q] = eq;
+                    if (it == 2) e[q] = eq;
                     double cq;
                     if (isbin & (1u << q)) {
                         int eb;
                         bool ok;
-                        const ParFn fn = f_item_fn(f, wa.sq, __float_as_int(v[q]), &eb, &ok);
+                        const ParFn fn = w_binfn(wa, __float_as_int(v[q]), &eb, &ok);
                         cq = it == 0 ? ldexp(0.5 * ((double)fn.f0 + (double)fn.f1), eb - 23)
                                      : ldexp((double)fn.f0, eb - 23);
                     } else if (it == 0) {
@@ -415,8 +450,9 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
                     }
                     loc += cq;
                 }
-                if (it < 3) tpre = f_block_excl_f64(loc, &tot, sm);
+                if (it < 2) tpre = f_block_excl_f64(loc, &tot, sm);
             }
+            F_TS(tsb + 2);
             // ---- segments: an item starts one if its grid differs from the item before ----
             int prev_e = __shfl_up(e[kWC - 1], 1, 64);
             if (lane == 63) sm.red_i32[w] = e[kWC - 1];
@@ -445,6 +481,7 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
                 agg = seg_op(agg, SegFn{(starts >> q) & 1u, fn});
             }
             const SegFn carry = f_block_seg_excl(agg, sm, f.wtot, f.wst);   // contains barriers
+            F_TS(tsb + 3);
             // segment table: first item and grid of each segment; for each
             // segment followed by another, the prefix before its last item
             // (the one that leaves the binade) and that item's summand
@@ -500,6 +537,7 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
             }
             if (t == 0) { f.wfail = kNone; f.wev = kNone; }
             __syncthreads();
+            F_TS(tsb + 4);
             // ---- chain the segments (one thread) ----
             if (t == 0) {
                 float cs = s;
@@ -537,6 +575,7 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
             }
             __syncthreads();
             const int nok = f.nseg, rend = f.round_end;
+            F_TS(tsb + 5);
             // ---- check every item up to rend, find the event ----
             int myfail = kNone, mykind = 0, myev = kNone;
             float myfs = 0.0f, myevs = 0.0f, mylast = 0.0f;
@@ -595,6 +634,7 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
             const float fs = f.wfs, evs = f.wevs, ends = f.wends;
             const float snext = (rend < cend && gfail == kNone) ? f.ss[nseg > (uint32_t)nused ? nused : nok] : 0.0f;
             __syncthreads();
+            F_TS(tsb + 6);
             if (gev < gfail) { *s_out = evs; return gev; }
             if (gfail != kNone) {
                 if (kind == kWFailBin) {
@@ -910,6 +950,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     auto e_at = [&](double bpos) { return exp((double)kFDUp - bpos * wbin + shift); };
     const double dl = 1.0 - kFDelta, dh = 1.0 + kFDelta;
 
+    F_TS(0);
     // ---- plan A (seq 1): the running sum before each bin, predicted from
     // the masses (top bins) and the counts times the rounded increment of the
     // bin's centre (the rest), refined twice; then each bin's class:
@@ -937,6 +978,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             if (mb[q] < 0.0) mb[q] = 0.0;
             loc += mb[q];
         }
+        F_TS(1);
         double tot;
         double pre = f_block_excl_f64(loc, &tot, sm) + osum;
         double ct[kPer];
@@ -956,6 +998,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             }
             pre = f_block_excl_f64(loc, &tot, sm) + osum;
         }
+        F_TS(2);
         // classes (records overwrite the masses: every thread has read
         // them); the predicted sums before / after each bin go through LDS
         {
@@ -968,10 +1011,11 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                 f.sege[b] = __float_as_uint((float)lo);
             }
         }
-        uint32_t capl = 0;
+        // (interleaved bins: the costly record bins spread over the threads)
+        __syncthreads();
 #pragma unroll 1
         for (int q = 0; q < kPer; q++) {
-            const int b = kPer * t + q;
+            const int b = t + q * kThreads;
             const double lo = (double)__uint_as_float(f.seg[b]), hi = (double)__uint_as_float(f.sege[b]);
             const uint32_t n = f.cnt[b];
             uint32_t cls = kCNone, rec = kNoRec, lvl = 0u;
@@ -997,8 +1041,12 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             if (cls == kCLst && cap > (uint32_t)(16 * kThreads)) f.fail = 1;
             f.v1[b] = cls == kCBag ? 0u : lvl;
             f.sege[b] = cap;
-            capl += cap;
         }
+        F_TS(3);
+        __syncthreads();
+        uint32_t capl = 0;
+#pragma unroll
+        for (int q = 0; q < kPer; q++) capl += f.sege[kPer * t + q];
         uint32_t ltot;
         uint32_t o = block_excl_u32(capl, &ltot, sm) + (uint32_t)nover;
 #pragma unroll
@@ -1084,7 +1132,8 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     GS_STAMP(14);
     float S;
     {
-        WArgs wa{c, 1, 1.0f, 0, 0.0f};
+        f_cache_fns(sm, 1, f.w23, f.v3);
+        WArgs wa{c, 1, 1.0f, 0, 0.0f, f.w23, f.v3};
         if (f_walk(sm, items1, N, wa, &S, 8) != N) F_FAIL();
     }
     if (!(S > 0.0f) || !isfinite(S)) F_FAIL();
@@ -1094,21 +1143,22 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
 
     // ---- plan B (seqs 2, 3): masses per bin, the cut and the draw; classes --
     {
-        float *mf = reinterpret_cast<float *>(f.v3);
-        for (int b = t; b < kFBins; b += kThreads) mf[b] = 0.0f;
+        // exact masses of the listed-and-sorted bins, in 2^-40 units (u64
+        // sums in w23 and v3: the same result in any order)
+        uint64_t *mf = reinterpret_cast<uint64_t *>(f.w23);
+        static_assert(offsetof(FullSmem, v3) == offsetof(FullSmem, w23) + 4 * kFBins, "w23, v3 adjacent");
+        for (int b = t; b < kFBins; b += kThreads) mf[b] = 0ull;
         __syncthreads();
-        // exact masses of the listed-and-sorted bins, one wave per bin (a
-        // fixed order of the f32 adds, so the plan is reproducible)
-        for (int b = wave_id(); b < kFBins; b += kWaves) {
-            if ((f.w1[b] & 7u) != kCLst) continue;
-            float ms = 0.0f;
-            for (uint32_t p = f.seg[b] + lane_id(); p < f.sege[b]; p += 64) {
-                const uint64_t en = ldg(gl + p);
-                if (en) ms += glibc_expf_tab(f_entry_y(en) - m, f.exptab);
-            }
-            for (int d = 32; d > 0; d >>= 1) ms += __shfl_xor(ms, d, 64);
-            if (lane_id() == 0) mf[b] = ms;
+        F_TS(5);
+        for (uint32_t p = (uint32_t)nover + t; p < f.list_end; p += kThreads) {
+            const uint64_t en = ldg(gl + p);
+            if (!en) continue;
+            const float y = f_entry_y(en);
+            const int b = f_bin(y - m0);
+            if ((f.w1[b] & 7u) == kCLst)
+                atomicAdd((unsigned long long *)&mf[b], (unsigned long long)ldexp((double)glibc_expf_tab(y - m, f.exptab), 40));
         }
+        F_TS(6);
         double osum = 0.0;
         for (int p = t; p < nover; p += kThreads) {
             const uint64_t en = ldg(gl + p);
@@ -1127,7 +1177,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             mass[q] = 0.0;
             const uint32_t cls = w1[q] & 7u;
             if (cls == kCLst) {
-                mass[q] = (double)mf[b];
+                mass[q] = ldexp((double)mf[b], -40);
             } else if (cls != kCNone) {
                 int eb;
                 bool ok;
@@ -1139,6 +1189,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
         double tot;
         const double pre = f_block_excl_f64(loc, &tot, sm) + osum;   // (barriers: masses and records read)
         tot += osum;
+        F_TS(7);
         const double iS = 1.0 / (double)S;
         if (t == 0) { f.cutb = kFBins; f.nrec = 0; f.last2 = -1; f.last3 = -1; }
         __syncthreads();
@@ -1163,6 +1214,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             s2lo = top_p;
             s2hi = __double2float_ru((double)top_p + vmax + ldexp((double)top_p, -22));
         }
+        F_TS(8);
         // the predicted sums before / after each bin go through LDS (w23, v3:
         // every thread has read the masses)
         {
@@ -1176,9 +1228,10 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             }
         }
         int l23 = -1;
+        __syncthreads();
 #pragma unroll 1
         for (int q = 0; q < kPer; q++) {
-            const int b = kPer * t + q;
+            const int b = t + q * kThreads;      // interleaved (see plan A)
             const double lo = (double)__uint_as_float(f.w23[b]), hi = (double)__uint_as_float(f.v3[b]);
             const uint32_t n = f.cnt[b];
             const double c2lo = lo * iS, c2hi = hi * iS;
@@ -1233,8 +1286,9 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             f.v1[b] = cl2 == kCBag ? 0u : lvl2;
             f.v3[b] = cl3 == kCBag ? 0u : lvl3;
             if (listed3) f.sege[b] = n;        // + the raw values of penalized ids, below
-            if (rel2 || rel3) l23 = b;
+            if (rel2 || rel3) l23 = max(l23, b);
         }
+        F_TS(9);
         if (l23 >= 0) atomicMax(&f.last3, l23);
         __syncthreads();
         // list segments of the bins listed in pass 3 (room for raw values of
@@ -1366,7 +1420,8 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     int n3 = N;
     uint32_t cut_id = 0u;
     if (nuc) {
-        WArgs wa{c2, 2, 1.0f, 1, top_p};
+        f_cache_fns(sm, 2, f.w1, f.v1);
+        WArgs wa{c2, 2, 1.0f, 1, top_p, f.w1, f.v1};
         const int jc = f_walk(sm, items, N, wa, &s2, 9);
         if (jc < 0 || jc >= N) F_FAIL();
         cut_id = f_entry_id(ldg(items + jc));
@@ -1406,7 +1461,8 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
 
     // ---- walk seq 3: the draw (src/sampler.rs:71-78) ---------------------------
     {
-        WArgs wa{c2, 3, s2, 2, r};
+        f_cache_fns(sm, 3, f.w1, f.v1);
+        WArgs wa{c2, 3, s2, 2, r, f.w1, f.v1};
         float c3;
         const int jd = f_walk(sm, items, n3, wa, &c3, 10);
         if (jd < 0) F_FAIL();

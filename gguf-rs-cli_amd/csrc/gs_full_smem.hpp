@@ -44,15 +44,18 @@ struct FullSmem {
     // seq 1: bits 0-2 class, 3-12 record, 13 listed in pass 2, 14 increment
     // function in the tie table, 16-23 grid exponent + 128
     uint32_t w1[kFBins];
+    // seq 1, then seq 2: the level of a uniform / record bin, the increment
+    // sum of a bag bin; transiently the raw values of penalized ids per bin
+    // (pass 1), walk item offsets of listed bins, a walk's cached increment
+    // functions
+    uint32_t v1[kFBins];
     // seqs 2/3: bits 0-2 class of seq 2, 3-5 class of seq 3, 6-15 seq-2
     // record, 16-25 seq-3 record, 26 listed in pass 3, 27 visited by pass 3,
     // 28 / 29 seq-2 / seq-3 function in the tie table
     uint32_t w23[kFBins];
-    // seq 1, then seq 2: the level of a uniform / record bin, the increment
-    // sum of a bag bin; transiently (pass 1) the raw values of penalized ids
-    // per bin and (plan B) f32 masses
-    uint32_t v1[kFBins];
-    uint32_t v3[kFBins];    // seq 3: level or increment sum
+    // seq 3: level or increment sum.  Before plan B, w23 and v3 (adjacent)
+    // hold walk 1's cached increment functions, then plan B's u64 masses.
+    uint32_t v3[kFBins];
     uint8_t ex[kFBins][2];  // grid exponents of seqs 2 and 3 + 128
     union {
         FullRec rec[kRecCap + 1];

@@ -1432,6 +1432,10 @@ __global__ void synth_kernel(float *out, int B, int V, size_t ld, uint64_t seed,
 } // namespace gs
 
 #ifdef GS_TIMING
+extern "C" int gs_debug_vt(uint32_t *out)
+{
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_vt), sizeof(uint32_t) * 256 * 64) == hipSuccess ? 0 : -5;
+}
 extern "C" int gs_debug_stages(uint32_t *out)
 {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_stages), sizeof(uint32_t) * 256 * 32) == hipSuccess ? 0 : -5;
