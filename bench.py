@@ -44,34 +44,60 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def bench_c3(gs, torch, steps, warmup):
+def bench_c3(gs, torch, steps, warmup, nbuf=3):
+    """The metric: C3 (B=256, V=152064, k=0, p=0.95, T=1) per step.  The
+    timed steps rotate over `nbuf` distinct copies of the batch in HBM
+    (3 x 155.7 MB, more than the 256 MB Infinity Cache), so every step
+    streams its logits from HBM rather than from a cache that still holds
+    them; the same-buffer figure is reported beside it."""
     import workloads
     w = workloads.make("c3")
     B, V = w["B"], w["V"]
-    d_lg = torch.from_numpy(w["logits"]).cuda()
+    bufs = [torch.from_numpy(w["logits"]).cuda() for _ in range(nbuf)]
     d_u = torch.from_numpy(w["u"]).cuda()
     d_tok = torch.zeros(B, dtype=torch.int32, device="cuda")
     d_st = torch.zeros(B, dtype=torch.int32, device="cuda")
     s = gs.Sampler(1.0, 0, 0.95, 1.0, seed=42)
     s.reserve(B, V)
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        s.sample_batch(d_lg, d_tok, u=d_u, status=d_st, stream=stream)
+    for i in range(warmup):
+        s.sample_batch(bufs[i % nbuf], d_tok, u=d_u, status=d_st, stream=stream)
     torch.cuda.synchronize()
     assert int((d_st != 0).sum()) == 0, "sampler reported row errors"
     sort_rows = s.fallback_rows(stream)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(steps):
-        s.sample_batch(d_lg, d_tok, u=d_u, status=d_st, stream=stream)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+
+    def timed(rotate):
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(steps):
+            s.sample_batch(bufs[i % nbuf if rotate else 0], d_tok, u=d_u, status=d_st, stream=stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(True)
+    ms_same = timed(False)
     per_row = workloads.algorithmic_bytes_per_row(V, 0)
     tokens = d_tok.cpu().numpy().astype(np.int64)
-    return dict(B=B, V=V, ms=ms, bytes=per_row * B, tokens=tokens, w=w, sort_rows=sort_rows)
+    ties = tie_rows(gs, torch, s, bufs[0], u=d_u)
+    del bufs
+    return dict(B=B, V=V, ms=ms, ms_same_buffer=ms_same, nbuf=nbuf, bytes=per_row * B, tokens=tokens, w=w,
+                sort_rows=sort_rows, tie_rows=ties)
+
+
+def tie_rows(gs, torch, s, d_lg, params=None, recent=None, recent_len=None, u=None):
+    """Rows whose result depends on the order of equal scaled logits (the
+    reference's sort_unstable_by leaves it unspecified): equal values at rank
+    k, inside the kept prefix or at the nucleus cut, from gs_sample_detail's
+    sorted rows (outside the timed region)."""
+    B = int(d_lg.shape[0])
+    tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    out = s.sample_detail(d_lg, tok, 1, params=params, recent=recent, recent_len=recent_len, u=u)
+    torch.cuda.synchronize()
+    t = out["ties"].cpu().numpy()
+    return {"tie_in_kept_prefix": int((t & 1).sum()), "token_on_tie": int((t >> 1).sum())}
 
 
 def bench_c1_latency(gs, torch, steps=256):
@@ -366,33 +392,26 @@ def bench_token_decode(gs):
 
 def bench_configs(gs, torch, reps=20):
     """The sampler alone on the survey's other configurations (parity-test
-    shapes, reported for reference): C2 (Llama-3, B=64, V=128256, W=128, k=40),
-    C4 (Gemma, B=512, V=256000, W=256, per-row params) and one step of C5
-    (B=1024, V=152064, W=1024, the on-device generator's logits).  Per batch:
-    microseconds (HIP events on the launch stream) and algorithmic GB/s."""
+    shapes, reported for reference): C2 (Llama-3, B=64, V=128256, W=128, k=40)
+    and C4 (Gemma, B=512, V=256000, W=256, per-row params): microseconds per
+    batch (HIP events on the launch stream) and algorithmic GB/s; C5 as its
+    loop (bench_c5_graph).  Each with the count of rows that take the sort
+    path and of rows holding ties that the order of equal keys decides."""
     import workloads
     out = {}
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for name in ("c2", "c4", "c5"):
+    for name in ("c2", "c4"):
         w = workloads.make(name)
         B, V, W = w["B"], w["V"], w["W"]
-        s = gs.Sampler(w.get("T", 0.7), w.get("k", 40), w.get("p", 0.9), w.get("rep", 1.1), seed=42)
+        s = gs.Sampler(0.7, 40, 0.9, 1.1, seed=42)
         s.reserve(B, V)
         tok = torch.zeros(B, dtype=torch.int32, device="cuda")
-        if name == "c5":
-            d_lg = torch.empty((B, V), dtype=torch.float32, device="cuda")
-            gs.synth_logits(d_lg, w["synth_seed"], 0, w["sigma"], stream=st)
-            d_rec = torch.from_numpy(w["window"].view(np.int32)).cuda()
-            call = lambda: s.sample_batch(d_lg, tok, recent=d_rec, stream=st)
-            hetero = False
-        else:
-            d_lg = torch.from_numpy(w["logits"]).cuda()
-            d_rec = torch.from_numpy(w["recent"].view(np.int32)).cuda() if w["recent"] is not None else None
-            d_u = torch.from_numpy(w["u"]).cuda()
-            d_pr = torch.from_numpy(np.ascontiguousarray(w["params"]).view(np.uint8)).cuda()
-            call = lambda: s.sample_batch(d_lg, tok, params=d_pr, recent=d_rec, u=d_u, stream=st)
-            hetero = name == "c4"
+        d_lg = torch.from_numpy(w["logits"]).cuda()
+        d_rec = torch.from_numpy(w["recent"].view(np.int32)).cuda() if w["recent"] is not None else None
+        d_u = torch.from_numpy(w["u"]).cuda()
+        d_pr = torch.from_numpy(np.ascontiguousarray(w["params"]).view(np.uint8)).cuda()
+        call = lambda: s.sample_batch(d_lg, tok, params=d_pr, recent=d_rec, u=d_u, stream=st)
         for _ in range(3):
             call()
         torch.cuda.synchronize()
@@ -403,13 +422,82 @@ def bench_configs(gs, torch, reps=20):
         e1.record(st)
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / reps
-        nbytes = B * workloads.algorithmic_bytes_per_row(V, W, hetero=hetero)
+        nbytes = B * workloads.algorithmic_bytes_per_row(V, W, hetero=name == "c4")
         out[name] = {"B": B, "V": V, "W": W, "us_per_batch": us, "rows_per_s": B / us * 1e6,
                      "GB_per_s": nbytes / us / 1e3, "frac_of_hbm_peak": nbytes / us / 1e3 / PEAK_HBM_GBS,
-                     "sort_path_rows": sort_rows}
+                     "sort_path_rows": sort_rows,
+                     "tie_rows": tie_rows(gs, torch, s, d_lg, params=d_pr, recent=d_rec, u=d_u)}
         log("%s: %.1f us per batch of %d rows (%.0f GB/s)" % (name, us, B, nbytes / us / 1e3))
         del d_lg
+    out["c5"] = bench_c5_graph(gs, torch)
     return out
+
+
+def bench_c5_graph(gs, torch, reps=3):
+    """C5 as specified: B = 1024 rows, V = 152064, 128 steps captured in one
+    HIP graph (the on-device generator's logits, then the decode step:
+    sample with the 1024-id ring window and commit; the rows' LCGs on the
+    device).  Per step: graph time / 128 (HIP events on the replay stream),
+    and the sampler's share (the graph time less a graph of the generator
+    alone).  Tie rows and sort-path rows from the first step's logits."""
+    import workloads
+    w = workloads.make("c5")
+    B, V, W, steps = w["B"], w["V"], w["W"], w["steps"]
+    seeds = [w["seed"] + b for b in range(B)]
+    s = gs.Sampler(w["T"], w["k"], w["p"], w["rep"], seed=1)
+    s.reserve(B, V)
+    dec = gs.Decoder(B, W=W, max_new=steps + 1, stop=())
+    d_lg = torch.empty((B, V), dtype=torch.float32, device="cuda")
+
+    def reset():
+        dec.init(s, seeds, init_recent=w["window"])
+        torch.cuda.synchronize()
+
+    reset()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream()
+        for t in range(steps):
+            gs.synth_logits(d_lg, w["synth_seed"], t * B * V, w["sigma"], stream=st)
+            dec.step(s, logits=d_lg, stream=st)
+    gg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gg):
+        st = torch.cuda.current_stream()
+        for t in range(steps):
+            gs.synth_logits(d_lg, w["synth_seed"], t * B * V, w["sigma"], stream=st)
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def run(graph):
+        times = []
+        for _ in range(reps):
+            reset()
+            e0.record(st)
+            graph.replay()
+            e1.record(st)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / steps)
+        return float(np.median(times))
+
+    us_step = run(g)
+    us_gen = run(gg)
+    done = int((dec.row_state()["done"] != gs.DONE_RUNNING).sum())
+    # the first step's logits: sort-path rows and tie rows
+    gs.synth_logits(d_lg, w["synth_seed"], 0, w["sigma"], stream=st)
+    tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    reset()
+    s.sample_batch(d_lg, tok, recent=dec.window, recent_len=dec.window_len, u=dec.u, stream=st)
+    sort_rows = s.fallback_rows(st)
+    ties = tie_rows(gs, torch, s, d_lg, recent=dec.window, recent_len=dec.window_len, u=dec.u)
+    us_sampler = us_step - us_gen
+    nbytes = B * workloads.algorithmic_bytes_per_row(V, W, window_append=True)
+    log("c5: %.1f us per step in a %d-step graph (generator %.1f us)" % (us_step, steps, us_gen))
+    del d_lg
+    return {"B": B, "V": V, "W": W, "steps_per_graph": steps, "us_per_step_graph": us_step,
+            "us_generator_per_step": us_gen, "us_sampler_per_step": us_sampler,
+            "rows_per_s": B / us_sampler * 1e6, "GB_per_s": nbytes / us_sampler / 1e3,
+            "frac_of_hbm_peak": nbytes / us_sampler / 1e3 / PEAK_HBM_GBS, "rows_ended": done,
+            "sort_path_rows": sort_rows, "tie_rows": ties}
 
 
 def calib_copy(torch, nbytes=1 << 30, reps=5):
@@ -521,10 +609,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded numpy N(0,2^2) logits resident in HBM)",
+        "data": "synthetic (seeded numpy N(0,2^2) logits resident in HBM); the timed steps rotate over "
+                "%d copies (%.0f MB, beyond the 256 MB Infinity Cache)" % (c3["nbuf"], c3["nbuf"] * c3["bytes"] / 1e6),
+        "ms_per_step_same_buffer": c3["ms_same_buffer"],
         "config": {"workload": "c3 Qwen2.5 V=152064 B=256 top_k=0 top_p=0.95 T=1.0 rep=1.0",
                    "global_batch": c3["B"], "vocab": c3["V"], "parallelism": "none (1 GPU)",
-                   "sort_path_rows": c3["sort_rows"]},
+                   "sort_path_rows": c3["sort_rows"], "tie_rows": c3["tie_rows"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": profiled_traffic(),
                      "kernel": "gs::sample_rows_kernel", "bytes_per_launch": c3["bytes"]},

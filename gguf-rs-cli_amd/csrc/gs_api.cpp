@@ -49,6 +49,17 @@ struct gs_sampler {
 namespace gs { int init_static_scratch(int device); }
 
 namespace {
+// Is `stream` being captured into a HIP graph?
+int capturing(hipStream_t stream, bool *cap)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) { (void)hipGetLastError(); return GS_ERR_HIP; }
+    *cap = cs != hipStreamCaptureStatusNone;
+    return GS_OK;
+}
+} // namespace
+
+namespace {
 
 // Device pointer test with a one-allocation cache: consecutive rows of one
 // device tensor skip the runtime query.
@@ -353,6 +364,77 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
     return GS_OK;
 }
 
+int gs_sample_mut(gs_sampler *s, float *logits, size_t V, const uint32_t *recent, size_t W, uint32_t *out_token)
+{
+    int rc = gs_sample(s, logits, V, recent, W, out_token);
+    if (rc != GS_OK || V == 0) return rc;
+    // gs_sample left the row on the device (the caller's buffer or the
+    // staging copy) and a host window in the mapped buffer
+    const bool dev_row = is_device_ptr(s, logits);
+    float *d_row = dev_row ? logits : s->d_row;
+    const uint32_t *d_rec = (W > 0 && !is_device_ptr(s, recent)) ? s->d_rec_map : recent;
+    if (gs::launch_writeback(d_row, 1, (int)V, V, nullptr, s->params, W ? d_rec : nullptr, W, nullptr, (int)W,
+                             s->stream) != hipSuccess)
+        return GS_ERR_HIP;
+    if (!dev_row &&
+        hipMemcpyAsync(logits, d_row, V * sizeof(float), hipMemcpyDeviceToHost, s->stream) != hipSuccess)
+        return GS_ERR_HIP;
+    return hipStreamSynchronize(s->stream) == hipSuccess ? GS_OK : GS_ERR_HIP;
+}
+
+int gs_sample_detail(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld, const gs_params *d_params,
+                     const uint32_t *d_recent, size_t ld_recent, const uint32_t *d_recent_len, size_t W,
+                     const float *d_u, uint32_t *d_tokens, int32_t *d_status, const gs_detail *det, void *stream)
+{
+    if (!s || !d_tokens || !det || (B > 0 && V > 0 && !d_logits) || ld < V) return GS_ERR_INVALID;
+    if (d_recent && ld_recent < W) return GS_ERR_INVALID;
+    if (!d_u && d_params) return GS_ERR_INVALID;
+    if ((det->ids || det->p) && det->cap == 0) return GS_ERR_INVALID;
+    if (V > GS_MAX_VOCAB || B > 0x7fffffff) return GS_ERR_UNSUPPORTED;
+    if (d_recent && W > (size_t)gs::kMaxWindow) return GS_ERR_UNSUPPORTED;
+    s->fb_rows = 0;
+    if (B == 0) return GS_OK;
+    int rc;
+    bool cap = false;
+    if ((rc = capturing((hipStream_t)stream, &cap))) return rc;
+    if (cap) return GS_ERR_UNSUPPORTED;   // a diagnostic: not for graphs
+    if ((rc = reserve_scratch(s, B, V))) return rc;
+    gs::RowArgs a;
+    memset(&a, 0, sizeof(a));
+    a.logits = d_logits;
+    a.ld = ld;
+    a.V = (int)V;
+    a.params = d_params;
+    a.uparams = s->params;
+    a.recent = d_recent;
+    a.ld_recent = ld_recent;
+    a.recent_len = d_recent_len;
+    a.W = d_recent ? (int)W : 0;
+    a.u = d_u;
+    a.lcg_state = s->state;
+    a.tokens = d_tokens;
+    a.status = d_status;
+    a.scratch = s->scratch;
+    a.scratch_stride = gs::scratch_u32_per_row(V);
+    a.det = *det;
+    if (gs::launch_detail_rows(a, (int)B, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+    if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
+    return GS_OK;
+}
+
+int gs_logits_writeback(gs_sampler *s, float *d_logits, size_t B, size_t V, size_t ld, const gs_params *d_params,
+                        const uint32_t *d_recent, size_t ld_recent, const uint32_t *d_recent_len, size_t W,
+                        void *stream)
+{
+    if (!s || (B > 0 && V > 0 && !d_logits) || ld < V) return GS_ERR_INVALID;
+    if (d_recent && ld_recent < W) return GS_ERR_INVALID;
+    if (V > GS_MAX_VOCAB || B > 65535) return GS_ERR_UNSUPPORTED;
+    if (B == 0 || V == 0) return GS_OK;
+    return gs::launch_writeback(d_logits, (int)B, (int)V, ld, d_params, s->params, d_recent, ld_recent,
+                                d_recent_len, d_recent ? (int)W : 0, (hipStream_t)stream) == hipSuccess
+               ? GS_OK : GS_ERR_HIP;
+}
+
 int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_t ld,
                     const gs_params *d_params, const uint32_t *d_recent, size_t ld_recent,
                     const uint32_t *d_recent_len, size_t W, const float *d_u,
@@ -367,15 +449,6 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, si
 namespace gs {
 
 namespace {
-
-// Is `stream` being captured into a HIP graph?
-int capturing(hipStream_t stream, bool *cap)
-{
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) { (void)hipGetLastError(); return GS_ERR_HIP; }
-    *cap = cs != hipStreamCaptureStatusNone;
-    return GS_OK;
-}
 
 // Device buffers of one batched call.  `fixed` buffers come from the caller
 // (the static scratch of gs_sample_batch_noalloc) and never grow.

@@ -1087,9 +1087,63 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
 // --------------------------------------------------------------------------
 // Full-vocabulary path: stable LSD radix sort of (~key, index) in scratch.
 // ~key ascending == key descending; stability keeps equal keys in index order.
+// finish_sorted's result over the sorted row, plus the detail outputs
+// (gs_detail): the kept ids, a_j / S, n, the cut, S, s2 and the tie flag.
+// kA holds the sorted keys (complemented), for the tie test.
+template <typename YV, typename IX>
+__device__ int finish_detail(RowSmem &sm, int n, int V, YV yv, IX idx, const uint32_t *kA, float top_p, float r,
+                             const gs_detail &d, int b)
+{
+    const int t = threadIdx.x;
+    const float m = yv(0);
+    auto e_of = [&](int j) { return glibc_expf(yv(j) - m); };
+    float sum = NAN;
+    if (!isinf(m)) block_seqsum(e_of, n, 0.0f, [](float) { return false; }, &sum, sm.seq);
+    auto p_of = [&](int j) { return e_of(j) / sum; };
+    const size_t cap = d.cap;
+    for (int j = t; j < n && (size_t)j < cap; j += kThreads) {
+        if (d.ids) d.ids[(size_t)b * cap + j] = idx(j);
+        if (d.p) d.p[(size_t)b * cap + j] = p_of(j);
+    }
+    int cut = n, pos;
+    float s2 = 1.0f;
+    if (isinf(m)) {
+        // every probability is NaN: no cut, no draw succeeds (src/sampler.rs:64, 76)
+        s2 = NAN;
+        pos = n - 1;
+    } else if (top_p < 1.0f) {
+        int stop = block_seqsum(p_of, n, 0.0f, [top_p](float c) { return c >= top_p; }, &s2, sm.seq);
+        cut = stop < n ? stop + 1 : n;   // s2: the sum through the cut, or of every p (src/sampler.rs:67)
+        auto q_of = [&](int j) { return p_of(j) / s2; };
+        float c;
+        int pick = block_seqsum(q_of, cut, 0.0f, [r](float cc) { return r < cc; }, &c, sm.seq);
+        pos = pick < cut ? pick : cut - 1;
+    } else {
+        float c;
+        int pick = block_seqsum(p_of, n, 0.0f, [r](float cc) { return r < cc; }, &c, sm.seq);
+        pos = pick < n ? pick : n - 1;
+    }
+    const int tok = (int)idx(pos);
+    // bit 0: equal keys meet inside [0, cut] or at the truncation boundary;
+    // bit 1: the drawn element's key is shared (the token depends on the
+    // order of equal keys; the sums never do: equal summands commute)
+    int tie = 0;
+    for (int j = t; j < cut && j + 1 < V; j += kThreads) tie |= (int)(kA[j] == kA[j + 1]);
+    if (t == 0 && n < V) tie |= (int)(kA[n - 1] == kA[n]);
+    if (t == 0 && ((pos > 0 && kA[pos - 1] == kA[pos]) || (pos + 1 < V && kA[pos + 1] == kA[pos]))) tie |= 2;
+    tie = block_or(tie & 1, sm) | (block_or(tie >> 1, sm) << 1);
+    if (t == 0) {
+        if (d.n_kept) d.n_kept[b] = (uint32_t)n;
+        if (d.cut) d.cut[b] = (uint32_t)cut;
+        if (d.sums) { d.sums[2 * b] = sum; d.sums[2 * b + 1] = s2; }
+        if (d.ties) d.ties[b] = (uint32_t)tie;
+    }
+    return tok;
+}
+
 __device__ int full_row(RowSmem &sm, const float *row, int V, int keep, float T, float top_p,
                         bool has_pen, float r, uint32_t *kA, uint32_t *iA, uint32_t *kB,
-                        uint32_t *iB, int *status)
+                        uint32_t *iB, int *status, const gs_detail *det = nullptr)
 {
     const int t = threadIdx.x;
     int nan = 0;
@@ -1179,6 +1233,7 @@ __device__ int full_row(RowSmem &sm, const float *row, int V, int keep, float T,
     auto yv = [&](int j) { return key2f(~kA[j]); };
     auto ix = [&](int j) { return iA[j]; };
     *status = GS_OK;
+    if (det) return finish_detail(sm, keep, V, yv, ix, kA, top_p, r, *det, blockIdx.x);
     return finish_sorted(sm, keep, yv, ix, top_p, r);
 }
 
@@ -1211,7 +1266,7 @@ __device__ __forceinline__ bool is_full_path(const gs_params &p, int V)
     return !(keep < V && keep <= kMaxTopK);
 }
 
-enum { kModeSmall = 0, kModeBins = 1, kModeSort = 2 };
+enum { kModeSmall = 0, kModeBins = 1, kModeSort = 2, kModeDetail = 3 };
 
 template <int MODE>
 __global__ void __launch_bounds__(kThreads)
@@ -1222,9 +1277,16 @@ sample_rows_kernel(RowArgs a)
     const int t = threadIdx.x;
     const int V = a.V;
     const gs_params p = a.params ? a.params[b] : a.uparams;
-    const bool full = is_full_path(p, V);
+    // the detail kernel sorts every row with T > 0 (the rest: the small path)
+    const bool sorted_row = MODE == kModeDetail && p.temperature > 0.0f && V >= 2;
+    const bool full = MODE == kModeDetail ? sorted_row : is_full_path(p, V);
+    if (MODE == kModeDetail && !sorted_row && t == 0) {
+        if (a.det.n_kept) a.det.n_kept[b] = 0u;
+        if (a.det.cut) a.det.cut[b] = 0u;
+        if (a.det.ties) a.det.ties[b] = 0u;
+    }
     if (MODE == kModeSmall && full) return;
-    if (MODE != kModeSmall && !full) {
+    if (MODE != kModeSmall && MODE != kModeDetail && !full) {
         if (MODE == kModeBins && t == 0 && a.fb != nullptr) a.fb[b] = 0;
         return;
     }
@@ -1291,7 +1353,7 @@ sample_rows_kernel(RowArgs a)
     const bool aligned = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
     const int keep = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
 
-    if (MODE == kModeSmall) {
+    if (MODE == kModeSmall || (MODE == kModeDetail && !sorted_row)) {
         if (V == 0) {
             tok = 0;
             status = p.temperature > 0.0f ? GS_ERR_EMPTY : GS_OK;
@@ -1344,7 +1406,12 @@ sample_rows_kernel(RowArgs a)
             const size_t off = (size_t)b * a.scratch_stride;
             tok = full_row(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, a.scratch + off,
                            a.scratch + off + V, a.scratch + off + 2 * (size_t)V,
-                           a.scratch + off + 3 * (size_t)V, &status);
+                           a.scratch + off + 3 * (size_t)V, &status, MODE == kModeDetail ? &a.det : nullptr);
+        }
+        if (MODE == kModeDetail && status != GS_OK && t == 0) {
+            if (a.det.n_kept) a.det.n_kept[b] = 0u;
+            if (a.det.cut) a.det.cut[b] = 0u;
+            if (a.det.ties) a.det.ties[b] = 0u;
         }
     }
     GS_STAMP(8 * MODE + 7);
@@ -1418,6 +1485,44 @@ __global__ void window_push_kernel(uint32_t *win, int B, size_t ld, int W, size_
 {
     int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b < B) win[(size_t)b * ld + (pos % (size_t)W)] = tok[b];
+}
+
+// What src/sampler.rs:37 and :41 leave in the caller's logits: each id of the
+// row's window penalized once per occurrence (apply_rep_penalty, :23-30),
+// then every logit divided by T when T > 0 (a row with T <= 0 returns from
+// greedy before the division, :39).  Grid: (chunks of kMutChunk logits, B).
+constexpr int kMutChunk = 4096;
+__global__ void __launch_bounds__(256)
+writeback_kernel(float *logits, size_t ld, int V, const gs_params *params, gs_params up,
+                 const uint32_t *recent, size_t ld_recent, const uint32_t *recent_len, int W)
+{
+    __shared__ uint32_t cnt[kMutChunk];
+    const int b = blockIdx.y;
+    const int base = blockIdx.x * kMutChunk;
+    const int n = min(kMutChunk, V - base);
+    const gs_params p = params ? params[b] : up;
+    const bool pen = recent != nullptr && p.rep_penalty != 1.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) cnt[i] = 0u;
+    __syncthreads();
+    if (pen) {
+        int w = recent_len ? (int)recent_len[b] : W;
+        if (w > W) w = W;
+        const uint32_t *rec = recent + (size_t)b * ld_recent;
+        for (int j = threadIdx.x; j < w; j += blockDim.x) {
+            const uint32_t id = rec[j];
+            if (id >= (uint32_t)base && id < (uint32_t)(base + n)) atomicAdd(&cnt[id - base], 1u);
+        }
+    }
+    __syncthreads();
+    const bool div = !(p.temperature <= 0.0f);
+    float *row = logits + (size_t)b * ld + base;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float l = row[i];
+        const uint32_t c = cnt[i];
+        if (c) l = penalize(l, c, p.rep_penalty);
+        if (div) l = l / p.temperature;
+        row[i] = l;
+    }
 }
 
 __global__ void synth_kernel(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0, float sigma)
@@ -1553,6 +1658,11 @@ hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hi
     }
     return hipGetLastError();
 }
+hipError_t launch_detail_rows(const RowArgs &a, int B, hipStream_t st)
+{
+    hipLaunchKernelGGL(sample_rows_kernel<kModeDetail>, dim3(B), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
 hipError_t launch_reg_row(const RowArgs &a, hipStream_t st)
 {
     hipLaunchKernelGGL(reg_row_kernel, dim3(1), dim3(kThreads), 0, st, a);
@@ -1591,6 +1701,15 @@ hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos
                               const uint32_t *tok, hipStream_t st)
 {
     hipLaunchKernelGGL(window_push_kernel, dim3((B + 255) / 256), dim3(256), 0, st, win, B, ld, W, pos, tok);
+    return hipGetLastError();
+}
+hipError_t launch_writeback(float *logits, int B, int V, size_t ld, const gs_params *params, const gs_params &up,
+                           const uint32_t *recent, size_t ld_recent, const uint32_t *recent_len, int W,
+                           hipStream_t st)
+{
+    const int chunks = (V + kMutChunk - 1) / kMutChunk;
+    hipLaunchKernelGGL(writeback_kernel, dim3(chunks, B), dim3(256), 0, st, logits, ld, V, params, up, recent,
+                       ld_recent, recent_len, W);
     return hipGetLastError();
 }
 hipError_t launch_synth(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0, float sigma,

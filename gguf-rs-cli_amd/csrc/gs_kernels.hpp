@@ -34,6 +34,7 @@ struct RowArgs {
     DecodeHook hook;               // decode step: the kernel that stores a row's token commits it
     int kwin_n;                    // single-row calls: a host window of W <= kKernWin ids passed
     uint32_t kwin[kKernWin];       // by value here (used instead of `recent` when kwin_n != 0)
+    gs_detail det;                 // diagnostic outputs of the detail kernel (gs_sample_detail)
 };
 
 // Per-row scratch (u32 units) of the full-vocabulary paths: the sort path
@@ -46,6 +47,8 @@ inline size_t scratch_u32_per_row(size_t V)
 }
 
 hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st);
+// Every row sorted (diagnostic; fills a.det); scratch as the sort path.
+hipError_t launch_detail_rows(const RowArgs &a, int B, hipStream_t st);
 // Single-row register path (B = 1); rows it cannot finish report kStatusRetryHost.
 constexpr int kStatusRetryHost = 0x7f;
 bool reg_row_fits(const gs_params &p, size_t V, const void *row);
@@ -71,6 +74,10 @@ int sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V, size_
                  const float *d_u, uint32_t *d_tokens, int32_t *d_status, const DecodeHook *hook, void *stream);
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st);
+// The caller-visible mutation of src/sampler.rs:37,41 (penalty, then / T when T > 0).
+hipError_t launch_writeback(float *logits, int B, int V, size_t ld, const gs_params *params, const gs_params &up,
+                           const uint32_t *recent, size_t ld_recent, const uint32_t *recent_len, int W,
+                           hipStream_t st);
 hipError_t launch_synth(float *out, int B, int V, size_t ld, uint64_t seed, uint64_t c0,
                         float sigma, hipStream_t st);
 

@@ -41,7 +41,7 @@ _ERRNAMES = {
 EXPORTS = [
     "gs_sampler_create", "gs_sampler_destroy", "gs_sampler_set_params",
     "gs_sampler_set_seed", "gs_sampler_get_state", "gs_sampler_set_state",
-    "gs_sampler_reserve", "gs_sample", "gs_sample_batch", "gs_sample_batch_noalloc", "gs_window_push",
+    "gs_sampler_reserve", "gs_sample", "gs_sample_mut", "gs_logits_writeback", "gs_sample_detail", "gs_sample_batch", "gs_sample_batch_noalloc", "gs_window_push",
     "gs_synth_logits", "gs_limits", "gs_version",
     # include/gs_gemv.h
     "gs_qmatrix_upload", "gs_qmatrix_destroy", "gs_qmatrix_shape", "gs_gemv",
@@ -62,6 +62,13 @@ class SamplerError(RuntimeError):
 class GsParams(ctypes.Structure):
     _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_uint32),
                 ("top_p", ctypes.c_float), ("rep_penalty", ctypes.c_float)]
+
+
+class GsDetail(ctypes.Structure):
+    """gs_detail (include/gs_sampler.h)."""
+    _fields_ = [("ids", ctypes.c_void_p), ("p", ctypes.c_void_p), ("cap", ctypes.c_size_t),
+                ("n_kept", ctypes.c_void_p), ("cut", ctypes.c_void_p), ("sums", ctypes.c_void_p),
+                ("ties", ctypes.c_void_p)]
 
 
 class DecodeCtx(ctypes.Structure):
@@ -95,6 +102,9 @@ def load_library(path=LIB_PATH):
         "gs_sampler_set_state": ([P, U64], I),
         "gs_sampler_reserve": ([P, SZ, SZ], I),
         "gs_sample": ([P, P, SZ, P, SZ, ctypes.POINTER(ctypes.c_uint32)], I),
+        "gs_sample_mut": ([P, P, SZ, P, SZ, ctypes.POINTER(ctypes.c_uint32)], I),
+        "gs_logits_writeback": ([P, P, SZ, SZ, SZ, P, P, SZ, P, SZ, P], I),
+        "gs_sample_detail": ([P, P, SZ, SZ, SZ, P, P, SZ, P, SZ, P, P, P, ctypes.POINTER(GsDetail), P], I),
         "gs_sample_batch": ([P, P, SZ, SZ, SZ, P, P, SZ, P, SZ, P, P, P, P], I),
         "gs_sample_batch_noalloc": ([P, P, SZ, SZ, SZ, P, P, SZ, P, SZ, P, P, P, P], I),
         "gs_window_push": ([P, SZ, SZ, SZ, SZ, P, P], I),
@@ -275,6 +285,80 @@ class Sampler:
                                    ctypes.byref(out)), "gs_sample")
         return int(out.value)
 
+    def sample_mut(self, logits, recent=()):
+        """sample(&mut logits, ...) as the reference takes it: returns the
+        token and leaves `logits` (a contiguous numpy f32 array, or a torch
+        f32 tensor on the host or the device) penalized and divided by T
+        (src/sampler.rs:37,41), in place."""
+        import numpy as np
+        if isinstance(logits, np.ndarray):
+            if logits.dtype != np.float32 or not logits.flags.c_contiguous or not logits.flags.writeable:
+                raise TypeError("logits must be a writeable contiguous float32 array")
+        elif hasattr(logits, "data_ptr"):
+            if str(logits.dtype) != "torch.float32" or not logits.is_contiguous():
+                raise TypeError("logits must be a contiguous float32 tensor")
+            if logits.is_cuda:
+                import torch
+                torch.cuda.current_stream(logits.device).synchronize()
+        else:
+            raise TypeError("logits must be a numpy array or a torch tensor (mutated in place)")
+        V = int(logits.numel() if hasattr(logits, "numel") else logits.size)
+        if recent is None or (not hasattr(recent, "data_ptr") and not hasattr(recent, "ctypes")):
+            recent = np.ascontiguousarray(np.asarray(list(recent or ()), dtype=np.uint32))
+        elif isinstance(recent, np.ndarray):
+            recent = np.ascontiguousarray(recent.astype(np.uint32, copy=False))
+        W = int(recent.numel() if hasattr(recent, "numel") else recent.size)
+        out = ctypes.c_uint32()
+        _check(self._lib.gs_sample_mut(self._h, _ptr(logits), V, _ptr(recent) if W else None, W,
+                                       ctypes.byref(out)), "gs_sample_mut")
+        return int(out.value)
+
+    def logits_writeback(self, logits, params=None, recent=None, recent_len=None, stream=None,
+                         V=None, ld=None, W=None, ld_recent=None):
+        """Batched write-back of the reference's mutation (penalty, then / T)
+        into device rows `logits` [B, ld]; stream-ordered, after
+        sample_batch on the same rows."""
+        B = int(logits.shape[0])
+        V = int(logits.shape[1]) if V is None else V
+        ld = (int(logits.stride(0)) if B > 1 else V) if ld is None else ld
+        if recent is not None:
+            W = int(recent.shape[1]) if W is None else W
+            if ld_recent is None:
+                ld_recent = int(recent.stride(0)) if recent.shape[0] > 1 else W
+        else:
+            W, ld_recent = 0, 0
+        _check(self._lib.gs_logits_writeback(self._h, _ptr(logits), B, V, ld, _ptr(params), _ptr(recent),
+                                             ld_recent, _ptr(recent_len), W, _stream_handle(stream)),
+               "gs_logits_writeback")
+
+    def sample_detail(self, logits, tokens, cap, params=None, recent=None, recent_len=None, u=None,
+                      status=None, stream=None):
+        """gs_sample_detail: the tokens of sample_batch plus, per row, the
+        kept candidates (ids, post-softmax p; the first `cap`), n_kept, the
+        nucleus cut, (S, s2) and the tie flag.  Returns a dict of device
+        tensors; rows with T > 0 are sorted (slow)."""
+        import torch
+        B, V = int(logits.shape[0]), int(logits.shape[1])
+        ld = int(logits.stride(0)) if B > 1 else V
+        dev = logits.device
+        out = {"ids": torch.zeros((B, cap), dtype=torch.int32, device=dev),
+               "p": torch.zeros((B, cap), dtype=torch.float32, device=dev),
+               "n_kept": torch.zeros(B, dtype=torch.int32, device=dev),
+               "cut": torch.zeros(B, dtype=torch.int32, device=dev),
+               "sums": torch.zeros((B, 2), dtype=torch.float32, device=dev),
+               "ties": torch.zeros(B, dtype=torch.int32, device=dev)}
+        det = GsDetail(_ptr(out["ids"]), _ptr(out["p"]), cap, _ptr(out["n_kept"]), _ptr(out["cut"]),
+                       _ptr(out["sums"]), _ptr(out["ties"]))
+        if recent is not None:
+            W = int(recent.shape[1])
+            ld_recent = int(recent.stride(0)) if recent.shape[0] > 1 else W
+        else:
+            W, ld_recent = 0, 0
+        _check(self._lib.gs_sample_detail(self._h, _ptr(logits), B, V, ld, _ptr(params), _ptr(recent), ld_recent,
+                                          _ptr(recent_len), W, _ptr(u), _ptr(tokens), _ptr(status),
+                                          ctypes.byref(det), _stream_handle(stream)), "gs_sample_detail")
+        return out
+
     def sample_batch(self, logits, tokens, params=None, recent=None, recent_len=None,
                      u=None, status=None, stream=None, V=None, ld=None, W=None, ld_recent=None,
                      noalloc=False):
@@ -353,6 +437,14 @@ def sample(logits, temperature, top_k, top_p, rep_penalty, recent):
     g = _get_global()
     g.set_params(temperature, top_k, top_p, rep_penalty)
     return g.sample(logits, recent)
+
+
+def sample_mut(logits, temperature, top_k, top_p, rep_penalty, recent):
+    """sample() that also leaves `logits` mutated in place as the reference
+    does (src/sampler.rs:37,41): penalized, then divided by T when T > 0."""
+    g = _get_global()
+    g.set_params(temperature, top_k, top_p, rep_penalty)
+    return g.sample_mut(logits, recent)
 
 
 # ---- quantized output projection (include/gs_gemv.h) --------------------------

@@ -86,10 +86,20 @@ int gs_sampler_reserve(gs_sampler *s, size_t B, size_t V);
  * src/main.rs:280.  `logits` and `recent` may be host or device pointers.
  * One LCG draw is consumed iff temperature > 0, as in the reference.
  * Synchronous: returns after the token is in *out_token.
- * Unlike the reference, `logits` is not modified (the reference leaves it
- * penalized and divided by T; its only caller discards it, src/main.rs:305). */
+ * `logits` is not modified (the reference leaves it penalized and divided
+ * by T; its only caller discards it, src/main.rs:305): gs_sample_mut is the
+ * variant that leaves it as the reference does. */
 int gs_sample(gs_sampler *s, const float *logits, size_t V,
               const uint32_t *recent, size_t W, uint32_t *out_token);
+
+/* sample(&mut logits, ...) exactly as src/sampler.rs:35-41 takes it: the
+ * token of gs_sample, and on return `logits` (host or device) holds what the
+ * reference leaves in the caller's Vec: every id of `recent` penalized once
+ * per occurrence (:37, apply_rep_penalty :23-30), then every logit divided
+ * by T when T > 0 (:41; a row with T <= 0 returns before the division, :39).
+ * `logits` is written only when the call returns GS_OK. */
+int gs_sample_mut(gs_sampler *s, float *logits, size_t V,
+                  const uint32_t *recent, size_t W, uint32_t *out_token);
 
 /* ---- batched: B independent rows (new; no reference counterpart beyond
  * calling src/sampler.rs:35 once per row) ----------------------------------
@@ -144,6 +154,58 @@ int gs_sample_batch_noalloc(gs_sampler *s, const float *d_logits, size_t B, size
                             const uint32_t *d_recent, size_t ld_recent,
                             const uint32_t *d_recent_len, size_t W, const float *d_u,
                             uint32_t *d_tokens, int32_t *d_status, void *stream);
+
+/* ---- diagnostic: the reference's intermediate results -------------------
+ * No counterpart in the reference's API: it exposes what src/sampler.rs:44-78
+ * computes on the way to the token, for parity checks.  Per row b (device
+ * buffers, any may be NULL):
+ *   ids[b*cap + j], p[b*cap + j]  for j < min(n_kept, cap): the candidates
+ *       after truncate(top_k) in the reference's order (scaled logit
+ *       descending, equal values by index) and their post-softmax
+ *       probabilities a_j / S (:55-56);
+ *   n_kept[b]  candidates after truncate(top_k) (:48-50); 0 for a greedy
+ *              row (T <= 0, :39) or a failed row;
+ *   cut[b]     candidates after the nucleus cut (:59-66); n_kept if
+ *              top_p >= 1;
+ *   sums[2b], sums[2b+1]  S (:54) and s2 (:67; 1 if top_p >= 1);
+ *   ties[b]    bit 0: two equal scaled logits meet at rank k (the
+ *              truncation boundary), inside the kept prefix or at the
+ *              nucleus cut; bit 1: the drawn element's value is shared by
+ *              another element, so the token depends on the order the
+ *              reference's sort_unstable_by gives equal keys (index
+ *              ascending here).  Equal summands commute, so S, s2 and the
+ *              cumulative sums never depend on that order. */
+typedef struct {
+    uint32_t *ids;
+    float *p;
+    size_t cap;
+    uint32_t *n_kept;
+    uint32_t *cut;
+    float *sums;
+    uint32_t *ties;
+} gs_detail;
+
+/* gs_sample_batch's arguments and tokens, plus `det`.  Every row with
+ * T > 0 takes a sort-based kernel (slow: a diagnostic, not a sampling
+ * path); tokens are the same as gs_sample_batch's. */
+int gs_sample_detail(gs_sampler *s, const float *d_logits, size_t B, size_t V,
+                     size_t ld, const gs_params *d_params,
+                     const uint32_t *d_recent, size_t ld_recent,
+                     const uint32_t *d_recent_len, size_t W, const float *d_u,
+                     uint32_t *d_tokens, int32_t *d_status, const gs_detail *det,
+                     void *stream);
+
+/* ---- batched write-back of the reference's mutation ----------------------
+ * Leaves rows [0, B) of d_logits as src/sampler.rs:37,41 leave each row it
+ * samples: penalized per window occurrence (the row's window as
+ * gs_sample_batch reads it: d_recent, d_recent_len, W), then divided by the
+ * row's T when T > 0.  Stream-ordered on `stream`; call it after
+ * gs_sample_batch on the same rows (the sampler reads the unmodified
+ * logits).  Same argument meaning as gs_sample_batch; d_params NULL = this
+ * sampler's params. */
+int gs_logits_writeback(gs_sampler *s, float *d_logits, size_t B, size_t V, size_t ld,
+                        const gs_params *d_params, const uint32_t *d_recent, size_t ld_recent,
+                        const uint32_t *d_recent_len, size_t W, void *stream);
 
 /* ---- device-resident decode helpers (decode loop, src/main.rs:279-311) ---
  * Append each row's token to its ring window: window[b*ld + (pos % W)] =
