@@ -181,29 +181,77 @@ __device__ __forceinline__ ParFn f_binfn(uint32_t lvl, uint32_t nup, uint32_t nt
 }
 __device__ __forceinline__ ParFn f_fn_id() { return ParFn{0u, 0u}; }
 
-// Classify one bin for accumulation sq at grid exponent e: returns 0 (one
-// increment: *lvl), 1 (two: *lvl, *thr, *up), 2 (more: list it).  For seq 3
-// of a nucleus row s2 lies in [s2lo, s2hi]: lvl is the lowest increment over
-// the range, and (thr, up) bound the deferred elements: y >= up adds lvl + 1
-// for every s2 in the range, y < thr adds lvl for every s2.
+// Classify one bin for accumulation sq at grid exponent e from its
+// increments at the edges of its y-range: returns 0 (one increment: *lvl),
+// 1 (two: *lvl and lvl + 1; f_threshold then finds the boundaries), 2 (more:
+// list it).  For seq 3 of a nucleus row s2 lies in [s2lo, s2hi]: lvl is the
+// lowest increment over the range.
 __device__ int f_classify(const FSeq &c, int sq, int e, float ylo, float yhi, float s2lo, float s2hi,
-                          uint32_t *lvl, float *thr, float *up)
+                          uint32_t *lvl)
 {
     uint32_t d0, u0, d1, u1;
     f_incs(f_val(c, sq, ylo, s2hi), e, &d0, &u0);
     f_incs(f_val(c, sq, yhi, s2lo), e, &d1, &u1);
     if (u1 - d0 > 1u || u1 < d0) return 2;
     *lvl = d0;
-    if (u1 == d0) return 0;
+    return u1 == d0 ? 0 : 1;
+}
+// One boundary of a two-increment bin (f_classify returned 1): which == 0
+// gives thr, the smallest y whose increment reaches lvl + 1 with a rounding
+// tie counted as reaching it (for every s2 in the range: at s2lo); which ==
+// 1 gives up, the smallest y that reaches lvl + 1 without a tie for every s2
+// (at s2hi), or +inf if no y in the bin does.  Elements with y >= up add
+// lvl + 1, those with thr <= y < up are ties (or, for seq 3 of a nucleus
+// row, undecided until s2 is exact), the rest add lvl.
+__device__ float f_threshold(const FSeq &c, int sq, int e, uint32_t lvl, float ylo, float yhi, float s2lo,
+                             float s2hi, int which)
+{
     // the real summand reaches (lvl + 1/2) g at y = m + ln((lvl + 1/2) g S s2)
-    const double a = ldexp((double)d0 + 0.5, e - 23) * (sq >= 2 ? (double)c.S : 1.0);
-    const double elo = (double)c.m + log(a * (sq == 3 && c.nuc ? (double)s2lo : 1.0));
-    const double ehi = (double)c.m + log(a * (sq == 3 && c.nuc ? (double)s2hi : 1.0));
-    *thr = f_first(c, sq, e, d0, ylo, yhi, s2lo, true, elo);
+    const double a = ldexp((double)lvl + 0.5, e - 23) * (sq >= 2 ? (double)c.S : 1.0);
+    const bool s3 = sq == 3 && c.nuc;
+    if (which == 0) {
+        const double elo = (double)c.m + log(a * (s3 ? (double)s2lo : 1.0));
+        return f_first(c, sq, e, lvl, ylo, yhi, s2lo, true, elo);
+    }
     uint32_t d2, u2;
     f_incs(f_val(c, sq, yhi, s2hi), e, &d2, &u2);
-    *up = d2 >= d0 + 1u ? f_first(c, sq, e, d0, ylo, yhi, s2hi, false, ehi) : INFINITY;
-    return 1;
+    if (d2 < lvl + 1u) return INFINITY;
+    const double ehi = (double)c.m + log(a * (s3 ? (double)s2hi : 1.0));
+    return f_first(c, sq, e, lvl, ylo, yhi, s2hi, false, ehi);
+}
+// Pending record (set by a classification loop, resolved by f_thresholds):
+// thr holds bin | sq << 12 | (grid exponent + 128) << 16, up holds lvl.
+__device__ __forceinline__ FullRec f_rec_pending(int b, int sq, int e, uint32_t lvl)
+{
+    return FullRec{__uint_as_float((uint32_t)b | ((uint32_t)sq << 12) | ((uint32_t)(e + 128) << 16)),
+                   __uint_as_float(lvl), 0u, 0u};
+}
+
+// Resolve the pending records [0, nrec) of a classification loop: two
+// threads per record (thr and up), all threads of the block.
+__device__ void f_thresholds(RowSmem &sm, const FSeq &c, float m0, float s2lo, float s2hi)
+{
+    FullSmem &f = sm.x.fs;
+    const int t = threadIdx.x;
+    const int nr = min(f.nrec, kRecCap);
+    for (int base = 0; base < nr; base += kThreads / 2) {
+        const int r = base + (t >> 1), which = t & 1;
+        uint32_t info = 0u, lvl = 0u;
+        if (r < nr) {
+            info = __float_as_uint(f.u.rec[r].thr);
+            lvl = __float_as_uint(f.u.rec[r].up);
+        }
+        __syncthreads();
+        if (r < nr) {
+            const int b = (int)(info & 0xfffu), sq = (int)((info >> 12) & 3u), e = (int)((info >> 16) & 255u) - 128;
+            float ylo, yhi;
+            f_range(m0, b, &ylo, &yhi);
+            const float v = f_threshold(c, sq, e, lvl, ylo, yhi, s2lo, s2hi, which);
+            if (which == 0) f.u.rec[r].thr = v;
+            else f.u.rec[r].up = v;
+        }
+        __syncthreads();
+    }
 }
 
 // Fields of the per-bin words.
@@ -250,6 +298,27 @@ __device__ __forceinline__ ParFn f_item_fn(const FullSmem &f, int sq, int b, int
 
 // ---------------------------------------------------------------------------
 // Block helpers.
+
+// f(p, entry) for list positions p in [lo, hi), strided over the block; each
+// thread issues U loads before it uses any (the loop bodies are short and
+// end in LDS atomics, so one load per iteration would expose its latency).
+template <int U, class F>
+__device__ __forceinline__ void f_list_for_each(const uint64_t *gl, uint32_t lo, uint32_t hi, F f)
+{
+    for (uint32_t base = lo + threadIdx.x; base < hi; base += kThreads * U) {
+        uint64_t e[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t q = base + (uint32_t)(u * kThreads);
+            e[u] = q < hi ? ldg(gl + q) : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t q = base + (uint32_t)(u * kThreads);
+            if (q < hi) f(q, e[u]);
+        }
+    }
+}
 __device__ double f_block_excl_f64(double v, double *tot, RowSmem &sm)
 {
     const int lane = lane_id(), w = wave_id();
@@ -718,15 +787,14 @@ __device__ int f_items(RowSmem &sm, const uint64_t *gl, uint64_t *items, size_t 
         const uint64_t en = ldg(gl + p);
         if (en) stg(items + f_rank(gl, 0u, (uint32_t)nover, en), en);
     }
-    for (uint32_t p = (uint32_t)nover + t; p < f.list_end; p += kThreads) {
-        const uint64_t en = ldg(gl + p);
-        if (!en) continue;
+    f_list_for_each<4>(gl, (uint32_t)nover, f.list_end, [&](uint32_t, uint64_t en) {
+        if (!en) return;
         const int b = f_bin(f_entry_y(en) - f.m0);
-        if (b >= nb || !lst(b)) continue;
+        if (b >= nb || !lst(b)) return;
         const uint32_t rk = f_rank(gl, f.seg[b], f.sege[b], en);
         if (rk < f.cnt[b]) stg(items + f.v1[b] + rk, en);
         else f.fail = 1;
-    }
+    });
     __threadfence_block();
     __syncthreads();
     return f.fail ? -1 : (int)tot + nov;
@@ -747,15 +815,14 @@ __device__ void f_bags(RowSmem &sm, const uint64_t *gl, const FSeq &c, int sq, f
     auto grid = [&](int b) {
         return sq == 1 ? (int)((f.w1[b] >> 16) & 255u) - 128 : (int)f.ex[b][sq - 2] - 128;
     };
-    for (uint32_t p = (uint32_t)f.nover + t; p < f.list_end; p += kThreads) {
-        const uint64_t en = ldg(gl + p);
-        if (!en) continue;
+    f_list_for_each<8>(gl, (uint32_t)f.nover, f.list_end, [&](uint32_t, uint64_t en) {
+        if (!en) return;
         const float y = f_entry_y(en);
         const int b = f_bin(y - f.m0);
-        if (f_cls(f.w1[b], f.w23[b], sq) != kCBag) continue;
+        if (f_cls(f.w1[b], f.w23[b], sq) != kCBag) return;
         uint32_t dn, up;
         f_incs(f_val(c, sq, y, s2), grid(b), &dn, &up);
-        if (dn >= (1u << 24)) { f.fail = 1; continue; }
+        if (dn >= (1u << 24)) { f.fail = 1; return; }
         if (dn == up) {
             atomicAdd(&val[b], dn);
         } else {
@@ -763,7 +830,7 @@ __device__ void f_bags(RowSmem &sm, const uint64_t *gl, const FSeq &c, int sq, f
             if (slot < kTieCap) f.ties[slot] = FullTie{en, (uint32_t)b | ((uint32_t)sq << 16), dn};
             else f.fail = 1;
         }
-    }
+    });
     __syncthreads();
     const int nt = min(f.nties, kTieCap);
     for (int i = wave_id(); i < nt; i += kWaves) {
@@ -858,6 +925,12 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     int nan = 0;
     float m0 = 0.0f;
     auto visit1 = [&](int i, float y) {
+#ifdef GS_EXP_P1MIN
+        tmax = fmaxf(tmax, y); return;
+#endif
+#ifdef GS_EXP_P1CNT
+        { tmax = fmaxf(tmax, y); const float dp = y - m0; if (dp >= -kFDLo) atomicAdd(&f.cnt[f_bin(dp)], 1u); return; }
+#endif
         nan |= (int)isnan(y);
         if (y > tmax && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) tmax = y;
         const float dp = y - m0;
@@ -1025,13 +1098,13 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                     cls = kCLst;
                 } else {
                     e = f_dexp(lo);
-                    float ylo, yhi, thr = 0.0f, up = 0.0f;
+                    float ylo, yhi;
                     f_range(m0, b, &ylo, &yhi);
-                    const int k = f_classify(c, 1, e, ylo, yhi, 1.0f, 1.0f, &lvl, &thr, &up);
+                    const int k = f_classify(c, 1, e, ylo, yhi, 1.0f, 1.0f, &lvl);
                     cls = k == 0 ? kCUni : kCBag;
                     if (k == 1 && n < 65536u) {
                         const int rr = atomicAdd(&f.nrec, 1);
-                        if (rr < kRecCap) { f.u.rec[rr] = FullRec{thr, up, 0u, 0u}; rec = (uint32_t)rr; cls = kCRec; }
+                        if (rr < kRecCap) { f.u.rec[rr] = f_rec_pending(b, 1, e, lvl); rec = (uint32_t)rr; cls = kCRec; }
                     }
                 }
             }
@@ -1044,6 +1117,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
         }
         F_TS(3);
         __syncthreads();
+        f_thresholds(sm, c, m0, 1.0f, 1.0f);
         uint32_t capl = 0;
 #pragma unroll
         for (int q = 0; q < kPer; q++) capl += f.sege[kPer * t + q];
@@ -1066,6 +1140,9 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
 
     // ---- pass 2 (cache): seq-1 record counts; listed bins written ----------
     auto visit2 = [&](int i, float y) {
+#ifdef GS_EXP_P2MIN
+        if (y == 12345.0f) f.fail = 1; return;
+#endif
         const float dp = y - m0;
         if (!(dp <= kFDUp) || dp < -kFDLo) return;
         const int b = f_bin(dp);
@@ -1150,14 +1227,13 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
         for (int b = t; b < kFBins; b += kThreads) mf[b] = 0ull;
         __syncthreads();
         F_TS(5);
-        for (uint32_t p = (uint32_t)nover + t; p < f.list_end; p += kThreads) {
-            const uint64_t en = ldg(gl + p);
-            if (!en) continue;
+        f_list_for_each<8>(gl, (uint32_t)nover, f.list_end, [&](uint32_t, uint64_t en) {
+            if (!en) return;
             const float y = f_entry_y(en);
             const int b = f_bin(y - m0);
             if ((f.w1[b] & 7u) == kCLst)
                 atomicAdd((unsigned long long *)&mf[b], (unsigned long long)ldexp((double)glibc_expf_tab(y - m, f.exptab), 40));
-        }
+        });
         F_TS(6);
         double osum = 0.0;
         for (int p = t; p < nover; p += kThreads) {
@@ -1250,12 +1326,11 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                     cl2 = kCLst;
                 } else {
                     e2 = f_dexp(c2lo);
-                    float thr = 0.0f, up = 0.0f;
-                    const int k = f_classify(c2, 2, e2, ylo, yhi, 1.0f, 1.0f, &lvl2, &thr, &up);
+                    const int k = f_classify(c2, 2, e2, ylo, yhi, 1.0f, 1.0f, &lvl2);
                     cl2 = k == 0 ? kCUni : kCBag;
                     if (k == 1 && !listed2 && n < 65536u) {
                         const int rr = atomicAdd(&f.nrec, 1);
-                        if (rr < kRecCap) { f.u.rec[rr] = FullRec{thr, up, 0u, 0u}; r2 = (uint32_t)rr; cl2 = kCRec; }
+                        if (rr < kRecCap) { f.u.rec[rr] = f_rec_pending(b, 2, e2, lvl2); r2 = (uint32_t)rr; cl2 = kCRec; }
                     }
                 }
             }
@@ -1264,12 +1339,11 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                     cl3 = kCLst;
                 } else {
                     e3 = f_dexp(c3lo);
-                    float thr = 0.0f, up = 0.0f;
-                    const int k = f_classify(c2, 3, e3, ylo, yhi, s2lo, s2hi, &lvl3, &thr, &up);
+                    const int k = f_classify(c2, 3, e3, ylo, yhi, s2lo, s2hi, &lvl3);
                     cl3 = k == 0 ? kCUni : kCBag;
                     if (k == 1 && !listed2 && n < 65536u) {
                         const int rr = atomicAdd(&f.nrec, 1);
-                        if (rr < kRecCap) { f.u.rec[rr] = FullRec{thr, up, 0u, 0u}; r3 = (uint32_t)rr; cl3 = kCRec; }
+                        if (rr < kRecCap) { f.u.rec[rr] = f_rec_pending(b, 3, e3, lvl3); r3 = (uint32_t)rr; cl3 = kCRec; }
                     }
                 }
             }
@@ -1291,6 +1365,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
         F_TS(9);
         if (l23 >= 0) atomicMax(&f.last3, l23);
         __syncthreads();
+        f_thresholds(sm, c2, m0, s2lo, s2hi);
         // list segments of the bins listed in pass 3 (room for raw values of
         // penalized ids too)
         if (has_pen) {
