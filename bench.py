@@ -26,18 +26,35 @@ sys.path.insert(0, os.path.join(ROOT, "gguf-rs-cli_amd"))
 PEAK_HBM_GBS = 8000.0   # MI355X HBM3E
 
 
+def sources_digest():
+    """SHA-1 over the library's kernel sources (gguf-rs-cli_amd/csrc, sorted
+    by name): identifies the code a committed profile was taken from."""
+    import hashlib
+    h = hashlib.sha1()
+    csrc = os.path.join(ROOT, "gguf-rs-cli_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".hpp", ".cpp", ".h")):
+            h.update(name.encode())
+            h.update(open(os.path.join(csrc, name), "rb").read())
+    return h.hexdigest()
+
+
 def profiled_traffic():
     """HBM bytes per c3 step from the committed rocprofv3 summary
-    (FETCH_SIZE and WRITE_SIZE runs, scaled by a plain-copy calibration), or
-    None if the summary is absent."""
+    (FETCH_SIZE and WRITE_SIZE runs, scaled by a plain-copy calibration).
+    None if the summary is absent or was taken from other kernel sources
+    than these (its kernel_sources_sha1 line differs from sources_digest())."""
     path = os.path.join(ROOT, "profiles", "sample_rows_c3_qwen_V152064_B256.md")
+    traffic, digest = None, None
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
+                traffic = int(line.split(":", 1)[1])
+            elif line.startswith("kernel_sources_sha1:"):
+                digest = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None
+    return traffic if digest == sources_digest() else None
 
 
 def log(*a):
@@ -556,9 +573,14 @@ def main():
                     help="only the Q6_K logits projection (for profiling)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the graph-captured decode step (for profiling)")
+    ap.add_argument("--digest", action="store_true",
+                    help="print the kernel sources' digest (for a profile summary) and exit")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 1 GiB device copy 5x (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.digest:
+        print(sources_digest())
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: the sampler's rows are independent and this "
               "build runs on a single MI355X (--gpus %d not supported)" % args.gpus, file=sys.stderr)
