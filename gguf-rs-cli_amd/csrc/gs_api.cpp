@@ -44,6 +44,7 @@ struct gs_sampler {
     bool captured;               // a call was recorded into a graph: buffers are never freed before destroy
     void **retired;              // buffers replaced after a capture, freed by gs_sampler_destroy
     size_t n_retired, cap_retired;
+    int n_cus;                   // compute units of the device (0: not queried yet)
 };
 
 namespace gs { int init_static_scratch(int device); }
@@ -107,6 +108,20 @@ int grow(gs_sampler *s, void **buf, size_t *cap, size_t need_bytes)
     return GS_OK;
 }
 
+// Compute units of the sampler's device (queried once).
+int num_cus(gs_sampler *s)
+{
+    if (!s->n_cus) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, s->device) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        s->n_cus = n;
+    }
+    return s->n_cus;
+}
+
 bool needs_full_path(const gs_params &p, size_t V)
 {
     if (!(p.temperature > 0.0f) || V <= 1) return false;
@@ -117,6 +132,8 @@ bool needs_full_path(const gs_params &p, size_t V)
 // Buffer of the split top-k path for `rows` rows of width `width`: the
 // virtual rows' values, then their ids.
 size_t split_bytes(size_t rows, size_t width) { return rows * width * 8; }
+// Buffer of the chunked top-k path (virtual rows of stride chunk_stride).
+size_t chunk_bytes(size_t B, size_t V) { return split_bytes(B, gs::chunk_stride(V)); }
 
 int reserve_split(gs_sampler *s, size_t rows, size_t width)
 {
@@ -254,9 +271,11 @@ int gs_sampler_set_state(gs_sampler *s, uint64_t state)
 int gs_sampler_reserve(gs_sampler *s, size_t B, size_t V)
 {
     if (!s || V > GS_MAX_VOCAB) return GS_ERR_INVALID;
-    if (V > gs::kRegMaxV) {               // rows the split top-k path may take, any k
+    if (V > gs::kRegMaxV) {               // rows the split or chunked top-k paths may take, any k
         const size_t rows = B < (size_t)gs::kSplitMaxRows ? B : (size_t)gs::kSplitMaxRows;
-        int rc = reserve_split(s, rows ? rows : 1, gs::kSplitMaxWidth);
+        size_t need = split_bytes(rows ? rows : 1, gs::kSplitMaxWidth);
+        if (gs::chunk_path_ok(V) && chunk_bytes(B, V) > need) need = chunk_bytes(B, V);
+        int rc = grow(s, &s->split, &s->split_cap, need);
         if (rc) return rc;
     }
     return reserve_scratch(s, B, V);
@@ -321,7 +340,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
         // the full-vocabulary path (several kernels) synchronises the stream
         s->fb_rows = 1;
         s->fb_last = s->fb;
-        if (gs::launch_sample_rows(a, 1, false, true, s->stream) != hipSuccess) return GS_ERR_HIP;
+        if (gs::launch_sample_rows(a, 1, s->stream) != hipSuccess) return GS_ERR_HIP;
         if (hipStreamSynchronize(s->stream) != hipSuccess) return GS_ERR_HIP;
         st = *(volatile int32_t *)s->h_status;
         tok = *(volatile uint32_t *)s->h_tok;
@@ -338,7 +357,7 @@ int gs_sample(gs_sampler *s, const float *logits, size_t V, const uint32_t *rece
             a.done_val = ++s->seq;
             const hipError_t le = reg     ? gs::launch_reg_row(a, s->stream)
                                   : split ? launch_split_rows(s->split, a, 1, gs::split_width(s->params, V), s->stream)
-                                          : gs::launch_sample_rows(a, 1, true, false, s->stream);
+                                          : gs::launch_sample_rows(a, 1, s->stream);
             if (le != hipSuccess) return GS_ERR_HIP;
             volatile uint64_t *f = s->h_done;
             uint64_t w = *f;
@@ -482,7 +501,6 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
     if (cap && !d_u && s->params.temperature > 0.0f) return GS_ERR_UNSUPPORTED;
     if (cap) s->captured = true;
     const bool full = d_params || needs_full_path(s->params, V);
-    const bool small = d_params || !needs_full_path(s->params, V);
     CallBufs bf;
     if (fixed) {
         bf = *fixed;
@@ -513,10 +531,14 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
     a.scratch_stride = gs::scratch_u32_per_row(V);
     a.fb = bf.fb;
     if (hook) a.hook = *hook;
-    // measured on MI355X: at V = 152064 the split path wins up to B = 16
-    // (2368 chunks) and loses at B = 32; at V = 40000 it wins up to B = 32
+    // measured on MI355X: the split path (1024-logit chunks) beats the
+    // chunked path up to about 2000 chunks per call (V = 152064: B <= 8;
+    // V = 128256: B <= 16; V = 256000: B <= 4)
     bool split = !d_params && B <= (size_t)gs::kSplitMaxRows && B * (V / gs::kSplitL) <= gs::kSplitMaxChunks &&
                  gs::split_fits(s->params, V);
+#ifdef GS_EXP_NOSPLIT
+    split = false;
+#endif
     const size_t wd = split ? gs::split_width(s->params, V) : 0;
     if (split && bf.split_cap < split_bytes(B, wd)) {
         // the buffers must grow: not with fixed buffers or under stream
@@ -526,12 +548,29 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
         else if ((rc = reserve_split(s, B, wd))) return rc;
         else bf.split = s->split;
     }
+    // top-k rows of a large vocabulary in a batch with fewer rows than CUs:
+    // chunks of up to 32768 logits, one workgroup each (per-row params: the
+    // kernels pick the rows).  With B >= #CUs one workgroup per row already
+    // fills the chip, and leaves the CUs that a batch's full-vocabulary rows
+    // do not use to its top-k rows.
+    bool chunked = !split && gs::chunk_path_ok(V) && B < (size_t)num_cus(s) &&
+                   (d_params || gs::chunk_fits(s->params, V));
+    if (chunked && bf.split_cap < chunk_bytes(B, V)) {
+        if (bf.fixed || cap) chunked = false;
+        else if ((rc = grow(s, &s->split, &s->split_cap, chunk_bytes(B, V)))) return rc;
+        else { bf.split = s->split; bf.split_cap = s->split_cap; }
+    }
     if (split) {
         // a few rows of a large vocabulary: spread each row over the chip
         if (launch_split_rows(bf.split, a, B, wd, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
     } else {
         if (full) { s->fb_rows = B; s->fb_last = bf.fb; }
-        if (gs::launch_sample_rows(a, (int)B, small, full, (hipStream_t)stream) != hipSuccess) return GS_ERR_HIP;
+        else a.fb = nullptr;            // no full-vocabulary row: the flags are not written
+        const hipError_t le =
+            chunked ? gs::launch_chunked(a, (int)B, (float *)bf.split,
+                                         (uint32_t *)((float *)bf.split + B * gs::chunk_stride(V)), (hipStream_t)stream)
+                    : gs::launch_sample_rows(a, (int)B, (hipStream_t)stream);
+        if (le != hipSuccess) return GS_ERR_HIP;
     }
     if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);
     return GS_OK;
@@ -603,7 +642,9 @@ int gs_sample_batch_noalloc(gs_sampler *s, const float *d_logits, size_t B, size
     // kSplitMaxRows rows) | full-vocabulary scratch
     const size_t fb_bytes = gs::align256((B ? B : 1) * sizeof(int32_t));
     const size_t split_rows = B < (size_t)gs::kSplitMaxRows ? B : (size_t)gs::kSplitMaxRows;
-    const size_t sp_bytes = V > gs::kRegMaxV ? gs::align256(split_bytes(split_rows, gs::kSplitMaxWidth)) : 0;
+    size_t sp_need = split_bytes(split_rows, gs::kSplitMaxWidth);
+    if (gs::chunk_path_ok(V) && chunk_bytes(B, V) > sp_need) sp_need = chunk_bytes(B, V);
+    const size_t sp_bytes = V > gs::kRegMaxV ? gs::align256(sp_need) : 0;
     const size_t full_bytes = B * gs::scratch_u32_per_row(V) * sizeof(uint32_t);
     if (fb_bytes + sp_bytes + full_bytes > gs::kStaticScratchBytes) return GS_ERR_UNSUPPORTED;
     char *p = (char *)base;

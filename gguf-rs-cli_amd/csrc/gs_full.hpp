@@ -1071,6 +1071,9 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             }
             pre = f_block_excl_f64(loc, &tot, sm) + osum;
         }
+#if defined(GS_TIMING) || defined(GS_DIAG)
+        if (t == 0 && blockIdx.x < 1024) g_vdiag[blockIdx.x * 16 + 14] = __float_as_int((float)(tot + osum));
+#endif
         F_TS(2);
         // classes (records overwrite the masses: every thread has read
         // them); the predicted sums before / after each bin go through LDS

@@ -1259,14 +1259,28 @@ __device__ __forceinline__ void store_row(const RowArgs &a, int b, int tok, int 
 // Row paths: the small kernel serves greedy, degenerate and top-k rows; the
 // full-vocabulary rows go to the binned kernel and, when its checks fail, to
 // the sort kernel.  Each kernel derives the path from the row's parameters.
-__device__ __forceinline__ bool is_full_path(const gs_params &p, int V)
+__host__ __device__ __forceinline__ bool is_full_path(const gs_params &p, int V)
 {
     if (!(p.temperature > 0.0f) || V < 2) return false;
     const int keep = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
     return !(keep < V && keep <= kMaxTopK);
 }
 
+// The row kernel's modes.  kModeSmall: greedy, degenerate and top-k rows
+// (and the virtual rows of chunked top-k rows); kModeBins: full-vocabulary
+// rows by the exact binned path; kModeSort: the full-vocabulary rows whose
+// binned checks failed (fb[b] = 1), by the sort path; kModeDetail: every
+// row sorted, with the diagnostic outputs.  (A kernel that runs both kinds
+// of rows in one launch was measured: instantiating it raises the binned
+// kernel's register spills from 5 to 72, and c3 by 7%.)
 enum { kModeSmall = 0, kModeBins = 1, kModeSort = 2, kModeDetail = 3 };
+
+// A row of the chunked top-k path (gs_kernels.hpp: chunk_count etc.).
+__device__ __forceinline__ bool chunk_row(const gs_params &p, int V)
+{
+    return p.temperature > 0.0f && p.temperature < INFINITY && p.top_k > 0 && (int)p.top_k < V &&
+           p.top_k <= kChunkMaxK;
+}
 
 template <int MODE>
 __global__ void __launch_bounds__(kThreads)
@@ -1275,8 +1289,12 @@ sample_rows_kernel(RowArgs a)
     __shared__ RowSmem sm;
     const int b = blockIdx.x;
     const int t = threadIdx.x;
-    const int V = a.V;
     const gs_params p = a.params ? a.params[b] : a.uparams;
+    // A chunked top-k row: its virtual row (the chunks' best kp, penalized,
+    // in index order) is sampled as a row of width nch * kp with no penalty,
+    // and the token maps back through cvidx.
+    const bool crow = MODE == kModeSmall && a.chunked && chunk_row(p, a.V);
+    const int V = crow ? a.cnch * (((int)p.top_k + 3) & ~3) : a.V;
     // the detail kernel sorts every row with T > 0 (the rest: the small path)
     const bool sorted_row = MODE == kModeDetail && p.temperature > 0.0f && V >= 2;
     const bool full = MODE == kModeDetail ? sorted_row : is_full_path(p, V);
@@ -1286,22 +1304,22 @@ sample_rows_kernel(RowArgs a)
         if (a.det.ties) a.det.ties[b] = 0u;
     }
     if (MODE == kModeSmall && full) return;
-    if (MODE != kModeSmall && MODE != kModeDetail && !full) {
-        if (MODE == kModeBins && t == 0 && a.fb != nullptr) a.fb[b] = 0;
+    if (MODE == kModeBins && !full) {
+        if (t == 0) a.fb[b] = 0;
         return;
     }
-    if (MODE == kModeSort && a.fb != nullptr && a.fb[b] == 0) return;
+    if (MODE == kModeSort && (!full || a.fb[b] == 0)) return;
     GS_STAMP(8 * MODE);
 #ifdef GS_TIMING
     if (MODE == kModeSmall && blockIdx.x == g_row && (threadIdx.x & 63) == 0)
         g_fails[1100 + (threadIdx.x >> 6)] = (int)__builtin_amdgcn_s_memrealtime();
     const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
 #endif
-    const float *row = a.logits + (size_t)b * a.ld;
+    const float *row = crow ? a.cvrow + (size_t)b * a.cvld : a.logits + (size_t)b * a.ld;
     if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
 
     int tok = 0, status = GS_OK;
-    const bool has_pen = (p.rep_penalty != 1.0f) && a.recent != nullptr;
+    const bool has_pen = !crow && (p.rep_penalty != 1.0f) && a.recent != nullptr;
     int W = 0;
     if (has_pen) {
         W = a.recent_len ? (int)a.recent_len[b] : a.W;
@@ -1399,7 +1417,7 @@ sample_rows_kernel(RowArgs a)
 #endif
         }
         if (t == 0) a.fb[b] = done ? 0 : 1;
-        if (!done) return;
+        if (!done) return;   // the sort kernel finishes the row
     } else {
         if (sm.flag_nan) status = GS_ERR_NAN;
         else {
@@ -1418,6 +1436,7 @@ sample_rows_kernel(RowArgs a)
 #ifdef GS_TIMING
     if (t == 0 && b < 256 && MODE == kModeBins) g_fails[256 + b] = (int)(__builtin_amdgcn_s_memrealtime() - t_begin);
 #endif
+    if (crow) tok = status == GS_OK ? (int)ldg(a.cvidx + (size_t)b * a.cvld + tok) : 0;
     if (t == 0) store_row(a, b, tok, status);
 }
 
@@ -1616,18 +1635,45 @@ split_select_kernel(RowArgs a, int nch, int kp, float *vrow, uint32_t *vidx, siz
     chunk_select<kSplitThreads, kSplitPer>(sm, s, b, c, c0, L, [row](int i) { return ldg(row + i); });
 }
 
-// Pass 2: sample virtual row b (width vld, a multiple of 4, 16-byte aligned;
-// no penalty): the register path, else the general top-k paths; the token
-// is mapped back through vidx.
+// Chunked top-k path, pass 1: chunk c of row b (a row with chunk_row true;
+// the others return) is [c V / nch, (c+1) V / nch), at most kChunkL logits,
+// 32 per thread; its best kp = round_up(k, 4) go to slots [c kp, (c+1) kp)
+// of row b's virtual row (stride vld), in index order.
+constexpr int kChunkPer = kChunkL / kThreads;
 __global__ void __launch_bounds__(kThreads)
-split_finish_kernel(RowArgs a, const float *vrow, const uint32_t *vidx, size_t vld)
+chunk_topk_kernel(RowArgs a, int nch, float *vrow, uint32_t *vidx, size_t vld)
 {
-    __shared__ RowSmem sm;
+    __shared__ SelSmem<kThreads, kChunkPer> sm;
+    const int c = blockIdx.x, b = blockIdx.y;
+    const gs_params p = a.params ? a.params[b] : a.uparams;
+    if (!chunk_row(p, a.V)) return;
+    const int c0 = (int)((int64_t)c * a.V / nch);
+    const int L = (int)((int64_t)(c + 1) * a.V / nch) - c0;
+    const float *row = a.logits + (size_t)b * a.ld + c0;
+    SelArgs s;
+    s.T = p.temperature;
+    s.rep = p.rep_penalty;
+    s.kp = ((int)p.top_k + 3) & ~3;
+    s.recent = a.recent;
+    s.ld_recent = a.ld_recent;
+    s.recent_len = a.recent_len;
+    s.W = a.W;
+    s.vrow = vrow;
+    s.vidx = vidx;
+    s.vld = vld;
+    chunk_select<kThreads, kChunkPer>(sm, s, b, c, c0, L, [row](int i) { return ldg(row + i); });
+}
+
+// Pass 2: sample virtual row b (its width nch * kp is a multiple of 4 and
+// the row is 16-byte aligned; no penalty: the values are already penalized):
+// the register path, else the general top-k paths; the token is mapped
+// back through vidx.  All threads of the block call it.
+__device__ void finish_virtual_row(RowSmem &sm, const RowArgs &a, int b, const gs_params &p, const float *vrow,
+                                   const uint32_t *vidx, size_t vld, int nch)
+{
     const int t = threadIdx.x;
-    const int b = blockIdx.x;
-    const gs_params p = a.uparams;
     const float *vr = vrow + (size_t)b * vld;
-    const int V2 = (int)vld;
+    const int V2 = nch * (((int)p.top_k + 3) & ~3);
     float4 rv[kRegF4];
     {
         const float4 *r4 = reinterpret_cast<const float4 *>(vr);
@@ -1649,8 +1695,18 @@ split_finish_kernel(RowArgs a, const float *vrow, const uint32_t *vidx, size_t v
     if (t == 0) store_row(a, b, status == GS_OK ? (int)ldg(vidx + (size_t)b * vld + tok) : 0, status);
 }
 
-hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st)
+__global__ void __launch_bounds__(kThreads)
+split_finish_kernel(RowArgs a, const float *vrow, const uint32_t *vidx, size_t vld, int nch)
 {
+    __shared__ RowSmem sm;
+    finish_virtual_row(sm, a, blockIdx.x, a.uparams, vrow, vidx, vld, nch);
+}
+
+hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st)
+{
+    // with per-row params a batch may hold rows of both kinds
+    const bool full = a.params || is_full_path(a.uparams, a.V);
+    const bool small = a.params || !full;
     if (small) hipLaunchKernelGGL(sample_rows_kernel<kModeSmall>, dim3(B), dim3(kThreads), 0, st, a);
     if (full) {
         hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
@@ -1694,8 +1750,20 @@ hipError_t launch_split(const RowArgs &a, int B, float *vrow, uint32_t *vidx, hi
     const size_t vld = (size_t)nch * kp;
     hipLaunchKernelGGL(split_select_kernel, dim3(nch, B), dim3(kSplitThreads), 0, st, a, nch, kp, vrow, vidx, vld);
     hipLaunchKernelGGL(split_finish_kernel, dim3(B), dim3(kThreads), 0, st, a, (const float *)vrow,
-                       (const uint32_t *)vidx, vld);
+                       (const uint32_t *)vidx, vld, nch);
     return hipGetLastError();
+}
+hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st)
+{
+    const int nch = chunk_count((size_t)a.V);
+    const size_t vld = chunk_stride((size_t)a.V);
+    hipLaunchKernelGGL(chunk_topk_kernel, dim3(nch, B), dim3(kThreads), 0, st, a, nch, vrow, vidx, vld);
+    a.chunked = 1;
+    a.cvrow = vrow;
+    a.cvidx = vidx;
+    a.cvld = vld;
+    a.cnch = nch;
+    return launch_sample_rows(a, B, st);   // the virtual rows go through the small kernel
 }
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st)

@@ -35,6 +35,11 @@ struct RowArgs {
     int kwin_n;                    // single-row calls: a host window of W <= kKernWin ids passed
     uint32_t kwin[kKernWin];       // by value here (used instead of `recent` when kwin_n != 0)
     gs_detail det;                 // diagnostic outputs of the detail kernel (gs_sample_detail)
+    int chunked;                   // rows with chunk_row() true are sampled by the chunked top-k path:
+    const float *cvrow;            // its virtual rows (values, ids), stride cvld, cnch chunks
+    const uint32_t *cvidx;
+    size_t cvld;
+    int cnch;
 };
 
 // Per-row scratch (u32 units) of the full-vocabulary paths: the sort path
@@ -46,7 +51,10 @@ inline size_t scratch_u32_per_row(size_t V)
     return 6 * V + 2 * (3 * 256 + 2 * 4096 + 6 * 2048) + 16384;
 }
 
-hipError_t launch_sample_rows(const RowArgs &a, int B, bool small, bool full, hipStream_t st);
+// The row kernels of a batch: the small-path rows (and, when a.chunked is
+// set, the chunked rows' virtual rows), then the full-vocabulary rows by the
+// exact binned path and, for rows whose checks failed, by the sort path.
+hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st);
 // Every row sorted (diagnostic; fills a.det); scratch as the sort path.
 hipError_t launch_detail_rows(const RowArgs &a, int B, hipStream_t st);
 // Single-row register path (B = 1); rows it cannot finish report kStatusRetryHost.
@@ -62,9 +70,27 @@ constexpr size_t kRegMaxV = 32768;   // widest row the register kernel holds (10
 constexpr int kSplitL = 1024;          // elements per chunk; the last chunk takes the rest (< 2 kSplitL)
 constexpr int kSplitMaxKp = 128;
 constexpr int kSplitMaxRows = 32;      // more rows fill the chip one workgroup per row
-constexpr size_t kSplitMaxChunks = 2560; // B * V / kSplitL above this: one workgroup per row is faster
+constexpr size_t kSplitMaxChunks = 2000; // B * V / kSplitL above this: the chunked path is faster
 constexpr size_t kSplitMaxWidth = 32768;
 bool split_fits(const gs_params &p, size_t V);
+// Chunked top-k path for batches: rows with V > kRegMaxV, finite T > 0 and
+// 0 < k <= kChunkMaxK (checked per row on the device, so per-row params
+// work) are cut into nch = chunk_count(V) balanced chunks of at most
+// kChunkL logits; each chunk keeps its best kp = round_up(k, 4) in a virtual
+// row of stride chunk_stride(V) (pass 1, one 1024-thread workgroup per
+// chunk), then one launch of the row kernel samples the virtual rows and
+// every other row of the batch (pass 2).
+constexpr int kChunkL = 32768;
+constexpr uint32_t kChunkMaxK = 128;
+inline int chunk_count(size_t V) { return (int)((V + kChunkL - 1) / kChunkL); }
+inline size_t chunk_stride(size_t V) { return (size_t)chunk_count(V) * kChunkMaxK; }
+inline bool chunk_path_ok(size_t V) { return V > kRegMaxV && chunk_stride(V) <= kSplitMaxWidth; }
+hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st);
+inline bool chunk_fits(const gs_params &p, size_t V)
+{
+    return p.temperature > 0.0f && p.temperature < INFINITY && p.top_k > 0 && (size_t)p.top_k < V &&
+           p.top_k <= kChunkMaxK;
+}
 size_t split_width(const gs_params &p, size_t V);
 hipError_t launch_split(const RowArgs &a, int B, float *vrow, uint32_t *vidx, hipStream_t st);
 // gs_sample_batch with an optional decode hook (the sampler's last kernel

@@ -26,10 +26,16 @@ struct SelArgs {
     size_t vld;
 };
 
+constexpr int kSelHist = 2048;        // bins of the thread maxima's keys
+
 template <int NT, int PER>
 struct SelSmem {
-    uint32_t cnt[NT * PER];           // window occurrences per chunk element
-    uint64_t tmax[NT];
+    uint32_t cnt[NT * PER / 2];       // window occurrences per chunk element, two u16 per word
+    uint64_t tmax[NT];                // thread maxima at or above the histogram's edge
+    uint32_t hist[kSelHist];
+    uint32_t red[2 * (NT / 64)];      // per-wave key min / max
+    uint32_t edge;
+    int nlist;
     uint64_t cand[PER * kSelMaxKp];
     float candx[PER * kSelMaxKp];
     uint64_t top[kSelMaxKp];
@@ -39,12 +45,10 @@ struct SelSmem {
     int nan;
 };
 
-// (key of y << 32) | ~id: larger is earlier in the sampler's order (y
-// descending, then index ascending).
-__device__ __forceinline__ uint64_t sel_key(float y, uint32_t id) { return ((uint64_t)f2key(y) << 32) | (uint64_t)(~id); }
-
 // Chunk c of row b: elements c0 + i for i < L, kp <= L <= NT * PER, element i
-// held by thread i % NT; val(i) is its raw logit.  Applies the penalty (the
+// held by thread i % NT; val(i) is its raw logit.  Candidates are ordered by
+// (key of y << 32) | ~id: larger is earlier in the sampler's order (y
+// descending, then index ascending).  Applies the penalty (the
 // window's occurrences of each id in the chunk, one op per occurrence),
 // divides by T, keeps the kp largest keys and writes their penalized logits
 // and ids in index order.  A NaN in the chunk goes to its first slot.  All
@@ -70,57 +74,110 @@ __device__ void chunk_select(SelSmem<NT, PER> &sm, const SelArgs &s, int b, int 
         x[u] = i < L ? val(i) : -INFINITY;
     }
     if (has_pen)
-        for (int i = t; i < L; i += NT) sm.cnt[i] = 0u;
+        for (int i = t; i < (L + 1) / 2; i += NT) sm.cnt[i] = 0u;
     if (t == 0) { sm.ncand = 0; sm.nan = 0; }
     __syncthreads();
     if (has_pen) {
         const uint32_t *rec = s.recent + (size_t)b * s.ld_recent;
         for (int j = t; j < W; j += NT) {
             const uint32_t d = ldg(rec + j) - (uint32_t)c0;   // ids >= V never fall in a chunk
-            if (d < (uint32_t)L) atomicAdd(&sm.cnt[d], 1u);
+            if (d < (uint32_t)L) atomicAdd(&sm.cnt[d >> 1], 1u << ((d & 1u) * 16u));   // W < 65536
         }
         __syncthreads();
     }
-    uint64_t key[PER];
+    // keys of y (the element's id completes the order): 32 bits per element
+    uint32_t key[PER];
     uint64_t best = 0ull;
     bool nan = false;
+    const uint16_t *cnt16 = reinterpret_cast<const uint16_t *>(sm.cnt);
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const int i = u * NT + t;
-        key[u] = 0ull;
+        key[u] = 0u;
         if (i < L) {
             float xv = x[u];
             if (has_pen) {
-                const uint32_t n = sm.cnt[i];
+                const uint32_t n = cnt16[i];
                 if (n) xv = penalize(xv, n, s.rep);
             }
             x[u] = xv;
             const float y = xv / s.T;
             nan |= isnan(y);
-            key[u] = sel_key(y, (uint32_t)(c0 + i));
-            best = key[u] > best ? key[u] : best;
+            key[u] = f2key(y);
+            const uint64_t k = ((uint64_t)key[u] << 32) | (uint64_t)(~(uint32_t)(c0 + i));
+            best = k > best ? k : best;
         }
     }
-    sm.tmax[t] = best;
-    if (__any(nan) && (t & 63) == 0) sm.nan = 1;
+    // tau = the kp-th largest thread maximum (keys carry the id: all
+    // distinct).  A histogram of the maxima's y keys over their range finds
+    // an edge with at least kp maxima at or above it; those maxima are
+    // ranked among themselves.
+    const bool has = t < L;                            // threads without elements have best 0
+    const uint32_t bk = (uint32_t)(best >> 32);
+    const int lane = t & 63, w = t >> 6;
+    {
+        uint32_t lo = has ? bk : 0xffffffffu, hi = has ? bk : 0u;
+        for (int d = 32; d > 0; d >>= 1) {
+            lo = min(lo, (uint32_t)__shfl_xor((int)lo, d, 64));
+            hi = max(hi, (uint32_t)__shfl_xor((int)hi, d, 64));
+        }
+        if (lane == 0) { sm.red[2 * w] = lo; sm.red[2 * w + 1] = hi; }
+    }
+    for (int i = t; i < kSelHist; i += NT) sm.hist[i] = 0u;
+    if (__any(nan) && lane == 0) sm.nan = 1;
+    if (t == 0) sm.nlist = 0;
+    __syncthreads();
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+    for (int i = 0; i < NT / 64; i++) { kmin = min(kmin, sm.red[2 * i]); kmax = max(kmax, sm.red[2 * i + 1]); }
+    const uint64_t range = (uint64_t)(kmax - kmin) + 1u;
+    if (has) atomicAdd(&sm.hist[(uint32_t)(((uint64_t)(bk - kmin) * kSelHist) / range)], 1u);
+    __syncthreads();
+    if (w == 0) {
+        // lane l sums bins [32 l, 32 l + 32); suffix sums over lanes find the
+        // bin j holding the kp-th largest maximum
+        constexpr int kPerLane = kSelHist / 64;
+        uint32_t own = 0u;
+#pragma unroll 8
+        for (int i = 0; i < kPerLane; i++) own += sm.hist[lane * kPerLane + i];
+        uint32_t suf = own;                            // bins of lanes >= lane
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_down((int)suf, d, 64);
+            if (lane + d < 64) suf += o;
+        }
+        const uint32_t above = suf - own;              // bins of lanes > lane
+        if (suf >= (uint32_t)s.kp && above < (uint32_t)s.kp) {
+            uint32_t acc = above;
+            int j = lane * kPerLane;
+            for (int i = kPerLane - 1; i >= 0; i--) {
+                acc += sm.hist[lane * kPerLane + i];
+                if (acc >= (uint32_t)s.kp) { j = lane * kPerLane + i; break; }
+            }
+            // the smallest key whose bin is >= j
+            sm.edge = kmin + (uint32_t)(((uint64_t)j * range + kSelHist - 1) / kSelHist);
+        }
+    }
+    __syncthreads();
+    if (has && bk >= sm.edge) sm.tmax[atomicAdd(&sm.nlist, 1)] = best;
     __syncthreads();
     {
-        int rk = 0;
-        const ulonglong2 *t2 = reinterpret_cast<const ulonglong2 *>(sm.tmax);
-#pragma unroll 8
-        for (int j = 0; j < NT / 2; j++) {
-            const ulonglong2 v = t2[j];
-            rk += (v.x > best) + (v.y > best);
+        const int nl = sm.nlist;
+        for (int i = t; i < nl; i += NT) {
+            const uint64_t me = sm.tmax[i];
+            int rk = 0;
+            for (int j = 0; j < nl; j++) rk += sm.tmax[j] > me;
+            if (rk == s.kp - 1) sm.tau = me;
         }
-        if (rk == s.kp - 1) sm.tau = best;             // threads without elements have best 0
     }
     __syncthreads();
     const uint64_t tau = sm.tau;
 #pragma unroll
     for (int u = 0; u < PER; u++) {
-        if (key[u] >= tau && key[u] != 0ull) {
+        const int i = u * NT + t;
+        const uint64_t k = ((uint64_t)key[u] << 32) | (uint64_t)(~(uint32_t)(c0 + i));
+        if (i < L && k >= tau) {
             const int pos = atomicAdd(&sm.ncand, 1);
-            sm.cand[pos] = key[u];
+            sm.cand[pos] = k;
             sm.candx[pos] = x[u];
         }
     }
