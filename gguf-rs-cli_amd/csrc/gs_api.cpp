@@ -45,6 +45,8 @@ struct gs_sampler {
     void **retired;              // buffers replaced after a capture, freed by gs_sampler_destroy
     size_t n_retired, cap_retired;
     int n_cus;                   // compute units of the device (0: not queried yet)
+    hipStream_t side;            // batches with per-row params: small rows beside the full rows
+    hipEvent_t ev_fork, ev_join;
 };
 
 namespace gs { int init_static_scratch(int device); }
@@ -176,6 +178,12 @@ int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out)
     s->state = seed;
     if (hipGetDevice(&s->device) != hipSuccess) { delete s; return GS_ERR_HIP; }
     if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) { delete s; return GS_ERR_HIP; }
+    if (hipStreamCreateWithFlags(&s->side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&s->ev_fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s->ev_join, hipEventDisableTiming) != hipSuccess) {
+        gs_sampler_destroy(s);
+        return GS_ERR_HIP;
+    }
     // set-up of gs_sample_batch_noalloc's scratch on this device (once per device)
     if (gs::init_static_scratch(s->device) != GS_OK) { (void)hipStreamDestroy(s->stream); delete s; return GS_ERR_HIP; }
     if (hipHostMalloc((void **)&s->h_tok, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
@@ -213,6 +221,10 @@ int gs_sampler_destroy(gs_sampler *s)
     for (size_t i = 0; i < s->n_retired; i++) (void)hipFree(s->retired[i]);
     free(s->retired);
     if (s->h_tok) (void)hipHostFree(s->h_tok);
+    if (s->side) (void)hipStreamSynchronize(s->side);
+    if (s->ev_fork) (void)hipEventDestroy(s->ev_fork);
+    if (s->ev_join) (void)hipEventDestroy(s->ev_join);
+    if (s->side) (void)hipStreamDestroy(s->side);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     (void)hipSetDevice(dev);
     delete s;
@@ -566,10 +578,13 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
     } else {
         if (full) { s->fb_rows = B; s->fb_last = bf.fb; }
         else a.fb = nullptr;            // no full-vocabulary row: the flags are not written
+        const hipStream_t st = (hipStream_t)stream;
         const hipError_t le =
             chunked ? gs::launch_chunked(a, (int)B, (float *)bf.split,
-                                         (uint32_t *)((float *)bf.split + B * gs::chunk_stride(V)), (hipStream_t)stream)
-                    : gs::launch_sample_rows(a, (int)B, (hipStream_t)stream);
+                                         (uint32_t *)((float *)bf.split + B * gs::chunk_stride(V)), st, s->side,
+                                         s->ev_fork, s->ev_join)
+            : d_params ? gs::launch_sample_rows_forked(a, (int)B, st, s->side, s->ev_fork, s->ev_join)
+                       : gs::launch_sample_rows(a, (int)B, st);
         if (le != hipSuccess) return GS_ERR_HIP;
     }
     if (!d_u && s->params.temperature > 0.0f) s->state = gs::lcg_jump(s->state, B);

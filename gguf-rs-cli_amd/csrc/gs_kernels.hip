@@ -1714,6 +1714,20 @@ hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st)
     }
     return hipGetLastError();
 }
+hipError_t launch_sample_rows_forked(const RowArgs &a, int B, hipStream_t st, hipStream_t side, hipEvent_t fork,
+                                    hipEvent_t join)
+{
+    // the full-vocabulary rows on st; the small-path rows on `side` at the
+    // same time (the CUs the full rows leave idle); the sort path after both
+    if (hipEventRecord(fork, st) != hipSuccess || hipStreamWaitEvent(side, fork, 0) != hipSuccess)
+        return hipGetLastError();
+    hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(sample_rows_kernel<kModeSmall>, dim3(B), dim3(kThreads), 0, side, a);
+    if (hipEventRecord(join, side) != hipSuccess || hipStreamWaitEvent(st, join, 0) != hipSuccess)
+        return hipGetLastError();
+    hipLaunchKernelGGL(sample_rows_kernel<kModeSort>, dim3(B), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
 hipError_t launch_detail_rows(const RowArgs &a, int B, hipStream_t st)
 {
     hipLaunchKernelGGL(sample_rows_kernel<kModeDetail>, dim3(B), dim3(kThreads), 0, st, a);
@@ -1753,7 +1767,8 @@ hipError_t launch_split(const RowArgs &a, int B, float *vrow, uint32_t *vidx, hi
                        (const uint32_t *)vidx, vld, nch);
     return hipGetLastError();
 }
-hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st)
+hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st, hipStream_t side,
+                          hipEvent_t fork, hipEvent_t join)
 {
     const int nch = chunk_count((size_t)a.V);
     const size_t vld = chunk_stride((size_t)a.V);
@@ -1763,7 +1778,12 @@ hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStre
     a.cvidx = vidx;
     a.cvld = vld;
     a.cnch = nch;
-    return launch_sample_rows(a, B, st);   // the virtual rows go through the small kernel
+    // the virtual rows go through the small kernel (in order: a fork and
+    // join of streams costs more than the short small-row kernel would gain)
+    (void)side;
+    (void)fork;
+    (void)join;
+    return launch_sample_rows(a, B, st);
 }
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,
                               const uint32_t *tok, hipStream_t st)

@@ -55,6 +55,11 @@ inline size_t scratch_u32_per_row(size_t V)
 // set, the chunked rows' virtual rows), then the full-vocabulary rows by the
 // exact binned path and, for rows whose checks failed, by the sort path.
 hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st);
+// The same for a batch with per-row params (rows of both kinds): the small
+// rows run on `side` beside the full-vocabulary rows on st (fork / join by
+// the two events, so graph capture records the same dependencies).
+hipError_t launch_sample_rows_forked(const RowArgs &a, int B, hipStream_t st, hipStream_t side, hipEvent_t fork,
+                                    hipEvent_t join);
 // Every row sorted (diagnostic; fills a.det); scratch as the sort path.
 hipError_t launch_detail_rows(const RowArgs &a, int B, hipStream_t st);
 // Single-row register path (B = 1); rows it cannot finish report kStatusRetryHost.
@@ -85,7 +90,8 @@ constexpr uint32_t kChunkMaxK = 128;
 inline int chunk_count(size_t V) { return (int)((V + kChunkL - 1) / kChunkL); }
 inline size_t chunk_stride(size_t V) { return (size_t)chunk_count(V) * kChunkMaxK; }
 inline bool chunk_path_ok(size_t V) { return V > kRegMaxV && chunk_stride(V) <= kSplitMaxWidth; }
-hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st);
+hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st, hipStream_t side,
+                          hipEvent_t fork, hipEvent_t join);
 inline bool chunk_fits(const gs_params &p, size_t V)
 {
     return p.temperature > 0.0f && p.temperature < INFINITY && p.top_k > 0 && (size_t)p.top_k < V &&
