@@ -751,51 +751,132 @@ __device__ __forceinline__ uint32_t f_rank(const uint64_t *gl, uint32_t st, uint
 }
 
 // The walk items of bins [0, nb), in order: the overflow entries, then per
-// bin either its list entries sorted (`lst(b)`: ranked from its list segment
-// [seg, sege)) or one bin item (`item(b)`).  A listed bin's first item
-// offset goes to v1[b].  Returns the item count, -1 if it does not fit.
+// bin either its list entries sorted (`lst(b)`: ranked within its list
+// segment [seg, sege)) or one bin item (`item(b)`).  A listed bin's first
+// item offset goes to v1[b].  Returns the item count, -1 if it does not fit.
+//
+// The listed segments are ranked in LDS: `stage` (stage_cap u64 words of
+// LDS that the caller does not use at this point) holds a table of the
+// segments (bin, staging offset, size, list offset), then their entries,
+// so every entry counts the larger entries of its segment with LDS
+// broadcast reads.  Segments past the staging room (in bin order) are
+// ranked from the list in global memory.
+constexpr int kFTab = 256;            // listed segments in the staging table
+constexpr uint32_t kFStaged = 0x80000000u;   // v1 flag: the bin's segment is staged
+struct FTabEnt { uint32_t x, y, z, w; };      // bin, staging offset, size, list offset
 template <class Lst, class Item>
 __device__ int f_items(RowSmem &sm, const uint64_t *gl, uint64_t *items, size_t icap, int nb, int nov,
-                       Lst lst, Item item)
+                       Lst lst, Item item, uint64_t *stage, int stage_cap, int tsb)
 {
+    (void)tsb;
+    F_TS(tsb + 0);
     FullSmem &f = sm.x.fs;
     const int t = threadIdx.x;
     constexpr int kPer = kFBins / kThreads;
-    uint32_t n[kPer], loc = 0;
+    FTabEnt *tab = reinterpret_cast<FTabEnt *>(stage);
+    int *hdr = reinterpret_cast<int *>(stage + 2 * kFTab);     // [0] staged end, [1] staged segments
+    uint64_t *se = stage + 2 * kFTab + 2;
+    const uint32_t se_cap = (uint32_t)(stage_cap - 2 * kFTab - 2);
+    uint32_t n[kPer], sz[kPer], loc = 0, nl = 0, szl = 0;
+    bool isl[kPer];
 #pragma unroll
     for (int c = 0; c < kPer; c++) {
         const int b = kPer * t + c;
         n[c] = 0u;
-        if (b < nb && f.cnt[b]) n[c] = lst(b) ? f.cnt[b] : (item(b) ? 1u : 0u);
+        isl[c] = false;
+        sz[c] = 0u;
+        if (b < nb && f.cnt[b]) {
+            isl[c] = lst(b);
+            n[c] = isl[c] ? f.cnt[b] : (item(b) ? 1u : 0u);
+            if (isl[c]) sz[c] = f.sege[b] - f.seg[b];
+        }
         loc += n[c];
+        nl += isl[c];
+        szl += sz[c];
     }
-    uint32_t tot;
+    if (t == 0) { hdr[0] = 0x7fffffff; hdr[1] = 0; }
+    uint32_t tot, nl_tot, sz_tot;
     uint32_t o = block_excl_u32(loc, &tot, sm) + (uint32_t)nov;
     if ((size_t)tot + nov > icap) return -1;
+    uint32_t ti = block_excl_u32(nl, &nl_tot, sm);
+    uint32_t so = block_excl_u32(szl, &sz_tot, sm);
 #pragma unroll
     for (int c = 0; c < kPer; c++) {
         const int b = kPer * t + c;
         if (n[c]) {
-            if (lst(b)) f.v1[b] = o;
-            else stg(items + o, f_bin_item(b));
+            if (isl[c]) {
+                const bool staged = ti < (uint32_t)kFTab && so + sz[c] <= se_cap;
+                if (staged) {
+                    tab[ti] = FTabEnt{(uint32_t)b, so, sz[c], f.seg[b]};
+                    atomicMax(&hdr[1], (int)ti + 1);
+                } else {
+                    atomicMin(&hdr[0], (int)so);      // staged segments end before this one
+                }
+                f.v1[b] = o | (staged ? kFStaged : 0u);
+                ti++;
+                so += sz[c];
+            } else {
+                stg(items + o, f_bin_item(b));
+            }
         }
         o += n[c];
     }
     __syncthreads();
+    F_TS(tsb + 1);
+    const int nst = hdr[1];
+    const uint32_t send = min((uint32_t)hdr[0], sz_tot);
+    // the staged segment holding staging position j (table in offset order)
+    auto seg_of = [&](uint32_t j) {
+        int lo = 0, hi = nst - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (tab[mid].y <= j) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
+    for (uint32_t j = t; j < send; j += kThreads) {
+        const FTabEnt e = tab[seg_of(j)];
+        se[j] = ldg(gl + e.w + (j - e.y));
+    }
+    // the overflow entries (above the bins), ranked among themselves: their
+    // LDS copy equals the list's first nover entries
     const int nover = f.nover;
     for (int p = t; p < nover; p += kThreads) {
-        const uint64_t en = ldg(gl + p);
-        if (en) stg(items + f_rank(gl, 0u, (uint32_t)nover, en), en);
+        const uint64_t en = f.over[p];
+        if (!en) continue;
+        uint32_t rk = 0u;
+        for (int q = 0; q < nover; q++) rk += f.over[q] > en;
+        stg(items + rk, en);
     }
-    f_list_for_each<4>(gl, (uint32_t)nover, f.list_end, [&](uint32_t, uint64_t en) {
+    __syncthreads();
+    F_TS(tsb + 2);
+    for (uint32_t j = t; j < send; j += kThreads) {
+        const FTabEnt e = tab[seg_of(j)];
+        const uint64_t me = se[j];
+        if (!me) continue;                          // a removed entry
+        uint32_t rk = 0u;
+        const uint64_t *sg = se + e.y;
+        for (uint32_t q = 0; q < e.z; q++) rk += sg[q] > me;
+        if (rk < f.cnt[e.x]) stg(items + (f.v1[e.x] & ~kFStaged) + rk, me);
+        else f.fail = 1;
+    }
+    F_TS(tsb + 3);
+    // segments that were not staged: ranked from the list
+    if (nst < (int)nl_tot) f_list_for_each<4>(gl, (uint32_t)nover, f.list_end, [&](uint32_t, uint64_t en) {
         if (!en) return;
         const int b = f_bin(f_entry_y(en) - f.m0);
-        if (b >= nb || !lst(b)) return;
+        if (b >= nb || !lst(b) || (f.v1[b] & kFStaged)) return;
         const uint32_t rk = f_rank(gl, f.seg[b], f.sege[b], en);
         if (rk < f.cnt[b]) stg(items + f.v1[b] + rk, en);
         else f.fail = 1;
     });
     __threadfence_block();
+    __syncthreads();
+    F_TS(tsb + 4);
+#pragma unroll
+    for (int c = 0; c < kPer; c++)
+        if (isl[c]) f.v1[kPer * t + c] &= ~kFStaged;
     __syncthreads();
     return f.fail ? -1 : (int)tot + nov;
 }
@@ -1191,7 +1272,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     }
     GS_STAMP(12);
     int nov = 0;
-    for (int j = 0; j < nover; j++) nov += ldg(gl + j) != 0ull;
+    for (int j = 0; j < nover; j++) nov += f.over[j] != 0ull;   // (the LDS copy of the list's first nover entries)
     f_bags(sm, gl, c, 1, 1.0f);
     if (f.fail) F_FAIL();
     GS_STAMP(13);
@@ -1203,7 +1284,8 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                         bool ok;
                         const ParFn fn = f_item_fn(f, 1, b, &eb, &ok);
                         return ok && (fn.f0 | fn.f1) != 0u;
-                    });
+                    },
+                    reinterpret_cast<uint64_t *>(f.w23), kFBins, 40);   // w23 and v3: unused until walk 1
     if (N < 0) F_FAIL();
     F_STAT(0, 0);
     F_STAT(1, 0);
@@ -1487,7 +1569,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     N = f_items(sm, gl, items, isz, nb23, nov, lst23, [&](int b) {
         const uint32_t w = f.w23[b];
         return (w & 7u) != kCNone || ((w >> 3) & 7u) != kCNone;
-    });
+    }, reinterpret_cast<uint64_t *>(f.w1), kFBins / 2, 48);   // w1: unused after plan B until walk 2
     GS_STAMP(20);
     if (N < 0) F_FAIL();
     F_STAT(4, N);
