@@ -269,6 +269,25 @@ def bench_gemv(gs, torch, steps=50, warmup=5, cpu=True):
                                "sample": "oracle matvec (src/tensor/dequant.rs:277-318 restated) on %d "
                                          "random rows of the %d, %d threads" % (len(sample), rows, nthr)}
     m.close()
+    # the other K-quant output types at the same shape (timing only; parity
+    # is tests/test_gemv.py's)
+    out["other_qtypes"] = {}
+    for name, qk in (("Q4_K", workloads.Q4_K), ("Q5_K", workloads.Q5_K)):
+        bk = workloads.synth_qblocks(qk, rows, cols, seed=13)
+        mk = gs.QMatrix(qk, bk, rows, cols)
+        del bk
+        for _ in range(warmup):
+            mk.gemv(d_x, d_o, stream=st)
+        e0.record(st)
+        for _ in range(steps):
+            mk.gemv(d_x, d_o, stream=st)
+        e1.record(st)
+        torch.cuda.synchronize()
+        uk = e0.elapsed_time(e1) / steps * 1e3
+        nk = workloads.qmatrix_bytes(qk, rows, cols) + 4 * cols + 4 * rows
+        out["other_qtypes"][name] = {"us": uk, "bytes_per_launch": nk, "GB_per_s": nk / uk / 1e3,
+                                     "frac_of_hbm_peak": nk / uk / 1e3 / PEAK_HBM_GBS}
+        mk.close()
     return out
 
 

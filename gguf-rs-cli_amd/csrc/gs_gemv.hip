@@ -1,6 +1,7 @@
 // gs_gemv.hip -- gfx950 quantized matrix-vector product that produces the
 // logits (the reference's output projection, src/model/llama.rs:333-334 on
-// the GPU path, :405-407 on the CPU path), for Q8_0 and Q6_K weights.
+// the GPU path, :405-407 on the CPU path), for Q8_0, Q4_K, Q5_K and Q6_K
+// weights.
 //
 // HBM-bound: every weight byte is read once per call and nothing else of
 // size moves.  Device layout (rearranged at upload from the GGUF blocks, the
@@ -395,6 +396,164 @@ q80_gemv_lds(const uint8_t *bits, const uint16_t *dq, const float *x, float *out
     }
 }
 
+// ------------------------------------------------------- Q4_K / Q5_K -----
+// Step s of block j (src/tensor/dequant.rs:149-196, a "pair" here) holds the
+// 64 weights 256 j + 64 s + l (sub-block 2s: low nibbles of qs[32 s + l])
+// and 256 j + 64 s + 32 + l (sub-block 2s + 1: high nibbles), l = 0..31;
+// Q5_K adds bit 2s / 2s + 1 of qh[l] as 16.  w = (d * sc) * q - dmin * m.
+// Planes (element e = 4 j + s of a row; rows of 4 nb pairs):
+//   qs: 32 bytes per pair; h (Q5_K): two words per pair, bit l = the fifth
+//   bit of weight l of sub-block 2s / 2s + 1; sm: one word per pair, bytes
+//   sc(2s), m(2s), sc(2s + 1), m(2s + 1); dd: one word per block, d | dmin << 16.
+struct KPlanes {
+    const uint8_t *qs;
+    const uint2 *h;
+    const uint32_t *sm;
+    const uint32_t *dd;
+};
+struct KPair {
+    uint4 a, b;         // qs[32 s .. 32 s + 15], qs[32 s + 16 .. 32 s + 31]
+    uint2 h;
+    uint32_t sm, dd;
+};
+template <bool Q5>
+__device__ __forceinline__ KPair kq_load(const KPlanes &P, uint32_t e)
+{
+    KPair q;
+    q.a = ntl4(P.qs + e * 32u);
+    q.b = ntl4(P.qs + e * 32u + 16u);
+    q.h = Q5 ? ntl2(P.h + e) : make_uint2(0u, 0u);
+    q.sm = __builtin_nontemporal_load(P.sm + e);
+    q.dd = __builtin_nontemporal_load(P.dd + (e >> 2));
+    return q;
+}
+// Bits 0..3 of n to bit 4 of bytes 0..3.
+__device__ __forceinline__ uint32_t kq_hi4(uint32_t n) { return ((n * 0x00204081u) & 0x01010101u) << 4; }
+
+// (d sc_A) sum qA x - (dmin m_A) sum x + the same for sub-block B; xa / xb
+// the pair's x, sa / sb their sums.
+template <bool Q5>
+__device__ __forceinline__ float kq_dot(const KPair &q, const float (&xa)[32], const float (&xb)[32], float sa, float sb)
+{
+    const uint32_t W[8] = {q.a.x, q.a.y, q.a.z, q.a.w, q.b.x, q.b.y, q.b.z, q.b.w};
+    float da = 0.0f, db = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t lo = W[k] & 0x0F0F0F0Fu, hi = (W[k] >> 4) & 0x0F0F0F0Fu;
+        if (Q5) {
+            lo |= kq_hi4((q.h.x >> (4 * k)) & 0xFu);
+            hi |= kq_hi4((q.h.y >> (4 * k)) & 0xFu);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            da = fmaf(ub(lo, t), xa[4 * k + t], da);
+            db = fmaf(ub(hi, t), xb[4 * k + t], db);
+        }
+    }
+    const float d = h2f((uint16_t)(q.dd & 0xffffu)), dmin = h2f((uint16_t)(q.dd >> 16));
+    const float d1 = d * (float)(q.sm & 0xffu), mb1 = dmin * (float)((q.sm >> 8) & 0xffu);     // as the reference
+    const float d2 = d * (float)((q.sm >> 16) & 0xffu), mb2 = dmin * (float)(q.sm >> 24);
+    return fmaf(d1, da, fmaf(-mb1, sa, fmaf(d2, db, -mb2 * sb)));
+}
+__device__ __forceinline__ void kq_xslice(const float *x, int j, int st, float (&xa)[32], float (&xb)[32],
+                                          float *sa, float *sb)
+{
+    const float4 *pa = reinterpret_cast<const float4 *>(x + 256 * j + 64 * st);
+    const float4 *pb = reinterpret_cast<const float4 *>(x + 256 * j + 64 * st + 32);
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 u = pa[i], v = pb[i];
+        xa[4 * i] = u.x; xa[4 * i + 1] = u.y; xa[4 * i + 2] = u.z; xa[4 * i + 3] = u.w;
+        xb[4 * i] = v.x; xb[4 * i + 1] = v.y; xb[4 * i + 2] = v.z; xb[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) { s1 += xa[i]; s2 += xb[i]; }
+    *sa = s1;
+    *sb = s2;
+}
+
+// As q6k_gemv_xreg, a pair per lane (rows of up to 16 blocks).
+template <bool Q5, int kRB, int PF, int NT>
+__global__ void __launch_bounds__(NT)
+kq_gemv_xreg(KPlanes P, const float *x, float *out, int rows, int nb)
+{
+    static_assert(kRB % PF == 0, "ring of PF row buffers, kRB rows per batch");
+    __shared__ float xs[4096];
+    __shared__ float tiles[NT / 64][kRB * 64];
+    const int cols = 256 * nb;
+    for (int i = threadIdx.x; i < cols; i += NT) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (NT / 64);
+    const int gw = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int NQ = 4 * nb;
+    const bool act = lane < NQ;
+    const int qi = act ? lane : 0;
+    float xa[32], xb[32], sa, sb;
+    kq_xslice(xs, qi >> 2, qi & 3, xa, xb, &sa, &sb);
+    const int rpw = (rows + nw - 1) / nw;
+    const int r0 = gw * rpw, r1 = min(rows, r0 + rpw);
+    if (r0 >= r1) return;
+    float *tile = tiles[threadIdx.x >> 6];
+    const uint32_t e1 = (uint32_t)(r1 - 1) * NQ + qi;
+    auto row_e = [&](int r) { return min((uint32_t)r * NQ + qi, e1); };   // past the run: its last row
+    KPair buf[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) buf[i] = kq_load<Q5>(P, row_e(r0 + i));
+    int rb = r0;
+    for (; rb + kRB <= r1; rb += kRB) {
+        float part[kRB];
+#pragma unroll
+        for (int k = 0; k < kRB; k++) {
+            const KPair nxt = kq_load<Q5>(P, row_e(rb + k + PF));
+            part[k] = act ? kq_dot<Q5>(buf[k % PF], xa, xb, sa, sb) : 0.0f;
+            buf[k % PF] = nxt;
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB) out[rb + lane] = v;
+    }
+    if (rb < r1) {
+        float part[kRB];
+#pragma unroll
+        for (int k = 0; k < kRB; k++) {
+            part[k] = 0.0f;
+            if (rb + k < r1 && act) part[k] = kq_dot<Q5>(buf[k % PF], xa, xb, sa, sb);
+            if (k + 1 < kRB && (k + 1) % PF == 0 && rb + k + 1 < r1) {
+#pragma unroll
+                for (int i = 0; i < PF; i++) buf[i] = kq_load<Q5>(P, row_e(rb + k + 1 + i));
+            }
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB && rb + lane < r1) out[rb + lane] = v;
+    }
+}
+
+template <bool Q5>
+__global__ void __launch_bounds__(kGemvThreads)
+kq_gemv_lds(KPlanes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[kMaxCols];
+    const int cols = 256 * nb;
+    for (int i = threadIdx.x; i < cols; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (kGemvThreads / 64);
+    const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+    const int NQ = 4 * nb;
+    for (int r = gw; r < rows; r += nw) {
+        float v = 0.0f;
+        for (int qi = lane; qi < NQ; qi += 64) {
+            float xa[32], xb[32], sa, sb;
+            kq_xslice(xs, qi >> 2, qi & 3, xa, xb, &sa, &sb);
+            v += kq_dot<Q5>(kq_load<Q5>(P, (uint32_t)r * NQ + qi), xa, xb, sa, sb);
+        }
+        v = wave_sum(v);
+        if (lane == 0) out[r] = v;
+    }
+}
+constexpr int kRBK = 8, kPFK = 2, kNTK = 768;   // K-quants: the Q6_K structure
+
 } // namespace gs
 
 // ------------------------------------------------------------- host side ---
@@ -405,9 +564,71 @@ struct gs_qmatrix {
     int cus;                   // compute units: one 1024-thread workgroup each on the register paths
     uint8_t *base;             // one device allocation holding the planes
     gs::Q6Planes q6;           // Q6_K
+    gs::KPlanes kq;            // Q4_K / Q5_K
     const uint8_t *q8;         // Q8_0: int8 quants
-    const uint16_t *d;         // f16 d per block (both types)
+    const uint16_t *d;         // f16 d per block (Q8_0, Q6_K)
 };
+
+namespace {
+// get_scale_min_k4 (src/tensor/dequant.rs:141-148): the 6-bit scale and min
+// of sub-block j from the block's 12 packed bytes.
+void scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t *m)
+{
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+// Q4_K (144-byte blocks) / Q5_K (176) to the K planes (see KPlanes).
+int upload_kquant(bool q5, const uint8_t *src, size_t rows, size_t nb, gs_qmatrix *m)
+{
+    const size_t n = rows * nb, np = 4 * n;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const size_t off_h = al(np * 32), off_sm = off_h + (q5 ? al(np * 8) : 0), off_dd = off_sm + al(np * 4);
+    const size_t total = off_dd + n * 4;
+    uint8_t *h = new (std::nothrow) uint8_t[total];
+    if (!h) return GS_ERR_NOMEM;
+    const size_t bb = q5 ? 176 : 144;
+    for (size_t i = 0; i < n; i++) {
+        const uint8_t *b = src + i * bb;
+        const uint8_t *scales = b + 4, *qh = b + 16, *qs = b + (q5 ? 48 : 16);
+        for (int st = 0; st < 4; st++) {
+            const size_t e = 4 * i + st;
+            memcpy(h + e * 32, qs + 32 * st, 32);
+            uint8_t sc1, m1, sc2, m2;
+            scale_min_k4(2 * st, scales, &sc1, &m1);
+            scale_min_k4(2 * st + 1, scales, &sc2, &m2);
+            const uint32_t w = (uint32_t)sc1 | ((uint32_t)m1 << 8) | ((uint32_t)sc2 << 16) | ((uint32_t)m2 << 24);
+            memcpy(h + off_sm + e * 4, &w, 4);
+            if (q5) {
+                uint32_t ha = 0, hb = 0;
+                for (int l = 0; l < 32; l++) {
+                    ha |= (uint32_t)((qh[l] >> (2 * st)) & 1u) << l;
+                    hb |= (uint32_t)((qh[l] >> (2 * st + 1)) & 1u) << l;
+                }
+                memcpy(h + off_h + e * 8, &ha, 4);
+                memcpy(h + off_h + e * 8 + 4, &hb, 4);
+            }
+        }
+        memcpy(h + off_dd + i * 4, b, 4);   // d, dmin (f16 each)
+    }
+    if (hipMalloc((void **)&m->base, total) != hipSuccess) {
+        (void)hipGetLastError();
+        delete[] h;
+        return GS_ERR_NOMEM;
+    }
+    const hipError_t ce = hipMemcpy(m->base, h, total, hipMemcpyHostToDevice);
+    delete[] h;
+    if (ce != hipSuccess) { (void)hipFree(m->base); m->base = nullptr; return GS_ERR_HIP; }
+    m->kq = gs::KPlanes{m->base, q5 ? (const uint2 *)(m->base + off_h) : nullptr,
+                        (const uint32_t *)(m->base + off_sm), (const uint32_t *)(m->base + off_dd)};
+    return GS_OK;
+}
+} // namespace
 
 extern "C" {
 
@@ -416,7 +637,24 @@ int gs_qmatrix_upload(uint32_t qtype, const void *blocks, size_t rows, size_t co
     if (!out) return GS_ERR_INVALID;
     *out = nullptr;
     if (!blocks || rows == 0 || cols == 0) return GS_ERR_INVALID;
-    if (qtype != GS_QTYPE_Q8_0 && qtype != GS_QTYPE_Q6_K) return GS_ERR_UNSUPPORTED;
+    if (qtype != GS_QTYPE_Q8_0 && qtype != GS_QTYPE_Q6_K && qtype != GS_QTYPE_Q4_K && qtype != GS_QTYPE_Q5_K)
+        return GS_ERR_UNSUPPORTED;
+    if (qtype == GS_QTYPE_Q4_K || qtype == GS_QTYPE_Q5_K) {
+        if (cols % 256 != 0 || cols > (size_t)gs::kMaxCols || rows > 0x7fffffffu) return GS_ERR_UNSUPPORTED;
+        if (rows * (cols / 64) >= (1ull << 27)) return GS_ERR_UNSUPPORTED;   // 32-bit byte offsets of the qs plane
+        gs_qmatrix *m = new (std::nothrow) gs_qmatrix();
+        if (!m) return GS_ERR_NOMEM;
+        m->qtype = qtype; m->rows = rows; m->cols = cols; m->nb = cols / 256;
+        if (hipGetDevice(&m->device) != hipSuccess ||
+            hipDeviceGetAttribute(&m->cus, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess) {
+            delete m; return GS_ERR_HIP;
+        }
+        if (m->cus <= 0) m->cus = 256;
+        const int rc = upload_kquant(qtype == GS_QTYPE_Q5_K, (const uint8_t *)blocks, rows, cols / 256, m);
+        if (rc != GS_OK) { delete m; return rc; }
+        *out = m;
+        return GS_OK;
+    }
     const bool q6 = qtype == GS_QTYPE_Q6_K;
     const size_t bw = q6 ? 256 : 32;        // weights per block
     const size_t bb = q6 ? 210 : 34;        // bytes per GGUF block
@@ -503,7 +741,16 @@ int gs_gemv(const gs_qmatrix *m, const float *d_x, size_t B, float *d_out, void 
     for (size_t b = 0; b < B; b++) {
         const float *x = d_x + b * m->cols;
         float *o = d_out + b * m->rows;
-        if (m->qtype == GS_QTYPE_Q6_K) {
+        if (m->qtype == GS_QTYPE_Q4_K || m->qtype == GS_QTYPE_Q5_K) {
+            const bool q5 = m->qtype == GS_QTYPE_Q5_K;
+            if (4 * nb <= 64) {
+                if (q5) hipLaunchKernelGGL((gs::kq_gemv_xreg<true, gs::kRBK, gs::kPFK, gs::kNTK>), dim3(m->cus), dim3(gs::kNTK), 0, st, m->kq, x, o, rows, nb);
+                else hipLaunchKernelGGL((gs::kq_gemv_xreg<false, gs::kRBK, gs::kPFK, gs::kNTK>), dim3(m->cus), dim3(gs::kNTK), 0, st, m->kq, x, o, rows, nb);
+            } else {
+                if (q5) hipLaunchKernelGGL(gs::kq_gemv_lds<true>, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->kq, x, o, rows, nb);
+                else hipLaunchKernelGGL(gs::kq_gemv_lds<false>, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->kq, x, o, rows, nb);
+            }
+        } else if (m->qtype == GS_QTYPE_Q6_K) {
             if (4 * nb <= 64)
                 hipLaunchKernelGGL((gs::q6k_gemv_xreg<gs::kRB6, gs::kPF6, gs::kNT6>), dim3(m->cus), dim3(gs::kNT6), 0, st, m->q6, x, o, rows, nb);
             else

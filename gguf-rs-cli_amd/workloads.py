@@ -101,9 +101,9 @@ def algorithmic_bytes_per_row(V, W, hetero=False, window_append=False):
 
 # ---- quantized output matrices (the logits projection) ------------------------
 # GGUF block sizes (src/gguf/types.rs:62-71): Q8_0 34 bytes / 32 weights,
-# Q6_K 210 bytes / 256 weights.
-Q8_0, Q6_K = 8, 14
-QBLOCK = {Q8_0: (32, 34), Q6_K: (256, 210)}
+# Q4_K 144, Q5_K 176 and Q6_K 210 bytes / 256 weights.
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+QBLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 
 def qmatrix_bytes(qtype, rows, cols):
@@ -122,6 +122,9 @@ def synth_qblocks(qtype, rows, cols, seed=0, dscale=0.002):
     d = (rng.random(n) * dscale + dscale / 4).astype(np.float16).view(np.uint8).reshape(n, 2)
     if qtype == Q8_0:
         blk[:, 0:2] = d
+    elif qtype in (Q4_K, Q5_K):
+        blk[:, 0:2] = d                                       # d; dmin about a tenth of it
+        blk[:, 2:4] = (rng.random(n) * dscale / 10).astype(np.float16).view(np.uint8).reshape(n, 2)
     else:
         blk[:, 192:208] = rng.integers(-64, 64, size=(n, 16)).astype(np.int8).view(np.uint8)
         blk[:, 208:210] = d

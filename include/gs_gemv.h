@@ -7,21 +7,29 @@
  *
  *   pub fn upload(&mut self, wt: &QuantTensor) -> Option<GpuTensor>   src/gpu/mod.rs:222-238
  *
- * (repacking the blocks with pack_q6k_for_gpu / pack_q8_0_for_gpu,
- * src/tensor/dequant.rs:369-409) and runs
+ * (repacking the blocks with pack_q6k_for_gpu / pack_q8_0_for_gpu /
+ * pack_q4k_for_gpu / pack_q5k_for_gpu, src/tensor/dequant.rs:338-480) and runs
  *
  *   pub fn cmd_gemv(&mut self, wt: &GpuTensor, inp: &ActBuf, out: &ActBuf)   src/gpu/mod.rs:438-443
  *
- * with the Q6_K or Q8_0 shader (src/gpu/q6k_gemv.glsl, src/gpu/q8_0_gemv.glsl).
+ * with the Q6_K, Q8_0, Q4_K or Q5_K shader (src/gpu/q*_gemv.glsl).
  * Its CPU path is QuantTensor::matvec / row_dot (src/tensor/dequant.rs:277-318).
  *
  * Weights are the GGUF tensor's raw blocks (what QuantTensor::data() returns,
  * src/tensor/dequant.rs:265-267): Q8_0 = 34 bytes per 32 weights (f16 d, 32 int8),
- * Q6_K = 210 bytes per 256 weights (ql[128], qh[64], int8 scales[16], f16 d).
+ * Q6_K = 210 bytes per 256 weights (ql[128], qh[64], int8 scales[16], f16 d),
+ * Q4_K = 144 bytes (f16 d, f16 dmin, 12 bytes of 6-bit scales and mins,
+ * qs[128]), Q5_K = 176 bytes (the same with qh[32] before qs).
  * The result is out[r] = sum_c W[r][c] * x[c], W dequantized as the reference
- * does it (Q8_0: q * d; Q6_K: (d * scale) * q); the summation order is the
- * kernel's own, so results agree with the reference's to f32 rounding, not bit
- * for bit.  Same status codes as gs_sampler.h.
+ * does it (Q8_0: q * d; Q6_K: (d * scale) * q; Q4_K / Q5_K: (d * sc) * q -
+ * dmin * m, dq4k / dq5k, src/tensor/dequant.rs:141-196); the summation order
+ * is the kernel's own, so results agree with the reference's to f32 rounding,
+ * not bit for bit.  Q5_K follows the GGUF format where the reference's two
+ * paths cannot: its CPU dq5k indexes qh[32 + l] in a 32-byte slice from the
+ * third step on (a panic, :177,192) and its shader decodes the scales of
+ * sub-blocks 4-7 with another bit layout (q5k_gemv.glsl get_scale_min); here
+ * qh[l] serves every step and the scales are get_scale_min_k4's, as in dq4k.
+ * Same status codes as gs_sampler.h.
  */
 #ifndef GS_GEMV_H
 #define GS_GEMV_H
@@ -35,6 +43,8 @@ extern "C" {
 
 /* Block types, numbered as GgmlType (src/gguf/types.rs:43-48). */
 #define GS_QTYPE_Q8_0  8u
+#define GS_QTYPE_Q4_K  12u
+#define GS_QTYPE_Q5_K  13u
 #define GS_QTYPE_Q6_K  14u
 
 typedef struct gs_qmatrix gs_qmatrix;

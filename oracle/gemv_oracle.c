@@ -1,14 +1,16 @@
 /* gemv_oracle.c -- CPU restatement of gguf-rs-cli's quantized matrix-vector
- * product for the Q8_0 and Q6_K block types (the logits projection,
+ * product for the Q8_0, Q4_K, Q5_K and Q6_K block types (the logits projection,
  * src/model/llama.rs:405-407 on the CPU path).
  * TEST INFRASTRUCTURE ONLY (parity checker); never linked into the product.
  *
  * Follows src/tensor/dequant.rs:
  *   dq80      :86-94   Q8_0 dequantization, w = (q as f32) * d
  *   dq6k      :197-219 Q6_K dequantization, w = (d * (scale as f32)) * q
+ *   get_scale_min_k4 :141-148, dq4k :149-170, dq5k :171-196
+ *                      Q4_K / Q5_K, w = (d * sc) * q - dmin * m
  *   row_dot   :277-313 Q8_0: per block a sequential f32 sum of (q * d) * x,
  *                      then a sequential sum of the block sums;
- *                      other types (Q6_K): dequantize the row, then a
+ *                      other types (K-quants): dequantize the row, then a
  *                      sequential f32 sum of w * x
  *   matvec    :315-318 out[i] = row_dot(i, x), rows in parallel
  * f16 -> f32 is the `half` crate's (2.7.1, Cargo.lock:219) to_f32, an exact
@@ -22,6 +24,8 @@
 #include <string.h>
 
 #define QT_Q8_0 8u
+#define QT_Q4_K 12u
+#define QT_Q5_K 13u
 #define QT_Q6_K 14u
 
 /* IEEE binary16 -> binary32, exact (every f16 is an f32). */
@@ -86,9 +90,96 @@ void oracle_dequant_q6_k(const uint8_t *data, size_t n, float *o)
     }
 }
 
+/* get_scale_min_k4 (dequant.rs:141-148): the 6-bit scale and min of
+ * sub-block j from the 12 packed bytes q. */
+static void scale_min_k4(int j, const uint8_t *q, float *d, float *m)
+{
+    uint8_t a, b;
+    if (j < 4) {
+        a = q[j] & 63;
+        b = q[j + 4] & 63;
+    } else {
+        a = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        b = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+    *d = (float)a;
+    *m = (float)b;
+}
+
+/* dq4k (dequant.rs:149-170): n weights from n/256 blocks of 144 bytes,
+ * w = (df * sc) * q - dmin * m. */
+void oracle_dequant_q4_k(const uint8_t *data, size_t n, float *o)
+{
+    for (size_t b = 0; b < n / 256; b++) {
+        const uint8_t *d = data + b * 144;
+        const float df = oracle_f16_to_f32(rd16(d)), dmin = oracle_f16_to_f32(rd16(d + 2));
+        const uint8_t *scales = d + 4, *qs = d + 16;
+        size_t is = 0, qoff = 0, y = b * 256;
+        for (int it = 0; it < 4; it++) {
+            float sc1, m1, sc2, m2;
+            scale_min_k4((int)is, scales, &sc1, &m1);
+            scale_min_k4((int)is + 1, scales, &sc2, &m2);
+            const float d1 = df * sc1, mb1 = dmin * m1, d2 = df * sc2, mb2 = dmin * m2;
+            for (int l = 0; l < 32; l++) {
+                o[y + l] = d1 * (float)(qs[qoff + l] & 0xF) - mb1;
+                o[y + l + 32] = d2 * (float)(qs[qoff + l] >> 4) - mb2;
+            }
+            is += 2; qoff += 32; y += 64;
+        }
+    }
+}
+
+/* dq5k (dequant.rs:171-196): n weights from n/256 blocks of 176 bytes; the
+ * fifth bit of the two sub-blocks of step j is bit 2j / 2j+1 of qh[l].
+ * One deviation, from the GGUF format: the reference advances its qh offset
+ * by 32 after step 1 (:192), so step 2 indexes qh[32 + l] in the 32-byte qh
+ * slice (:177) and the Rust code panics on every Q5_K block; here qh[l]
+ * serves all four steps, as the format defines (the masks already select
+ * the step's bits).  Parity for Q5_K is therefore pinned to the format by
+ * bit probes, not to the reference. */
+void oracle_dequant_q5_k(const uint8_t *data, size_t n, float *o)
+{
+    for (size_t b = 0; b < n / 256; b++) {
+        const uint8_t *d = data + b * 176;
+        const float df = oracle_f16_to_f32(rd16(d)), dmin = oracle_f16_to_f32(rd16(d + 2));
+        const uint8_t *scales = d + 4, *qh = d + 16, *qs = d + 48;
+        size_t is = 0, qoff = 0, y = b * 256;
+        const size_t qhoff = 0;
+        for (int j = 0; j < 4; j++) {
+            const uint8_t hm1 = (uint8_t)(1u << (j * 2)), hm2 = (uint8_t)(1u << (j * 2 + 1));
+            float sc1, m1, sc2, m2;
+            scale_min_k4((int)is, scales, &sc1, &m1);
+            scale_min_k4((int)is + 1, scales, &sc2, &m2);
+            const float d1 = df * sc1, mb1 = dmin * m1, d2 = df * sc2, mb2 = dmin * m2;
+            for (int l = 0; l < 32; l++) {
+                const float v1 = (float)(qs[qoff + l] & 0xF) + ((qh[qhoff + l] & hm1) ? 16.0f : 0.0f);
+                const float v2 = (float)(qs[qoff + l] >> 4) + ((qh[qhoff + l] & hm2) ? 16.0f : 0.0f);
+                o[y + l] = d1 * v1 - mb1;
+                o[y + l + 32] = d2 * v2 - mb2;
+            }
+            is += 2; qoff += 32; y += 64;
+        }
+    }
+}
+
 static size_t row_bytes(uint32_t qt, size_t cols)
 {
-    return qt == QT_Q8_0 ? cols / 32 * 34 : cols / 256 * 210;
+    switch (qt) {
+    case QT_Q8_0: return cols / 32 * 34;
+    case QT_Q4_K: return cols / 256 * 144;
+    case QT_Q5_K: return cols / 256 * 176;
+    default: return cols / 256 * 210;
+    }
+}
+
+static void dequant(uint32_t qt, const uint8_t *d, size_t n, float *w)
+{
+    switch (qt) {
+    case QT_Q8_0: oracle_dequant_q8_0(d, n, w); break;
+    case QT_Q4_K: oracle_dequant_q4_k(d, n, w); break;
+    case QT_Q5_K: oracle_dequant_q5_k(d, n, w); break;
+    default: oracle_dequant_q6_k(d, n, w); break;
+    }
 }
 
 /* row_dot (dequant.rs:277-313) for one row's blocks.  `w` is scratch for
@@ -106,7 +197,7 @@ static float row_dot(uint32_t qt, const uint8_t *d, size_t cols, const float *x,
         }
         return acc;
     }
-    oracle_dequant_q6_k(d, cols, w);
+    dequant(qt, d, cols, w);      /* K-quants: the row dequantized, then one sequential sum */
     float acc = 0.0f;
     for (size_t i = 0; i < cols; i++) acc += w[i] * x[i];
     return acc;
@@ -127,8 +218,7 @@ float oracle_row_dot(uint32_t qtype, const uint8_t *row_blocks, size_t cols, con
  * and the sum of |w * x| for tolerances. */
 static double row_exact(uint32_t qt, const uint8_t *d, size_t cols, const float *x, float *w, double *abs_sum)
 {
-    if (qt == QT_Q8_0) oracle_dequant_q8_0(d, cols, w);
-    else oracle_dequant_q6_k(d, cols, w);
+    dequant(qt, d, cols, w);
     double s = 0.0, a = 0.0;
     for (size_t i = 0; i < cols; i++) {
         const double p = (double)w[i] * (double)x[i];
@@ -166,7 +256,7 @@ static void *run_rows(void *arg)
 int oracle_matvec(uint32_t qtype, const uint8_t *blocks, size_t rows, size_t cols, const float *x,
                   float *out, double *exact, double *abs_sum, int nthreads)
 {
-    if (qtype != QT_Q8_0 && qtype != QT_Q6_K) return -1;
+    if (qtype != QT_Q8_0 && qtype != QT_Q6_K && qtype != QT_Q4_K && qtype != QT_Q5_K) return -1;
     if (nthreads < 1) nthreads = 1;
     if ((size_t)nthreads > rows) nthreads = rows ? (int)rows : 1;
     pthread_t th[64];

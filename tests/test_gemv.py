@@ -1,7 +1,10 @@
 """The quantized output projection (the logits producer, src/model/llama.rs:333-334):
-CPU pins of the oracle's Q8_0 / Q6_K dequantization and matvec
-(src/tensor/dequant.rs:86-94, 197-219, 277-318), and GPU parity of gs_gemv
-(include/gs_gemv.h) against it.
+CPU pins of the oracle's Q8_0 / Q4_K / Q5_K / Q6_K dequantization and matvec
+(src/tensor/dequant.rs:86-94, 141-219, 277-318), and GPU parity of gs_gemv
+(include/gs_gemv.h) against it.  Q5_K follows the GGUF format where the
+reference cannot (its dq5k indexes past its 32-byte qh slice from the third
+step on, src/tensor/dequant.rs:177,192): its pins are the format's bit
+layout, not reference outputs.
 
 The GPU sums in its own order, so parity is a tolerance: with exact the
 float64 value of the reference's f32 weights times x (oracle.matvec exact=True),
@@ -13,7 +16,7 @@ above the bound.
 import numpy as np
 import pytest
 
-Q8_0, Q6_K = 8, 14
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 
 
 def _f32_bits(a):
@@ -81,6 +84,91 @@ def test_q6k_single_bit_probes(oracle):
                     assert w[diff[0]] - base[diff[0]] == (16 << bit) * 6.0
 
 
+def _k_block(q5, qs=None, qh=None, scales=None, d=1.0, dmin=0.0):
+    b = np.zeros(176 if q5 else 144, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    if scales is not None:
+        b[4:16] = scales
+    if q5 and qh is not None:
+        b[16:48] = qh
+    if qs is not None:
+        b[(48 if q5 else 16):] = qs
+    return b
+
+
+# GGML's packing of the eight 6-bit (scale, min) pairs in 12 bytes, bit by
+# bit: (byte, bit) -> (sub-block, 0 = scale / 1 = min, bit of the value).
+def _k_scale_bits():
+    tab = {}
+    for j in range(4):
+        for bit in range(6):
+            tab[(j, bit)] = (j, 0, bit)                 # bytes 0-3: scales 0-3
+            tab[(j + 4, bit)] = (j, 1, bit)             # bytes 4-7: mins 0-3
+        for bit in (6, 7):
+            tab[(j, bit)] = (j + 4, 0, bit - 2)         # top bits of scales 4-7
+            tab[(j + 4, bit)] = (j + 4, 1, bit - 2)     # top bits of mins 4-7
+        for bit in range(4):
+            tab[(j + 8, bit)] = (j + 4, 0, bit)         # bytes 8-11: low nibbles of scales 4-7
+            tab[(j + 8, bit + 4)] = (j + 4, 1, bit)     # high nibbles: mins 4-7
+    return tab
+
+
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K])
+def test_kquant_scale_min_bit_probes(oracle, qt):
+    """Every bit of the 12 scale bytes changes exactly the 32 weights of the
+    sub-block GGML's layout gives it, by the bit's value times d (scale) or
+    -dmin (min); with all quants 1 (d = 1, dmin = 0.5) a weight is
+    sc - 0.5 m."""
+    q5 = qt == Q5_K
+    qs = np.full(128, 0x11, np.uint8)          # every quant 1
+    base = oracle.dequant(qt, _k_block(q5, qs=qs, d=1.0, dmin=0.5), 256)
+    assert np.all(base == 0.0)
+    for (byte, bit), (sub, kind, vbit) in _k_scale_bits().items():
+        sc = np.zeros(12, np.uint8)
+        sc[byte] = 1 << bit
+        w = oracle.dequant(qt, _k_block(q5, qs=qs, scales=sc, d=1.0, dmin=0.5), 256)
+        diff = np.nonzero(w != base)[0]
+        assert list(diff) == list(range(32 * sub, 32 * sub + 32)), (byte, bit, diff[:4])
+        want = (1 << vbit) * (1.0 if kind == 0 else -0.5)
+        assert np.all(w[diff] == np.float32(want)), (byte, bit, w[diff[0]], want)
+
+
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K])
+def test_kquant_quant_bit_probes(oracle, qt):
+    """Each quant bit moves one weight by the bit's value times d * sc: qs
+    byte 32 s + l holds weight 64 s + l (low nibble) and 64 s + 32 + l (high);
+    for Q5_K bit 2 s / 2 s + 1 of qh[l] is the fifth bit (16) of those two.
+    Scales 1..8 per sub-block (min 0), d = 0.25."""
+    q5 = qt == Q5_K
+    sc = np.zeros(12, np.uint8)
+    sc[0:4] = [1, 2, 3, 4]
+    sc[8:12] = [5, 6, 7, 8]                    # scales 4-7: low nibbles of bytes 8-11
+    scale = np.array([1, 2, 3, 4, 5, 6, 7, 8], np.float32)
+    base = oracle.dequant(qt, _k_block(q5, scales=sc, d=0.25), 256)
+    assert np.all(base == 0.0)
+    for s_ in range(4):
+        for l in (0, 9, 31):
+            for nib in range(2):
+                for bit in range(4):
+                    qs = np.zeros(128, np.uint8)
+                    qs[32 * s_ + l] = 1 << (4 * nib + bit)
+                    w = oracle.dequant(qt, _k_block(q5, qs=qs, scales=sc, d=0.25), 256)
+                    diff = np.nonzero(w != base)[0]
+                    pos = 64 * s_ + 32 * nib + l
+                    assert list(diff) == [pos], (s_, l, nib, bit, diff)
+                    assert w[pos] == np.float32((1 << bit) * 0.25 * scale[2 * s_ + nib])
+            if q5:
+                for nib in range(2):
+                    qh = np.zeros(32, np.uint8)
+                    qh[l] = 1 << (2 * s_ + nib)
+                    w = oracle.dequant(qt, _k_block(q5, qh=qh, scales=sc, d=0.25), 256)
+                    diff = np.nonzero(w != base)[0]
+                    pos = 64 * s_ + 32 * nib + l
+                    assert list(diff) == [pos], (s_, l, nib, diff)
+                    assert w[pos] == np.float32(16 * 0.25 * scale[2 * s_ + nib])
+
+
 def test_q8_0_bytes_and_scale(oracle):
     """Q8_0: byte 2 + i is weight i as int8, times the f16 d in bytes 0-1."""
     q = np.arange(-128, 128, 8, dtype=np.int8)[:32]
@@ -95,13 +183,13 @@ def test_row_dot_order_and_unit_vectors(oracle):
     A unit vector picks one weight exactly."""
     import workloads
     rng = np.random.default_rng(3)
-    for qt, cols in ((Q6_K, 512), (Q8_0, 96)):
+    for qt, cols in ((Q6_K, 512), (Q8_0, 96), (Q4_K, 512), (Q5_K, 512)):
         blocks = workloads.synth_qblocks(qt, 1, cols, seed=5)
         w = oracle.dequant(qt, blocks, cols)
         x = rng.standard_normal(cols).astype(np.float32)
         got = oracle.row_dot(qt, blocks, cols, x)
-        p = (w * x).astype(np.float32) if qt == Q6_K else None
-        if qt == Q6_K:
+        p = (w * x).astype(np.float32) if qt != Q8_0 else None
+        if qt != Q8_0:
             want = np.add.accumulate(p, dtype=np.float32)[-1]
         else:
             q = blocks.reshape(-1, 34)[:, 2:].view(np.int8).astype(np.float32)
@@ -121,7 +209,7 @@ def test_matvec_exact_bound(oracle):
     the exact value; matvec rows equal row_dot."""
     import workloads
     rng = np.random.default_rng(4)
-    for qt, rows, cols in ((Q6_K, 20, 1024), (Q8_0, 20, 1024)):
+    for qt, rows, cols in ((Q6_K, 20, 1024), (Q8_0, 20, 1024), (Q4_K, 20, 1024), (Q5_K, 20, 1024)):
         blocks = workloads.synth_qblocks(qt, rows, cols, seed=6)
         x = rng.standard_normal(cols).astype(np.float32)
         f32 = oracle.matvec(qt, blocks, rows, cols, x, nthreads=2)
@@ -154,6 +242,11 @@ def _gpu_check(gpu, torch, oracle, qt, rows, cols, seed, B=1, x_kind="normal"):
     if qt == Q6_K:
         smax = np.abs(blocks.reshape(-1, 210)[:, 192:208].view(np.int8)).max() * \
             blocks.reshape(-1, 210)[:, 208:210].copy().view(np.float16).astype(np.float64).max()
+    elif qt in (Q4_K, Q5_K):
+        # the kernel takes (d sc) sum q x - (dmin m) sum x per 32 weights
+        kb = blocks.reshape(-1, 176 if qt == Q5_K else 144)
+        dd = kb[:, 0:4].copy().view(np.float16).astype(np.float64)
+        smax = 63.0 * (dd[:, 0].max() + dd[:, 1].max())
     else:
         smax = blocks.reshape(-1, 34)[:, :2].copy().view(np.float16).astype(np.float64).max()
     for b in range(B):
@@ -175,6 +268,14 @@ def _gpu_check(gpu, torch, oracle, qt, rows, cols, seed, B=1, x_kind="normal"):
     (Q8_0, 333, 3584),
     (Q8_0, 77, 32),          # one block per row
     (Q8_0, 200, 8192),       # LDS path
+    (Q4_K, 1000, 3584),      # register path, 56 of 64 lanes
+    (Q4_K, 517, 4096),
+    (Q4_K, 37, 256),
+    (Q4_K, 300, 8192),       # LDS path
+    (Q5_K, 1000, 3584),
+    (Q5_K, 517, 4096),
+    (Q5_K, 37, 256),
+    (Q5_K, 300, 8192),
 ])
 def test_gemv_parity(gpu, torch, oracle, qt, rows, cols):
     _gpu_check(gpu, torch, oracle, qt, rows, cols, seed=rows + cols)
@@ -189,3 +290,5 @@ def test_gemv_inputs(gpu, torch, oracle):
     _gpu_check(gpu, torch, oracle, Q6_K, 64, 3584, seed=3, B=3)
     _gpu_check(gpu, torch, oracle, Q6_K, 5, 1024, seed=4)
     _gpu_check(gpu, torch, oracle, Q8_0, 40000, 1024, seed=5)
+    _gpu_check(gpu, torch, oracle, Q4_K, 2000, 3584, seed=6, x_kind="spiky")
+    _gpu_check(gpu, torch, oracle, Q5_K, 64, 3584, seed=7, B=3)
