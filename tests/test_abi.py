@@ -41,7 +41,7 @@ def test_gemv_arguments_rejected_without_gpu():
     # cols not a multiple of the block size: the reference's upload returns None
     assert lib.gs_qmatrix_upload(14, blk, 1, 128, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
     assert lib.gs_qmatrix_upload(8, blk, 1, 48, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
-    assert lib.gs_qmatrix_upload(12, blk, 1, 256, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
+    assert lib.gs_qmatrix_upload(11, blk, 1, 256, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED   # Q3_K
     assert lib.gs_qmatrix_upload(14, blk, 1, 256 * 65, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
     assert lib.gs_qmatrix_destroy(None) == gs_sampler.GS_ERR_INVALID
     assert lib.gs_gemv(None, None, 1, None, None) == gs_sampler.GS_ERR_INVALID
