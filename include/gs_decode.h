@@ -112,7 +112,8 @@ int gs_decode_commit(gs_sampler *s, const gs_params *d_params, const gs_decode_c
 /* One whole decode step, stream-ordered and free of host synchronisation
  * and allocation (call gs_sampler_reserve(s, B, V) first when the rows take
  * the full-vocabulary or split paths):
- *   lm_head != NULL: d_logits[b*V + r] = gs_gemv(lm_head, d_x)   (V = rows of lm_head, ld = V)
+ *   lm_head != NULL: d_logits[b*V + r] = gs_gemv(lm_head, d_x)   (V = rows of lm_head, ld = V;
+ *                    one pass over the matrix per row b: for small B, see gs_gemv)
  *   lm_head == NULL: the caller's logits are already in d_logits (row stride ld)
  *   then gs_sample_batch with the ring window and ctx->u, whose last kernel
  *   commits each row as gs_decode_commit does.

@@ -64,7 +64,10 @@ int gs_qmatrix_shape(const gs_qmatrix *m, uint32_t *qtype, size_t *rows, size_t 
 /* Replaces Gpu::cmd_gemv (src/gpu/mod.rs:438-443): for b < B,
  * d_out[b*rows + r] = sum_c W[r][c] * d_x[b*cols + c].  Device pointers;
  * asynchronous on `stream` (NULL = default stream).  B = 1 is the reference's
- * decode step; each further vector is another pass over the weights. */
+ * decode step; each further vector is another full pass over the weights (a
+ * GEMV per vector, not a GEMM), so this entry is meant for small B: a
+ * batch of hundreds of vectors should bring its own GEMM and hand the logits
+ * to the sampler. */
 int gs_gemv(const gs_qmatrix *m, const float *d_x, size_t B, float *d_out, void *stream);
 
 #ifdef __cplusplus
