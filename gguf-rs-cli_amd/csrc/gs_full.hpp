@@ -990,9 +990,13 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     uint64_t *items1 = gl + lsz;
     uint64_t *items = items1 + isz;
     uint32_t *defer = reinterpret_cast<uint32_t *>(items + isz);
-    const float4 *r4 = reinterpret_cast<const float4 *>(row);
-    const int n4 = V >> 2;
-    if (n4 == 0) F_FAIL();
+    // the row need only be 4-byte aligned: the float4 passes start at the
+    // first 16-byte boundary (element h0 < 4); the elements before it are
+    // visited one per thread
+    const int h0 = (int)(((16u - ((uint32_t)reinterpret_cast<uintptr_t>(row) & 15u)) & 15u) >> 2);
+    const float4 *r4 = reinterpret_cast<const float4 *>(row + h0);
+    const int n4 = (V - h0) >> 2;
+    if (V < h0 || n4 == 0) F_FAIL();
     auto ydiv = [&](float x) { return t_one ? x : x / T; };
     auto pen_y = [&](int s) { return ydiv(__uint_as_float(sm.hval[s])); };
 
@@ -1041,14 +1045,15 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
         for (int u = 0; u < kUnroll; u++) {
             const int q = base + u * kThreads + t;
             if (q < n4) {
-                visit1(4 * q + 0, ydiv(v[u].x));
-                visit1(4 * q + 1, ydiv(v[u].y));
-                visit1(4 * q + 2, ydiv(v[u].z));
-                visit1(4 * q + 3, ydiv(v[u].w));
+                visit1(h0 + 4 * q + 0, ydiv(v[u].x));
+                visit1(h0 + 4 * q + 1, ydiv(v[u].y));
+                visit1(h0 + 4 * q + 2, ydiv(v[u].z));
+                visit1(h0 + 4 * q + 3, ydiv(v[u].w));
             }
         }
     }
-    for (int i = (n4 << 2) + t; i < V; i += kThreads) visit1(i, ydiv(ldg(row + i)));
+    for (int i = h0 + (n4 << 2) + t; i < V; i += kThreads) visit1(i, ydiv(ldg(row + i)));
+    if (t < h0) visit1(t, ydiv(ldg(row + t)));
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {
             if (sm.hkey[s] == kEmpty) continue;
@@ -1240,8 +1245,8 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             if (slot < lsz) stg(gl + slot, f_entry(y, (uint32_t)i));
         }
     };
-    if (t_one) row_for_each(row, V, true, visit2);
-    else row_for_each(row, V, true, [&](int i, float x) { visit2(i, x / T); });
+    if (t_one) row_for_each_any(row, V, visit2);
+    else row_for_each_any(row, V, [&](int i, float x) { visit2(i, x / T); });
     __syncthreads();
     if (has_pen) {
         // the raw values of penalized ids leave: listed entries are zeroed,
@@ -1517,8 +1522,8 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             }
         }
     };
-    if (t_one) row_for_each(row, V, true, [&](int i, float y) { visit3(i, y, 0u); });
-    else row_for_each(row, V, true, [&](int i, float x) { visit3(i, x / T, 0u); });
+    if (t_one) row_for_each_any(row, V, [&](int i, float y) { visit3(i, y, 0u); });
+    else row_for_each_any(row, V, [&](int i, float x) { visit3(i, x / T, 0u); });
     __syncthreads();
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {

@@ -215,6 +215,17 @@ __device__ __forceinline__ void row_for_each(const float *row, int V, bool align
     }
 }
 
+// f(i, row[i]) for every element of a row that is only 4-byte aligned: the
+// first h < 4 elements (up to the next 16-byte boundary) one per thread, the
+// body as float4, the last (V - h) % 4 one per thread.
+template <class F>
+__device__ __forceinline__ void row_for_each_any(const float *row, int V, F f)
+{
+    const int h = min(V, (int)(((16u - ((uint32_t)reinterpret_cast<uintptr_t>(row) & 15u)) & 15u) >> 2));
+    if ((int)threadIdx.x < h) f((int)threadIdx.x, ldg(row + threadIdx.x));
+    row_for_each(row + h, V - h, true, [&](int i, float x) { f(i + h, x); });
+}
+
 // Two-phase visit of a 16-byte aligned row: for each float4, cls(y) is
 // evaluated for the four values first (pure, so their LDS reads issue
 // together), then act(i, y, c) performs the side effects in index order.
@@ -1407,7 +1418,7 @@ sample_rows_kernel(RowArgs a)
     } else if (MODE == kModeBins) {
         bool done = false;
         if (sm.flag_nan) { status = GS_ERR_NAN; done = true; }
-        else if (aligned && keep == V) {
+        else if (keep == V && ((reinterpret_cast<uintptr_t>(row) & 3u) == 0)) {
             uint64_t *gl = reinterpret_cast<uint64_t *>(a.scratch + (size_t)b * a.scratch_stride);
             const uint32_t lcap = (uint32_t)(a.scratch_stride / 2);
 #ifdef GS_FULL_V1
