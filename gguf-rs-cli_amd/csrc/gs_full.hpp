@@ -891,7 +891,10 @@ __device__ void f_bags(RowSmem &sm, const uint64_t *gl, const FSeq &c, int sq, f
     FullSmem &f = sm.x.fs;
     const int t = threadIdx.x, lane = lane_id();
     uint32_t *val = sq == 3 ? f.v3 : f.v1;
+    const int tsb = 54 + 3 * sq;   // timing builds: 57.. (seq 1), 60.. (seq 2), 63 (seq 3)
+    (void)tsb;
     if (t == 0) f.nties = 0;
+    F_TS(tsb);
     __syncthreads();
     auto grid = [&](int b) {
         return sq == 1 ? (int)((f.w1[b] >> 16) & 255u) - 128 : (int)f.ex[b][sq - 2] - 128;
@@ -901,8 +904,15 @@ __device__ void f_bags(RowSmem &sm, const uint64_t *gl, const FSeq &c, int sq, f
         const float y = f_entry_y(en);
         const int b = f_bin(y - f.m0);
         if (f_cls(f.w1[b], f.w23[b], sq) != kCBag) return;
-        uint32_t dn, up;
-        f_incs(f_val(c, sq, y, s2), grid(b), &dn, &up);
+        // the increment from the compensated fast exp (relative error below
+        // kExpErr, plus half an ulp per division) when that decides its
+        // rounding; else (near a half step, where a rounding tie may be, or
+        // from 2^23 up) from the exact summand
+        uint32_t dn, up, k;
+        const float af = fast_exp(y - c.m);
+        const float vf = sq == 1 ? af : ((sq == 2 || !c.nuc) ? af / c.S : (af / c.S) / s2);
+        if (inc_of(ldexpf(vf, 23 - grid(b)), 2.0f * kExpErr, &k)) dn = up = k;
+        else f_incs(f_val(c, sq, y, s2), grid(b), &dn, &up);
         if (dn >= (1u << 24)) { f.fail = 1; return; }
         if (dn == up) {
             atomicAdd(&val[b], dn);
@@ -913,6 +923,7 @@ __device__ void f_bags(RowSmem &sm, const uint64_t *gl, const FSeq &c, int sq, f
         }
     });
     __syncthreads();
+    F_TS(tsb + 1);
     const int nt = min(f.nties, kTieCap);
     for (int i = wave_id(); i < nt; i += kWaves) {
         const uint32_t key = f.ties[i].key;
@@ -1310,7 +1321,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
 
     // ---- plan B (seqs 2, 3): masses per bin, the cut and the draw; classes --
     {
-        // exact masses of the listed-and-sorted bins, in 2^-40 units (u64
+        // masses of the listed-and-sorted bins (fast exp: a prediction), in 2^-40 units (u64
         // sums in w23 and v3: the same result in any order)
         uint64_t *mf = reinterpret_cast<uint64_t *>(f.w23);
         static_assert(offsetof(FullSmem, v3) == offsetof(FullSmem, w23) + 4 * kFBins, "w23, v3 adjacent");
@@ -1321,8 +1332,8 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             if (!en) return;
             const float y = f_entry_y(en);
             const int b = f_bin(y - m0);
-            if ((f.w1[b] & 7u) == kCLst)
-                atomicAdd((unsigned long long *)&mf[b], (unsigned long long)ldexp((double)glibc_expf_tab(y - m, f.exptab), 40));
+            if ((f.w1[b] & 7u) == kCLst)   // (a prediction: the fast exp is close enough)
+                atomicAdd((unsigned long long *)&mf[b], (unsigned long long)ldexpf(fast_exp(y - m), 40));
         });
         F_TS(6);
         double osum = 0.0;
