@@ -186,7 +186,15 @@ def _torch_fast_args(logits, recent):
 
 
 def _stream_handle(stream):
+    """The HIP stream of a call: `stream` (a torch.cuda.Stream or a handle),
+    or by default torch's current stream when torch has initialised the GPU
+    (so calls order with torch's work, inside torch.cuda.stream() blocks and
+    under graph capture), else the NULL stream."""
     if stream is None:
+        import sys as _sys
+        torch = _sys.modules.get("torch")
+        if torch is not None and torch.cuda.is_initialized():
+            return torch.cuda.current_stream().cuda_stream
         return None
     if isinstance(stream, int):
         return stream
