@@ -547,6 +547,25 @@ def calib_copy(torch, nbytes=1 << 30, reps=5):
     log("calib copy: %d bytes read + %d bytes written per dispatch" % (nbytes, nbytes))
 
 
+def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
+    """Achievable HBM bandwidth on this box: a 1 GiB device-to-device copy
+    (read + write bytes over the median of `reps` copies, HIP events)."""
+    x = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    y.copy_(x)
+    times = []
+    for _ in range(reps):
+        e0.record(st)
+        y.copy_(x)
+        e1.record(st)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3)
+    del x, y
+    return 2 * nbytes / float(np.median(times)) / 1e9
+
+
 def cpu_baseline(c3):
     """The oracle (C restatement of src/sampler.rs, full sort per row) over
     the whole c3 batch, once with all host threads (<= 16) and once on one
@@ -636,6 +655,8 @@ def main():
     dstep = bench_decode(gs, torch, cpu=not args.no_cpu, gemv_us=gemv["us"])
     log("decode step: %.1f us (graph), %.1f us (eager), sampler alone %.1f us" % (
         dstep["us_per_step_graph"], dstep["us_per_step_eager"], dstep["us_sample_batch_entry"]))
+    copy_gbps = copy_bandwidth(torch)
+    log("device copy: %.0f GB/s" % copy_gbps)
     value = c3["B"] / (c3["ms"] / 1e3)
     achieved = c3["bytes"] / (c3["ms"] / 1e3) / 1e9
     out = {
@@ -658,7 +679,8 @@ def main():
                    "sort_path_rows": c3["sort_rows"], "tie_rows": c3["tie_rows"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": profiled_traffic(),
-                     "kernel": "gs::sample_rows_kernel", "bytes_per_launch": c3["bytes"]},
+                     "kernel": "gs::sample_rows_kernel", "bytes_per_launch": c3["bytes"],
+                     "copy_GBps": copy_gbps, "frac_of_copy": achieved / copy_gbps},
         "c1_latency": {"p50_us": c1["p50_us"], "p90_us": c1["p90_us"], "call": "gs_sample via the C ABI",
                        "p50_us_python_wrapper": c1["p50_us_python"],
                        "kernel_us_batch_entry": c1k,
