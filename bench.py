@@ -611,6 +611,8 @@ def main():
                     help="only the Q6_K logits projection (for profiling)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the graph-captured decode step (for profiling)")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="only the c2, c4 and c5 batches (for profiling)")
     ap.add_argument("--digest", action="store_true",
                     help="print the kernel sources' digest (for a profile summary) and exit")
     ap.add_argument("--calib-copy", action="store_true",
@@ -640,6 +642,10 @@ def main():
     if args.gemv_only:
         g = bench_gemv(gs, torch, steps=args.steps, warmup=args.warmup, cpu=False)
         log("gemv: %.1f us, %.0f GB/s" % (g["us"], g["roofline"]["achieved"]))
+        return
+    if args.configs_only:
+        for name, r in bench_configs(gs, torch).items():
+            log("%s: %s" % (name, json.dumps(r)))
         return
     c3 = bench_c3(gs, torch, args.steps, args.warmup)
     log("c3: %.3f ms/step" % c3["ms"])

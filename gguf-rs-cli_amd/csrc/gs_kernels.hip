@@ -40,7 +40,8 @@ constexpr int kHashSlots = 2 * kMaxWindow;     // open addressing, load <= 1/2
 constexpr int kHistBins = 4096;                 // 12-bit radix digits
 constexpr int kCandCap = 2048;                  // LDS candidate capacity
 constexpr uint32_t kEmpty = 0xffffffffu;
-constexpr int kPenBitsWords = 1024;             // bitmap of ids < 32768 (the register-resident rows)
+constexpr int kPenBitsWords = 8192;             // bitmap of ids < 262144 (the register and streamed rows)
+constexpr int kPenBitsTable = 1024;             // the part build_penalty keeps (ids < 32768)
 
 struct TopkSmem {
     union alignas(16) {
@@ -69,6 +70,7 @@ struct RowSmem {
     double red_f64[kWaves];
     alignas(16) float fin[256];                 // finish_wave: the values being accumulated
     int tok;
+    int flag_snan;                              // a NaN in the streamed part of a row (topk_row_reg)
     union {
         TopkSmem tk;
         FullSmem fs;
@@ -111,13 +113,13 @@ __device__ __forceinline__ PenLoad pen_load(const float *row, int V, const uint3
 
 // Build the penalty table for this row (src/sampler.rs:23-30): an LDS hash of
 // id -> penalized logit, the occurrence count applied one op at a time, and
-// a bitmap of the penalized ids below 32 * kPenBitsWords.  sm.nuniq receives
+// a bitmap of the penalized ids below 32 * kPenBitsTable.  sm.nuniq receives
 // the number of distinct ids.
 __device__ void build_penalty(RowSmem &sm, PenLoad pl, float T, float pen)
 {
     const int t = threadIdx.x;
     for (int i = t; i < kHashSlots; i += kThreads) { sm.hkey[i] = kEmpty; sm.hval[i] = 0; }
-    for (int i = t; i < kPenBitsWords; i += kThreads) sm.x.tk.pbits[i] = 0u;
+    for (int i = t; i < kPenBitsTable; i += kThreads) sm.x.tk.pbits[i] = 0u;
     if (t == 0) sm.nuniq = 0;
     __syncthreads();
     if (pl.id != kEmpty) {
@@ -133,7 +135,7 @@ __device__ void build_penalty(RowSmem &sm, PenLoad pl, float T, float pen)
             }
             h = (h + 1) & (kHashSlots - 1);
         }
-        if (id < 32u * kPenBitsWords) atomicOr(&sm.x.tk.pbits[id >> 5], 1u << (id & 31u));
+        if (id < 32u * kPenBitsTable) atomicOr(&sm.x.tk.pbits[id >> 5], 1u << (id & 31u));
     }
     __syncthreads();
     for (int i = t; i < kHashSlots; i += kThreads) {
@@ -770,15 +772,16 @@ __device__ __forceinline__ float f4c(const float4 &v, int c)
     return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
 }
 // LDS state of topk_row_reg, cleared before the kernel's first barrier.
-__device__ __forceinline__ void reg_clear(RowSmem &sm, bool has_pen)
+__device__ __forceinline__ void reg_clear(RowSmem &sm, bool has_pen, int V)
 {
     const int t = threadIdx.x;
     if (has_pen) {
         for (int i = t; i < kHashSlots; i += kThreads) { sm.hkey[i] = kEmpty; sm.hval[i] = 0u; }
-        for (int i = t; i < kPenBitsWords; i += kThreads) sm.x.tk.pbits[i] = 0u;
+        const int nw = min((V + 31) >> 5, kPenBitsWords);
+        for (int i = t; i < nw; i += kThreads) sm.x.tk.pbits[i] = 0u;
     }
     for (int i = t; i < kSelBins; i += kThreads) sm.x.tk.u.hist[i] = 0u;
-    if (t == 0) sm.ncand = 0;
+    if (t == 0) { sm.ncand = 0; sm.flag_snan = 0; }
 }
 
 // Penalty table of a register row (src/sampler.rs:23-30), built alongside
@@ -799,7 +802,7 @@ __device__ __forceinline__ int pen_insert(RowSmem &sm, const PenLoad &pl, bool h
             }
             h = (h + 1) & (kHashSlots - 1);
         }
-        atomicOr(&sm.x.tk.pbits[pl.id >> 5], 1u << (pl.id & 31u));   // V <= 32768: every id has a bit
+        atomicOr(&sm.x.tk.pbits[pl.id >> 5], 1u << (pl.id & 31u));   // V <= 32 * kPenBitsWords: every id has a bit
     }
     return myslot;
 }
@@ -808,7 +811,7 @@ __device__ __forceinline__ int pen_insert(RowSmem &sm, const PenLoad &pl, bool h
 // logits, the last index among equal maxima (src/sampler.rs:15-19: max_by
 // keeps the last of equal elements; -0 and +0 compare equal).  A NaN
 // anywhere makes the reference panic (V > 1).
-__device__ int greedy_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4], PenLoad pl, int V, bool has_pen,
+__device__ __forceinline__ int greedy_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4], PenLoad pl, int V, bool has_pen,
                               float pen, int *status)
 {
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
@@ -865,11 +868,12 @@ __device__ int greedy_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4
     return ix < 0 ? 0 : ix;
 }
 
-__device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
+__device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
                             float top_p, bool has_pen, float pen, float r, int *status, bool *ok)
 {
     const int t = threadIdx.x, lane = lane_id(), w = wave_id();
     const int n4 = V >> 2;
+    const int n4r = min(n4, kThreads * kRegF4);   // float4s held in registers (the whole row, or its head)
     *ok = false;
     if (pl.id >= (uint32_t)V) pl.id = kEmpty;   // also kEmpty itself
     if (pl.id != kEmpty) pl.raw = ldg(row + pl.id);
@@ -879,7 +883,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
     // a load is still filling waits for that load.
 #pragma unroll
     for (int u = 0; u < kRegF4; u++)
-        if (u * kThreads + t >= n4) rv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (u * kThreads + t >= n4r) rv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     // Thread maximum and NaN test.
     float fmx = -INFINITY;
     uint64_t nanm = 0;
@@ -889,7 +893,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
         nanm |= __ballot(__builtin_isunordered(rv[u].x, rv[u].y));
         nanm |= __ballot(__builtin_isunordered(rv[u].z, rv[u].w));
     }
-    const bool holds = t < n4;
+    const bool holds = t < n4r;
     const uint32_t tk = f2key(fmx);
     {
         const uint32_t wmax = wave_max_u32(holds ? tk : 0u);
@@ -919,7 +923,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
 #pragma unroll
         for (int u = 0; u < kRegF4; u++) {
             const int q = u * kThreads + t;
-            nib[u] = q < n4 ? (sm.x.tk.pbits[q >> 3] >> ((q & 7) * 4)) & 15u : 0u;
+            nib[u] = q < n4r ? (sm.x.tk.pbits[q >> 3] >> ((q & 7) * 4)) & 15u : 0u;
             anyp |= nib[u];
         }
         if (__builtin_expect(anyp != 0u, 0)) {
@@ -933,7 +937,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
         }
     }
     const uint32_t need = (uint32_t)k;
-    const uint32_t nmax = (uint32_t)min(n4, kThreads);      // threads holding elements
+    const uint32_t nmax = (uint32_t)min(n4r, kThreads);     // threads holding elements
     if (anynan) { *ok = true; *status = GS_ERR_NAN; return 0; }
     GS_STAMP(2);
     // Histogram of the thread maxima: bin = (kmax - key) >> shift.  Bin b
@@ -1018,6 +1022,49 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
         }
     }
     GS_SUB0(1);
+    if (n4 > n4r) {
+        // A row longer than the registers hold: the bound of its head (k
+        // unpenalized elements of the head reach it) also bounds the k-th
+        // largest of the whole row.  The rest streams through the same
+        // registers in one pass: slot u is consumed and refilled with the
+        // float4 kRegF4 slots ahead, so kRegF4 loads per thread stay in
+        // flight.  Elements at or above the bound (rare) join the list as
+        // above; a NaN anywhere makes the row an error.
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        bool snan = false;
+        auto ld = [&](int u) { return ldg(r4 + min(n4r + u * kThreads + t, n4 - 1)); };
+        float4 s0 = ld(0), s1 = ld(1), s2 = ld(2), s3 = ld(3), s4 = ld(4), s5 = ld(5), s6 = ld(6), s7 = ld(7);
+        auto slot = [&](float4 &r, int base, int u) __attribute__((always_inline)) {
+            const float4 v = r;
+            const int q = base + u * kThreads + t;
+            r = ldg(r4 + min(q + kRegF4 * kThreads, n4 - 1));
+            const bool in = q < n4;
+            snan |= in && (__builtin_isunordered(v.x, v.y) || __builtin_isunordered(v.z, v.w));
+            const bool hit = in && (v.x >= tf || v.y >= tf || v.z >= tf || v.w >= tf);
+            if (__builtin_expect(__ballot(hit) != 0, 0)) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float x = c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
+                    const bool h = in && x >= tf;
+                    const uint64_t m = __ballot(h);
+                    if (m != 0) {
+                        uint32_t p0 = 0u;
+                        if (lane == 0) p0 = atomicAdd((uint32_t *)&sm.ncand, (uint32_t)__popcll(m));
+                        p0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)p0);
+                        const uint32_t pos = p0 + (uint32_t)__popcll(m & lanemask_lt());
+                        if (h && pos < (uint32_t)kCandCap)
+                            sm.x.tk.cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(4 * q + c);
+                    }
+                }
+            }
+        };
+        static_assert(kRegF4 == 8, "the stream loop names its eight slots");
+        for (int base = n4r; base < n4; base += kRegF4 * kThreads) {
+            slot(s0, base, 0); slot(s1, base, 1); slot(s2, base, 2); slot(s3, base, 3);
+            slot(s4, base, 4); slot(s5, base, 5); slot(s6, base, 6); slot(s7, base, 7);
+        }
+        if (snan) sm.flag_snan = 1;
+    }
     constexpr uint32_t kPenFlag = 0x80000000u;   // entry holds an already penalized value
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {
@@ -1033,6 +1080,7 @@ __device__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4],
     GS_SUB0(2);
     __syncthreads();
     GS_STAMP(4);
+    if (n4 > n4r && sm.flag_snan) { *ok = true; *status = GS_ERR_NAN; return 0; }
     const int nc = sm.ncand;
     if (nc > kCandCap || nc < k) { __syncthreads(); return 0; }   // the fallback reuses the LDS
     // Raw entries -> (key of y, ~id); a penalized id found in the row is
@@ -1338,8 +1386,13 @@ sample_rows_kernel(RowArgs a)
     const int keep0 = (p.top_k > 0 && p.top_k < (uint32_t)V) ? (int)p.top_k : V;
     const bool regfit = MODE == kModeSmall && V > 1 && (V & 3) == 0 && V <= kThreads * 4 * kRegF4 &&
                         ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+    // Longer top-k rows (up to the penalty bitmap's reach): the head in
+    // registers, the rest streamed once (topk_row_reg).
+    const bool streamfit = MODE == kModeSmall && V > kThreads * 4 * kRegF4 && (V & 3) == 0 &&
+                           V <= 32 * kPenBitsWords && ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
     const bool reg_greedy = regfit && p.temperature <= 0.0f;
-    const bool regpath = (regfit && p.temperature > 0.0f && p.temperature < INFINITY && keep0 < V) || reg_greedy;
+    const bool regpath = ((regfit || streamfit) && p.temperature > 0.0f && p.temperature < INFINITY && keep0 < V) ||
+                         reg_greedy;
     // The register paths issue the window id load first and the row loads
     // after it, and test the id (ids >= V are skipped) only after the first
     // barrier: loads complete in issue order, so a test before the row loads
@@ -1368,7 +1421,7 @@ sample_rows_kernel(RowArgs a)
         for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
     }
     if (has_pen && !regpath) pl = pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W, true);
-    if (regpath) reg_clear(sm, has_pen);   // the register path builds its penalty table itself
+    if (regpath) reg_clear(sm, has_pen, V);   // the register path builds its penalty table itself
     __syncthreads();
     if (has_pen && !regpath) build_penalty(sm, pl, p.temperature > 0.0f ? p.temperature : 1.0f, p.rep_penalty);
     if (wsrc && t < W) pl.id = rid;        // tested against V by the register paths
@@ -1483,7 +1536,7 @@ reg_row_kernel(RowArgs a)
 #pragma unroll
         for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
     }
-    reg_clear(sm, has_pen);
+    reg_clear(sm, has_pen, V);
     __syncthreads();
     GS_STAMP(1);
     PenLoad pl{kEmpty, 0.0f};
@@ -1685,7 +1738,7 @@ __device__ void finish_virtual_row(RowSmem &sm, const RowArgs &a, int b, const g
 #pragma unroll
         for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
     }
-    reg_clear(sm, false);
+    reg_clear(sm, false, V2);
     if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
     __syncthreads();
     const PenLoad pl{kEmpty, 0.0f};
