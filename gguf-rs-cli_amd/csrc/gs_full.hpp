@@ -1069,29 +1069,35 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                 atomicAdd((unsigned long long *)&f.u.mass64[b], (unsigned long long)(fast_exp(dp) * kFMassScale));
         }
     };
-    for (int base = 0; base < n4; base += kThreads * kUnroll) {
-        float4 v[kUnroll];
+    // The loop is instantiated for T == 1 and for a division, so that rows
+    // with T == 1 carry no division (a select would compute it anyway).
+    auto pass1 = [&](auto yf) -> bool {
+        for (int base = 0; base < n4; base += kThreads * kUnroll) {
+            float4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));
-        if (base == 0) {
-            float lm = -INFINITY;
+            for (int u = 0; u < kUnroll; u++) v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));
+            if (base == 0) {
+                float lm = -INFINITY;
 #pragma unroll
-            for (int u = 0; u < kUnroll; u++)
-                if (u * kThreads + t < n4) lm = fmaxf(lm, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
-            m0 = ydiv(f_block_max(lm, sm));
-            if (!isfinite(m0)) F_FAIL();
-        }
+                for (int u = 0; u < kUnroll; u++)
+                    if (u * kThreads + t < n4) lm = fmaxf(lm, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
+                m0 = ydiv(f_block_max(lm, sm));
+                if (!isfinite(m0)) return false;
+            }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int q = base + u * kThreads + t;
-            if (q < n4) {
-                visit1(h0 + 4 * q + 0, ydiv(v[u].x));
-                visit1(h0 + 4 * q + 1, ydiv(v[u].y));
-                visit1(h0 + 4 * q + 2, ydiv(v[u].z));
-                visit1(h0 + 4 * q + 3, ydiv(v[u].w));
+            for (int u = 0; u < kUnroll; u++) {
+                const int q = base + u * kThreads + t;
+                if (q < n4) {
+                    visit1(h0 + 4 * q + 0, yf(v[u].x));
+                    visit1(h0 + 4 * q + 1, yf(v[u].y));
+                    visit1(h0 + 4 * q + 2, yf(v[u].z));
+                    visit1(h0 + 4 * q + 3, yf(v[u].w));
+                }
             }
         }
-    }
+        return true;
+    };
+    if (!(t_one ? pass1([](float x) { return x; }) : pass1([&](float x) { return x / T; }))) F_FAIL();
     for (int i = h0 + (n4 << 2) + t; i < V; i += kThreads) visit1(i, ydiv(ldg(row + i)));
     if (t < h0) visit1(t, ydiv(ldg(row + t)));
     if (has_pen) {
