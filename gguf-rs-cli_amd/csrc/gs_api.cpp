@@ -47,6 +47,7 @@ struct gs_sampler {
     int n_cus;                   // compute units of the device (0: not queried yet)
     hipStream_t side;            // batches with per-row params: small rows beside the full rows
     hipEvent_t ev_fork, ev_join;
+    uint32_t *csync;             // chunked top-k path: per-row chunk counters, zero between calls
 };
 
 namespace gs { int init_static_scratch(int device); }
@@ -184,8 +185,14 @@ int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out)
         gs_sampler_destroy(s);
         return GS_ERR_HIP;
     }
+    if (hipMalloc((void **)&s->csync, 2 * sizeof(uint32_t) * gs::kCSyncRows) != hipSuccess ||
+        hipMemsetAsync(s->csync, 0, 2 * sizeof(uint32_t) * gs::kCSyncRows, s->stream) != hipSuccess ||
+        hipStreamSynchronize(s->stream) != hipSuccess) {
+        gs_sampler_destroy(s);
+        return GS_ERR_HIP;
+    }
     // set-up of gs_sample_batch_noalloc's scratch on this device (once per device)
-    if (gs::init_static_scratch(s->device) != GS_OK) { (void)hipStreamDestroy(s->stream); delete s; return GS_ERR_HIP; }
+    if (gs::init_static_scratch(s->device) != GS_OK) { gs_sampler_destroy(s); return GS_ERR_HIP; }
     if (hipHostMalloc((void **)&s->h_tok, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
         hipHostGetDevicePointer((void **)&s->d_tok_map, s->h_tok, 0) != hipSuccess) {
         gs_sampler_destroy(s);
@@ -218,6 +225,7 @@ int gs_sampler_destroy(gs_sampler *s)
     if (s->scratch) (void)hipFree(s->scratch);
     if (s->fb) (void)hipFree(s->fb);
     if (s->split) (void)hipFree(s->split);
+    if (s->csync) (void)hipFree(s->csync);
     for (size_t i = 0; i < s->n_retired; i++) (void)hipFree(s->retired[i]);
     free(s->retired);
     if (s->h_tok) (void)hipHostFree(s->h_tok);
@@ -579,10 +587,13 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
         if (full) { s->fb_rows = B; s->fb_last = bf.fb; }
         else a.fb = nullptr;            // no full-vocabulary row: the flags are not written
         const hipStream_t st = (hipStream_t)stream;
+        // one launch for the chunked rows where the rows are float4-aligned
+        const bool self = B <= (size_t)gs::kCSyncRows && (V & 3) == 0 && (ld & 3) == 0 &&
+                          ((uintptr_t)d_logits & 15u) == 0 && gs::chunk_stride(V) <= gs::kChunkSelfMaxN;
         const hipError_t le =
             chunked ? gs::launch_chunked(a, (int)B, (float *)bf.split,
-                                         (uint32_t *)((float *)bf.split + B * gs::chunk_stride(V)), st, s->side,
-                                         s->ev_fork, s->ev_join)
+                                         (uint32_t *)((float *)bf.split + B * gs::chunk_stride(V)),
+                                         self ? s->csync : nullptr, st)
             : d_params ? gs::launch_sample_rows_forked(a, (int)B, st, s->side, s->ev_fork, s->ev_join)
                        : gs::launch_sample_rows(a, (int)B, st);
         if (le != hipSuccess) return GS_ERR_HIP;

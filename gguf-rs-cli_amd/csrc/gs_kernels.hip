@@ -75,6 +75,7 @@ struct RowSmem {
         TopkSmem tk;
         FullSmem fs;
     } x;
+    int clast;                                  // chunk_rows_kernel: this block finishes the row
 };
 
 // --------------------------------------------------------------------------
@@ -868,6 +869,9 @@ __device__ __forceinline__ int greedy_row_reg(RowSmem &sm, const float *row, flo
     return ix < 0 ? 0 : ix;
 }
 
+// SEL: select only -- return with the k best, sorted (key of y, ~id), in
+// the first k u64 of sm.x.tk.u.hist and *ok set, without sampling.
+template <bool SEL = false>
 __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float4 (&rv)[kRegF4], PenLoad pl, int V, int k, float T,
                             float top_p, bool has_pen, float pen, float r, int *status, bool *ok)
 {
@@ -1132,6 +1136,7 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
         if (bad) { __syncthreads(); return 0; }
     }
     *ok = true;
+    if (SEL) { *status = GS_OK; return 0; }
     auto yv = [&](int j) { return key2f((uint32_t)(top[j] >> 32)); };
     auto ix = [&](int j) { return ~(uint32_t)top[j]; };
     *status = GS_OK;
@@ -1338,18 +1343,23 @@ __device__ __forceinline__ bool chunk_row(const gs_params &p, int V)
            p.top_k <= kChunkMaxK;
 }
 
+// Row b of a batch by the kernel of mode MODE.  `chunked` (a.chunked, or
+// the chunk kernel's own value) says how rows with chunk_row() true are
+// handled: kChunkedX / kChunkedY sample the row's virtual row (penalized
+// logits x, or scaled logits y), kChunkedSelf leaves them to the chunk
+// kernel, 0 samples them as any other row.
 template <int MODE>
-__global__ void __launch_bounds__(kThreads)
-sample_rows_kernel(RowArgs a)
+__device__ __forceinline__ void sample_row(RowSmem &sm, const RowArgs &a, int b, int chunked)
 {
-    __shared__ RowSmem sm;
-    const int b = blockIdx.x;
     const int t = threadIdx.x;
-    const gs_params p = a.params ? a.params[b] : a.uparams;
-    // A chunked top-k row: its virtual row (the chunks' best kp, penalized,
-    // in index order) is sampled as a row of width nch * kp with no penalty,
-    // and the token maps back through cvidx.
-    const bool crow = MODE == kModeSmall && a.chunked && chunk_row(p, a.V);
+    gs_params p = a.params ? a.params[b] : a.uparams;
+    // A chunked top-k row: its virtual row (the chunks' best kp in index
+    // order) is sampled as a row of width nch * kp with no penalty, and the
+    // token maps back through cvidx.  Scaled values are sampled with T = 1
+    // (y / 1 == y).
+    const bool crow = MODE == kModeSmall && chunked && chunk_row(p, a.V);
+    if (crow && chunked == kChunkedSelf) return;
+    if (crow && chunked == kChunkedY) p.temperature = 1.0f;
     const int V = crow ? a.cnch * (((int)p.top_k + 3) & ~3) : a.V;
     // the detail kernel sorts every row with T > 0 (the rest: the small path)
     const bool sorted_row = MODE == kModeDetail && p.temperature > 0.0f && V >= 2;
@@ -1495,6 +1505,14 @@ sample_rows_kernel(RowArgs a)
 #endif
     if (crow) tok = status == GS_OK ? (int)ldg(a.cvidx + (size_t)b * a.cvld + tok) : 0;
     if (t == 0) store_row(a, b, tok, status);
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(kThreads)
+sample_rows_kernel(RowArgs a)
+{
+    __shared__ RowSmem sm;
+    sample_row<MODE>(sm, a, blockIdx.x, a.chunked);
 }
 
 // Single-row register path as a kernel of its own (B = 1): only the code of
@@ -1721,6 +1739,150 @@ chunk_topk_kernel(RowArgs a, int nch, float *vrow, uint32_t *vidx, size_t vld)
     chunk_select<kThreads, kChunkPer>(sm, s, b, c, c0, L, [row](int i) { return ldg(row + i); });
 }
 
+// Sample virtual row b of scaled logits (chunk_rows_kernel's output: n =
+// nch * kp values y and their ids, in index order): the k best by (y
+// descending, id ascending) -- the order the row's sort gives -- by rank,
+// then the softmax, nucleus and draw of finish_sorted.  A NaN makes the row
+// an error.  n <= kCandCap (kChunkSelfMaxN).  All threads of the block call it.
+static_assert(kChunkSelfMaxN <= kCandCap, "virtual row of the one-launch chunked path");
+__device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int b, const gs_params &p)
+{
+    const int t = threadIdx.x;
+    const int kp = ((int)p.top_k + 3) & ~3;
+    const int n = a.cnch * kp;
+    const float *vr = a.cvrow + (size_t)b * a.cvld;
+    const uint32_t *vi = a.cvidx + (size_t)b * a.cvld;
+    uint64_t *cand = sm.x.tk.cand;
+    int nan = 0;
+    for (int i = t; i < n; i += kThreads) {
+        const float y = __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t *>(vr) + i, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT));
+        nan |= (int)isnan(y);
+        cand[i] = cand_of(f2key(y), __hip_atomic_load(vi + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    if (block_or(nan, sm)) {   // its barriers also complete the list
+        if (t == 0) store_row(a, b, 0, GS_ERR_NAN);
+        return;
+    }
+    const int k = (int)p.top_k;
+    uint64_t *top = reinterpret_cast<uint64_t *>(sm.x.tk.u.hist);
+    for (int i = t; i < n; i += kThreads) {
+        const uint64_t me = cand[i];
+        int rk = 0;
+        for (int j = 0; j < n; j++) rk += cand[j] > me;
+        if (rk < k) top[rk] = me;
+    }
+    __syncthreads();
+    const float r = a.u ? a.u[b] : lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
+    auto yv = [&](int j) { return key2f((uint32_t)(top[j] >> 32)); };
+    auto ix = [&](int j) { return ~(uint32_t)top[j]; };
+    const int tok = finish_sorted(sm, k, yv, ix, p.top_p, r);
+    if (t == 0) store_row(a, b, tok, GS_OK);
+}
+
+// The chunked top-k path in one launch, for rows of V % 4 == 0 in 16-byte
+// aligned rows: block (c, b) takes chunk c of row b (elements [c0, c1),
+// c0 a multiple of 4, at most 32768 of them) through the register path's
+// selection -- the chunk's kp best under the sampler's order, penalized
+// (window ids inside the chunk) and scaled -- and writes their scaled
+// logits y and ids, in index order, to the chunk's kp slots of virtual row
+// b.  The last block of row b to finish (a device-scope counter) samples the
+// virtual row (the order of its slots is the row's index order, so ties
+// resolve as in the row) and clears the counter.  A chunk whose selection
+// cannot be decided sets the row's fallback flag: the finishing block then
+// samples the whole row.  A NaN in a chunk goes to its first slot (the row
+// is an error).
+__global__ void __launch_bounds__(kThreads)
+chunk_rows_kernel(RowArgs a)
+{
+    __shared__ RowSmem sm;
+    const int c = blockIdx.x, b = blockIdx.y;
+    const int t = threadIdx.x;
+    const gs_params p = a.params ? a.params[b] : a.uparams;
+    if (!chunk_row(p, a.V)) return;
+#ifdef GS_TIMING
+#define CR_TS(i) do { if (t == 0 && b == (int)g_row) g_fails[1000 + 8 * c + (i)] = (int)__builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define CR_TS(i) do { } while (0)
+#endif
+    CR_TS(0);
+    const int nch = a.cnch;
+    const int kp = ((int)p.top_k + 3) & ~3;
+    const int q4 = a.V >> 2;
+    const int c0 = 4 * (int)((int64_t)c * q4 / nch);
+    const int L = 4 * (int)((int64_t)(c + 1) * q4 / nch) - c0;
+    const float *row = a.logits + (size_t)b * a.ld + c0;
+    const bool has_pen = p.rep_penalty != 1.0f && a.recent != nullptr;
+    int W = 0;
+    if (has_pen) {
+        W = a.recent_len ? (int)a.recent_len[b] : a.W;
+        if (W > a.W) W = a.W;
+    }
+    // the window id load first, then the chunk's loads (as in the row kernel)
+    uint32_t rid = kEmpty;
+    if (has_pen && W > 0) rid = ldg(a.recent + (size_t)b * a.ld_recent + min(t, W - 1));
+    float4 rv[kRegF4];
+    {
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        const int n4 = L >> 2;
+#pragma unroll
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+    }
+    reg_clear(sm, has_pen, L);
+    if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
+    __syncthreads();
+    PenLoad pl{kEmpty, 0.0f};
+    if (has_pen && t < W) pl.id = rid - (uint32_t)c0;     // ids outside the chunk wrap to >= L: skipped
+    int status = GS_OK;
+    bool ok;
+    CR_TS(1);
+    topk_row_reg<true>(sm, row, rv, pl, L, kp, p.temperature, 1.0f, has_pen, p.rep_penalty, 0.0f, &status, &ok);
+    CR_TS(2);
+    float *vrow = const_cast<float *>(a.cvrow) + (size_t)b * a.cvld + (size_t)c * kp;
+    uint32_t *vidx = const_cast<uint32_t *>(a.cvidx) + (size_t)b * a.cvld + (size_t)c * kp;
+    // The slots are written with device-scope relaxed atomic stores, which
+    // the caches do not hold back (no L2 write-back fence needed); every
+    // wave waits for its stores to complete before the barrier, then one
+    // thread counts the chunk.  The last block reads the slots with
+    // device-scope atomic loads.
+    auto put = [&](int i, float y, uint32_t id) {
+        __hip_atomic_store(reinterpret_cast<uint32_t *>(vrow) + i, __float_as_uint(y), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(vidx + i, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if (ok && status == GS_OK) {
+        const uint64_t *top = reinterpret_cast<const uint64_t *>(sm.x.tk.u.hist);
+        if (t < kp) {
+            const uint64_t e = top[t];
+            const uint32_t id = ~(uint32_t)e;
+            int pos = 0;
+            for (int j = 0; j < kp; j++) pos += (~(uint32_t)top[j]) < id;
+            put(pos, key2f((uint32_t)(e >> 32)), (uint32_t)c0 + id);
+        }
+    } else if (ok) {
+        if (t < kp) put(t, t == 0 ? __builtin_nanf("") : -INFINITY, (uint32_t)c0);
+    } else if (t == 0) {
+        atomicOr(a.csync + 2 * (size_t)b + 1, 1u);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));   // vmcnt(0): this wave's stores are complete
+    __syncthreads();
+    if (t == 0) sm.clast = atomicAdd(a.csync + 2 * (size_t)b, 1u) == (uint32_t)(nch - 1) ? 1 : 0;
+    __syncthreads();
+    CR_TS(3);
+    if (!sm.clast) return;
+    CR_TS(4);
+    const bool whole = __hip_atomic_load(a.csync + 2 * (size_t)b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+    __syncthreads();
+    if (t == 0) {
+        __hip_atomic_store(a.csync + 2 * (size_t)b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.csync + 2 * (size_t)b + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (whole) sample_row<kModeSmall>(sm, a, b, 0);
+    else finish_vrow_y(sm, a, b, p);
+    CR_TS(5);
+}
+
 // Pass 2: sample virtual row b (its width nch * kp is a multiple of 4 and
 // the row is 16-byte aligned; no penalty: the values are already penalized):
 // the register path, else the general top-k paths; the token is mapped
@@ -1824,22 +1986,28 @@ hipError_t launch_split(const RowArgs &a, int B, float *vrow, uint32_t *vidx, hi
                        (const uint32_t *)vidx, vld, nch);
     return hipGetLastError();
 }
-hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st, hipStream_t side,
-                          hipEvent_t fork, hipEvent_t join)
+hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, uint32_t *csync, hipStream_t st)
 {
     const int nch = chunk_count((size_t)a.V);
     const size_t vld = chunk_stride((size_t)a.V);
-    hipLaunchKernelGGL(chunk_topk_kernel, dim3(nch, B), dim3(kThreads), 0, st, a, nch, vrow, vidx, vld);
-    a.chunked = 1;
     a.cvrow = vrow;
     a.cvidx = vidx;
     a.cvld = vld;
     a.cnch = nch;
+    if (csync) {
+        // one launch samples the chunked rows; with per-row params the row
+        // kernels take the batch's other rows (the small kernel skips
+        // the chunked ones)
+        a.chunked = kChunkedSelf;
+        a.csync = csync;
+        hipLaunchKernelGGL(chunk_rows_kernel, dim3(nch, B), dim3(kThreads), 0, st, a);
+        if (!a.params) return hipGetLastError();
+        return launch_sample_rows(a, B, st);
+    }
+    hipLaunchKernelGGL(chunk_topk_kernel, dim3(nch, B), dim3(kThreads), 0, st, a, nch, vrow, vidx, vld);
     // the virtual rows go through the small kernel (in order: a fork and
     // join of streams costs more than the short small-row kernel would gain)
-    (void)side;
-    (void)fork;
-    (void)join;
+    a.chunked = kChunkedX;
     return launch_sample_rows(a, B, st);
 }
 hipError_t launch_window_push(uint32_t *win, int B, size_t ld, int W, size_t pos,

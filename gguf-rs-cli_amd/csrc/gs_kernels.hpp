@@ -35,12 +35,22 @@ struct RowArgs {
     int kwin_n;                    // single-row calls: a host window of W <= kKernWin ids passed
     uint32_t kwin[kKernWin];       // by value here (used instead of `recent` when kwin_n != 0)
     gs_detail det;                 // diagnostic outputs of the detail kernel (gs_sample_detail)
-    int chunked;                   // rows with chunk_row() true are sampled by the chunked top-k path:
+    int chunked;                   // rows with chunk_row() true are sampled by the chunked top-k path
+                                   // (kChunkedX / kChunkedSelf / kChunkedY):
     const float *cvrow;            // its virtual rows (values, ids), stride cvld, cnch chunks
     const uint32_t *cvidx;
     size_t cvld;
     int cnch;
+    uint32_t *csync;               // kChunkedSelf: per row, chunks done and a fallback flag (zero
+                                   // between calls: the finishing block clears them)
 };
+
+// How the row kernels treat rows with chunk_row() true.
+constexpr int kChunkedX = 1;       // sample the virtual row of penalized logits (chunk_topk_kernel)
+constexpr int kChunkedSelf = 2;    // skip: chunk_rows_kernel samples them
+constexpr int kChunkedY = 3;       // sample the virtual row of scaled logits (chunk_rows_kernel)
+constexpr int kCSyncRows = 1024;   // rows of the csync buffer (2 words each)
+constexpr size_t kChunkSelfMaxN = 2048;   // widest virtual row (chunk_stride) of the one-launch path
 
 // Per-row scratch (u32 units) of the full-vocabulary paths: the sort path
 // needs 4V; the exact path its element list and walk items (each V plus
@@ -82,16 +92,18 @@ bool split_fits(const gs_params &p, size_t V);
 // 0 < k <= kChunkMaxK (checked per row on the device, so per-row params
 // work) are cut into nch = chunk_count(V) balanced chunks of at most
 // kChunkL logits; each chunk keeps its best kp = round_up(k, 4) in a virtual
-// row of stride chunk_stride(V) (pass 1, one 1024-thread workgroup per
-// chunk), then one launch of the row kernel samples the virtual rows and
-// every other row of the batch (pass 2).
+// row of stride chunk_stride(V), one 1024-thread workgroup per chunk.  With
+// csync (rows of V % 4 == 0, 16-byte aligned) that launch also samples the
+// row -- its last chunk to finish does -- and with per-row params the row
+// kernels then take the batch's other rows; without it (chunk_topk_kernel)
+// one launch of the row kernels samples the virtual rows and every other
+// row of the batch.
 constexpr int kChunkL = 32768;
 constexpr uint32_t kChunkMaxK = 128;
 inline int chunk_count(size_t V) { return (int)((V + kChunkL - 1) / kChunkL); }
 inline size_t chunk_stride(size_t V) { return (size_t)chunk_count(V) * kChunkMaxK; }
 inline bool chunk_path_ok(size_t V) { return V > kRegMaxV && chunk_stride(V) <= kSplitMaxWidth; }
-hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, hipStream_t st, hipStream_t side,
-                          hipEvent_t fork, hipEvent_t join);
+hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, uint32_t *csync, hipStream_t st);
 inline bool chunk_fits(const gs_params &p, size_t V)
 {
     return p.temperature > 0.0f && p.temperature < INFINITY && p.top_k > 0 && (size_t)p.top_k < V &&

@@ -102,3 +102,43 @@ def test_chunked_nan_row(gpu, torch, oracle):
     ok = [0, 1, 3, 5]
     want = oracle.sample_batch(x[ok], [(0.8, 20, 0.9, 1.0)] * 4, u[ok], nthreads=4, fast_topk=True)
     assert np.array_equal(tok.cpu().numpy()[ok].astype(np.int64), want)
+
+
+def test_chunked_graph_replays(gpu, torch, oracle):
+    """The one-launch chunked path in a HIP graph: its per-row chunk counters
+    return to zero after every call, so each replay (new logits copied in
+    between, eager calls on other batches between the replays) samples
+    exactly.  Rows of both kinds (per-row params) and a row whose chunks
+    fall back to the whole row (all equal)."""
+    import workloads
+    rng = np.random.default_rng(77)
+    V, B = 131072, 12
+    params = workloads.params_rows([(0.8, k, 0.9, 1.2) for k in (40, 128, 1, 7, 0, 200, 40, 64, 3, 100, 40, 2)])
+    rec = rng.integers(0, V, size=(B, 64)).astype(np.uint32)
+    u = rng.random(B).astype(np.float32)
+    d_lg = torch.zeros((B, V), dtype=torch.float32, device="cuda")
+    d_pr = torch.from_numpy(np.ascontiguousarray(params).view(np.uint8)).cuda()
+    d_rec = torch.from_numpy(rec.view(np.int32)).cuda()
+    d_u = torch.from_numpy(u).cuda()
+    tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    s = gpu.Sampler(0.7, 40, 0.9, 1.1, seed=1)
+    s.reserve(B, V)
+    s.sample_batch(d_lg, tok, params=d_pr, recent=d_rec, u=d_u)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s.sample_batch(d_lg, tok, params=d_pr, recent=d_rec, u=d_u)
+    other = torch.randn((5, V), device="cuda")
+    tother = torch.zeros(5, dtype=torch.int32, device="cuda")
+    for rep in range(4):
+        x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+        x[3] = 0.5                                    # the bound cannot be decided: whole-row fallback
+        d_lg.copy_(torch.from_numpy(x))
+        _say("chunked graph replay", rep)
+        tok.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        want = oracle.sample_batch(x, params, u, recent=rec, nthreads=12, fast_topk=True)
+        assert np.array_equal(tok.cpu().numpy().astype(np.int64), want), rep
+        s.sample_batch(other, tother, recent=d_rec[:5], u=d_u[:5])   # eager, uniform params, same sampler
+        torch.cuda.synchronize()
