@@ -551,14 +551,21 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
     a.scratch_stride = gs::scratch_u32_per_row(V);
     a.fb = bf.fb;
     if (hook) a.hook = *hook;
-    // measured on MI355X: the split path (1024-logit chunks) beats the
-    // chunked path up to about 2000 chunks per call (V = 152064: B <= 8;
-    // V = 128256: B <= 16; V = 256000: B <= 4)
-    bool split = !d_params && B <= (size_t)gs::kSplitMaxRows && B * (V / gs::kSplitL) <= gs::kSplitMaxChunks &&
-                 gs::split_fits(s->params, V);
-#ifdef GS_EXP_NOSPLIT
-    split = false;
-#endif
+    // top-k rows of a large vocabulary in a batch with fewer rows than CUs:
+    // chunks of up to 32768 logits, one workgroup each (per-row params: the
+    // kernels pick the rows).  With B >= #CUs one workgroup per row already
+    // fills the chip, and leaves the CUs that a batch's full-vocabulary rows
+    // do not use to its top-k rows.  Float4-aligned rows take the one-launch
+    // form (measured on MI355X faster than the split path at every B).
+    const bool chunk_ok = gs::chunk_path_ok(V) && B < (size_t)num_cus(s) &&
+                          (d_params || gs::chunk_fits(s->params, V));
+    const bool self = chunk_ok && B <= (size_t)gs::kCSyncRows && (V & 3) == 0 && (ld & 3) == 0 &&
+                      ((uintptr_t)d_logits & 15u) == 0 && gs::chunk_stride(V) <= gs::kChunkSelfMaxN;
+    // otherwise, measured on MI355X: the split path (1024-logit chunks)
+    // beats the two-launch chunked path up to about 2000 chunks per call
+    // (V = 152064: B <= 8; V = 128256: B <= 16; V = 256000: B <= 4)
+    bool split = !self && !d_params && B <= (size_t)gs::kSplitMaxRows &&
+                 B * (V / gs::kSplitL) <= gs::kSplitMaxChunks && gs::split_fits(s->params, V);
     const size_t wd = split ? gs::split_width(s->params, V) : 0;
     if (split && bf.split_cap < split_bytes(B, wd)) {
         // the buffers must grow: not with fixed buffers or under stream
@@ -568,13 +575,7 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
         else if ((rc = reserve_split(s, B, wd))) return rc;
         else bf.split = s->split;
     }
-    // top-k rows of a large vocabulary in a batch with fewer rows than CUs:
-    // chunks of up to 32768 logits, one workgroup each (per-row params: the
-    // kernels pick the rows).  With B >= #CUs one workgroup per row already
-    // fills the chip, and leaves the CUs that a batch's full-vocabulary rows
-    // do not use to its top-k rows.
-    bool chunked = !split && gs::chunk_path_ok(V) && B < (size_t)num_cus(s) &&
-                   (d_params || gs::chunk_fits(s->params, V));
+    bool chunked = !split && chunk_ok;
     if (chunked && bf.split_cap < chunk_bytes(B, V)) {
         if (bf.fixed || cap) chunked = false;
         else if ((rc = grow(s, &s->split, &s->split_cap, chunk_bytes(B, V)))) return rc;
@@ -587,9 +588,6 @@ int sample_batch_bufs(gs_sampler *s, const float *d_logits, size_t B, size_t V, 
         if (full) { s->fb_rows = B; s->fb_last = bf.fb; }
         else a.fb = nullptr;            // no full-vocabulary row: the flags are not written
         const hipStream_t st = (hipStream_t)stream;
-        // one launch for the chunked rows where the rows are float4-aligned
-        const bool self = B <= (size_t)gs::kCSyncRows && (V & 3) == 0 && (ld & 3) == 0 &&
-                          ((uintptr_t)d_logits & 15u) == 0 && gs::chunk_stride(V) <= gs::kChunkSelfMaxN;
         const hipError_t le =
             chunked ? gs::launch_chunked(a, (int)B, (float *)bf.split,
                                          (uint32_t *)((float *)bf.split + B * gs::chunk_stride(V)),

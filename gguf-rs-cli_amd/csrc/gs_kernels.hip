@@ -12,6 +12,8 @@
 //                       softmax / nucleus / draw over the sorted row.
 // All sequential f32 sums of the reference are evaluated exactly by
 // block_seqsum (see gs_block.hpp).
+#include <type_traits>
+
 #include "gs_block.hpp"
 #include "gs_kernels.hpp"
 #include "gs_full_smem.hpp"
@@ -1740,9 +1742,9 @@ chunk_topk_kernel(RowArgs a, int nch, float *vrow, uint32_t *vidx, size_t vld)
 }
 
 // Sample virtual row b of scaled logits (chunk_rows_kernel's output: n =
-// nch * kp values y and their ids, in index order): the k best by (y
-// descending, id ascending) -- the order the row's sort gives -- by rank,
-// then the softmax, nucleus and draw of finish_sorted.  A NaN makes the row
+// nch * kp values y and their ids, each chunk's kp sorted by (y
+// descending, id ascending) -- the order the row's sort gives): the k best
+// by rank, then the softmax, nucleus and draw of finish_sorted.  A NaN makes the row
 // an error.  n <= kCandCap (kChunkSelfMaxN).  All threads of the block call it.
 static_assert(kChunkSelfMaxN <= kCandCap, "virtual row of the one-launch chunked path");
 __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int b, const gs_params &p)
@@ -1764,15 +1766,43 @@ __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int
         if (t == 0) store_row(a, b, 0, GS_ERR_NAN);
         return;
     }
+    // Each chunk's kp entries are sorted (descending): an entry's rank is
+    // its place in its chunk plus, for every other chunk, the length of the
+    // prefix of larger entries there (binary lifting over all chunks at once).
     const int k = (int)p.top_k;
+    const int nch = a.cnch;
     uint64_t *top = reinterpret_cast<uint64_t *>(sm.x.tk.u.hist);
-    for (int i = t; i < n; i += kThreads) {
-        const uint64_t me = cand[i];
-        int rk = 0;
-        for (int j = 0; j < n; j++) rk += cand[j] > me;
-        if (rk < k) top[rk] = me;
-    }
+    auto rank_all = [&](auto mc) {
+        constexpr int kMaxCh = decltype(mc)::value;            // chunks searched (>= nch)
+        for (int i = t; i < n; i += kThreads) {
+            const int c = i / kp, j = i - c * kp;
+            if (j >= k) continue;                               // rank >= j >= k
+            const uint64_t me = cand[i];
+            int pos[kMaxCh];
+#pragma unroll
+            for (int c2 = 0; c2 < kMaxCh; c2++) pos[c2] = 0;
+#pragma unroll
+            for (int step = (int)kChunkMaxK; step >= 1; step >>= 1) {
+#pragma unroll
+                for (int c2 = 0; c2 < kMaxCh; c2++) {
+                    const int q = pos[c2] + step;
+                    if (c2 < nch && c2 != c && q <= kp && cand[c2 * kp + q - 1] > me) pos[c2] = q;
+                }
+            }
+            int rk = j;
+#pragma unroll
+            for (int c2 = 0; c2 < kMaxCh; c2++) rk += pos[c2];
+            if (rk < k) top[rk] = me;
+        }
+    };
+    static_assert(kChunkSelfMaxN / kChunkMaxK == 16, "chunk counts of the rank");
+    if (nch <= 4) rank_all(std::integral_constant<int, 4>());
+    else if (nch <= 8) rank_all(std::integral_constant<int, 8>());
+    else rank_all(std::integral_constant<int, 16>());
     __syncthreads();
+#ifdef GS_TIMING
+    if (t == 0 && b == (int)g_row) g_fails[1006] = (int)__builtin_amdgcn_s_memrealtime();
+#endif
     const float r = a.u ? a.u[b] : lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
     auto yv = [&](int j) { return key2f((uint32_t)(top[j] >> 32)); };
     auto ix = [&](int j) { return ~(uint32_t)top[j]; };
@@ -1785,10 +1815,10 @@ __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int
 // c0 a multiple of 4, at most 32768 of them) through the register path's
 // selection -- the chunk's kp best under the sampler's order, penalized
 // (window ids inside the chunk) and scaled -- and writes their scaled
-// logits y and ids, in index order, to the chunk's kp slots of virtual row
-// b.  The last block of row b to finish (a device-scope counter) samples the
-// virtual row (the order of its slots is the row's index order, so ties
-// resolve as in the row) and clears the counter.  A chunk whose selection
+// logits y and ids to the chunk's kp slots of virtual row
+// b, sorted by (y descending, id ascending).  The last block of row b to
+// finish (a device-scope counter) samples the virtual row (finish_vrow_y)
+// and clears the counter.  A chunk whose selection
 // cannot be decided sets the row's fallback flag: the finishing block then
 // samples the whole row.  A NaN in a chunk goes to its first slot (the row
 // is an error).
@@ -1854,10 +1884,7 @@ chunk_rows_kernel(RowArgs a)
         const uint64_t *top = reinterpret_cast<const uint64_t *>(sm.x.tk.u.hist);
         if (t < kp) {
             const uint64_t e = top[t];
-            const uint32_t id = ~(uint32_t)e;
-            int pos = 0;
-            for (int j = 0; j < kp; j++) pos += (~(uint32_t)top[j]) < id;
-            put(pos, key2f((uint32_t)(e >> 32)), (uint32_t)c0 + id);
+            put(t, key2f((uint32_t)(e >> 32)), (uint32_t)c0 + ~(uint32_t)e);
         }
     } else if (ok) {
         if (t < kp) put(t, t == 0 ? __builtin_nanf("") : -INFINITY, (uint32_t)c0);

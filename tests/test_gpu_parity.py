@@ -576,7 +576,7 @@ def test_c5_hip_graph(gpu, torch, oracle):
     assert np.array_equal(win, want_win)
 
 
-# --- split top-k rows (a few rows of a large vocabulary over many workgroups) ---
+# --- a few top-k rows of a large vocabulary over many workgroups (split / chunked) ---
 def _split_rows(rng, B, V, shape):
     if shape == "normal":
         x = rng.standard_normal((B, V)) * 2.0
@@ -602,9 +602,11 @@ def _split_rows(rng, B, V, shape):
     (837999, 1, 40, "spike", 1.0),
 ])
 def test_split_rows(gpu, torch, oracle, V, B, k, shape, T):
-    """Rows of V > 32768 with 0 < k <= 128 and at most 32 rows take the split
-    path: every chunk keeps its best round_up(k, 4) elements.  Penalty window
-    with duplicates, ids on chunk edges and ids >= V."""
+    """Rows of V > 32768 with 0 < k <= 128 in batches of a few rows: rows of
+    V % 4 == 0 take the one-launch chunked path (chunks of up to 32768), the
+    odd vocabularies here the split path (chunks of 1024); every chunk keeps
+    its best round_up(k, 4) elements.  Penalty window with duplicates, ids on
+    chunk edges and ids >= V."""
     rng = np.random.default_rng(V + B + k)
     x = _split_rows(rng, B, V, shape)
     W = 64
