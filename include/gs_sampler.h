@@ -56,7 +56,9 @@ typedef struct gs_sampler gs_sampler;
  * Replaces set_seed (src/sampler.rs:5) plus the four scalars the caller
  * passes on every call (src/main.rs:280).  `seed` initialises the sampler's
  * own copy of the reference LCG (src/sampler.rs:3-12).  The sampler binds to
- * the HIP device current at creation. */
+ * the HIP device current at creation.  Creation allocates the sampler's
+ * streams, its pinned host words and 8 KB of device counters (the chunked
+ * top-k path's), and synchronises once. */
 int gs_sampler_create(const gs_params *params, uint64_t seed, gs_sampler **out);
 int gs_sampler_destroy(gs_sampler *s);
 int gs_sampler_set_params(gs_sampler *s, const gs_params *params);
@@ -147,7 +149,9 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V,
  * Every call on one GPU shares that GPU's array (whichever sampler makes
  * it) and the array keeps the last call's contents: calls that overlap on
  * one GPU (two streams, or two threads) race and must be serialised by the
- * caller.  Nothing in the array needs to start at zero. */
+ * caller.  Nothing in the array needs to start at zero.  The chunked top-k
+ * path's per-row counters (8 KB) are the sampler's own, allocated and
+ * cleared by gs_sampler_create, and each call leaves them at zero. */
 #define GS_NOALLOC_SCRATCH_BYTES (64u << 20)
 int gs_sample_batch_noalloc(gs_sampler *s, const float *d_logits, size_t B, size_t V,
                             size_t ld, const gs_params *d_params,
