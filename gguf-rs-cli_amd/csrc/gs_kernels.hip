@@ -1744,8 +1744,9 @@ chunk_topk_kernel(RowArgs a, int nch, float *vrow, uint32_t *vidx, size_t vld)
 // Sample virtual row b of scaled logits (chunk_rows_kernel's output: n =
 // nch * kp values y and their ids, each chunk's kp sorted by (y
 // descending, id ascending) -- the order the row's sort gives): the k best
-// by rank, then the softmax, nucleus and draw of finish_sorted.  A NaN makes the row
-// an error.  n <= kCandCap (kChunkSelfMaxN).  All threads of the block call it.
+// by rank, then the softmax, nucleus and draw of finish_sorted (the chunks
+// report a NaN through the row's flags instead).  n <= kCandCap
+// (kChunkSelfMaxN).  All threads of the block call it.
 static_assert(kChunkSelfMaxN <= kCandCap, "virtual row of the one-launch chunked path");
 __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int b, const gs_params &p)
 {
@@ -1755,17 +1756,12 @@ __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int
     const float *vr = a.cvrow + (size_t)b * a.cvld;
     const uint32_t *vi = a.cvidx + (size_t)b * a.cvld;
     uint64_t *cand = sm.x.tk.cand;
-    int nan = 0;
     for (int i = t; i < n; i += kThreads) {
         const float y = __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t *>(vr) + i, __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_AGENT));
-        nan |= (int)isnan(y);
         cand[i] = cand_of(f2key(y), __hip_atomic_load(vi + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     }
-    if (block_or(nan, sm)) {   // its barriers also complete the list
-        if (t == 0) store_row(a, b, 0, GS_ERR_NAN);
-        return;
-    }
+    __syncthreads();
     // Each chunk's kp entries are sorted (descending): an entry's rank is
     // its place in its chunk plus, for every other chunk, the length of the
     // prefix of larger entries there (binary lifting over all chunks at once).
@@ -1820,8 +1816,8 @@ __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int
 // finish (a device-scope counter) samples the virtual row (finish_vrow_y)
 // and clears the counter.  A chunk whose selection
 // cannot be decided sets the row's fallback flag: the finishing block then
-// samples the whole row.  A NaN in a chunk goes to its first slot (the row
-// is an error).
+// samples the whole row.  A NaN in a chunk (or in its penalized values)
+// sets the row's NaN flag: the row is an error.
 __global__ void __launch_bounds__(kThreads)
 chunk_rows_kernel(RowArgs a)
 {
@@ -1886,10 +1882,9 @@ chunk_rows_kernel(RowArgs a)
             const uint64_t e = top[t];
             put(t, key2f((uint32_t)(e >> 32)), (uint32_t)c0 + ~(uint32_t)e);
         }
-    } else if (ok) {
-        if (t < kp) put(t, t == 0 ? __builtin_nanf("") : -INFINITY, (uint32_t)c0);
     } else if (t == 0) {
-        atomicOr(a.csync + 2 * (size_t)b + 1, 1u);
+        // bit 0: the whole row must be sampled; bit 1: a NaN (the row is an error)
+        atomicOr(a.csync + 2 * (size_t)b + 1, ok ? 2u : 1u);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));   // vmcnt(0): this wave's stores are complete
@@ -1899,14 +1894,19 @@ chunk_rows_kernel(RowArgs a)
     CR_TS(3);
     if (!sm.clast) return;
     CR_TS(4);
-    const bool whole = __hip_atomic_load(a.csync + 2 * (size_t)b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+    const uint32_t flags = __hip_atomic_load(a.csync + 2 * (size_t)b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (t == 0) {
         __hip_atomic_store(a.csync + 2 * (size_t)b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(a.csync + 2 * (size_t)b + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (whole) sample_row<kModeSmall>(sm, a, b, 0);
-    else finish_vrow_y(sm, a, b, p);
+    if (flags & 2u) {
+        if (t == 0) store_row(a, b, 0, GS_ERR_NAN);   // a NaN anywhere: the reference's sort panics
+    } else if (flags & 1u) {
+        sample_row<kModeSmall>(sm, a, b, 0);
+    } else {
+        finish_vrow_y(sm, a, b, p);
+    }
     CR_TS(5);
 }
 
