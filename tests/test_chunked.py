@@ -142,3 +142,33 @@ def test_chunked_graph_replays(gpu, torch, oracle):
         assert np.array_equal(tok.cpu().numpy().astype(np.int64), want), rep
         s.sample_batch(other, tother, recent=d_rec[:5], u=d_u[:5])   # eager, uniform params, same sampler
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("V,B", [(524288, 3), (524292, 2)])
+def test_chunked_widest_and_window_lengths(gpu, torch, oracle, V, B):
+    """The widest virtual row of the one-launch form (16 chunks of 32768,
+    k = 128: 2048 entries) and the first vocabulary beyond it (17 chunks: the
+    two-launch form), with per-row window lengths (recent_len) and a window
+    of 1024 ids."""
+    import workloads
+    rng = np.random.default_rng(V)
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    W = 1024
+    rec = rng.integers(0, V, size=(B, W)).astype(np.uint32)
+    rec[:, :8] = [0, 32767, 32768, V - 1, V - 1, V + 1, 65535, 65536]
+    rl = np.array([W, 17, 0][:B], np.uint32)
+    params = workloads.params_rows([(0.9, 128, 0.95, 1.3), (0.6, 3, 0.5, 1.05), (1.4, 64, 1.0, 2.0)][:B])
+    u = rng.random(B).astype(np.float32)
+    d_lg = torch.from_numpy(x).cuda()
+    d_pr = torch.from_numpy(np.ascontiguousarray(params).view(np.uint8)).cuda()
+    d_rec = torch.from_numpy(rec.view(np.int32)).cuda()
+    d_rl = torch.from_numpy(rl.view(np.int32)).cuda()
+    tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    st = torch.full((B,), 99, dtype=torch.int32, device="cuda")
+    s = gpu.Sampler(0.7, 40, 0.9, 1.1, seed=1)
+    _say("chunked widest V", V, "B", B)
+    s.sample_batch(d_lg, tok, params=d_pr, recent=d_rec, recent_len=d_rl, u=torch.from_numpy(u).cuda(), status=st)
+    torch.cuda.synchronize()
+    assert (st.cpu().numpy() == 0).all()
+    want = oracle.sample_batch(x, params, u, recent=rec, recent_len=rl, nthreads=8, fast_topk=True)
+    assert np.array_equal(tok.cpu().numpy().astype(np.int64), want)
