@@ -1825,7 +1825,12 @@ chunk_rows_kernel(RowArgs a)
     const int c = blockIdx.x, b = blockIdx.y;
     const int t = threadIdx.x;
     const gs_params p = a.params ? a.params[b] : a.uparams;
-    if (!chunk_row(p, a.V)) return;
+    if (!chunk_row(p, a.V)) {
+        // another small-path row of the batch (per-row params): its first
+        // block samples it here, so no separate small-row launch is needed
+        if (c == 0 && !is_full_path(p, a.V)) sample_row<kModeSmall>(sm, a, b, kChunkedSelf);
+        return;
+    }
 #ifdef GS_TIMING
 #define CR_TS(i) do { if (t == 0 && b == (int)g_row) g_fails[1000 + 8 * c + (i)] = (int)__builtin_amdgcn_s_memrealtime(); } while (0)
 #else
@@ -2022,14 +2027,17 @@ hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, uint32_
     a.cvld = vld;
     a.cnch = nch;
     if (csync) {
-        // one launch samples the chunked rows; with per-row params the row
-        // kernels take the batch's other rows (the small kernel skips
-        // the chunked ones)
+        // one launch samples the chunked rows and the batch's other
+        // small-path rows; with per-row params the full-vocabulary kernels
+        // follow for the rest
         a.chunked = kChunkedSelf;
         a.csync = csync;
         hipLaunchKernelGGL(chunk_rows_kernel, dim3(nch, B), dim3(kThreads), 0, st, a);
-        if (!a.params) return hipGetLastError();
-        return launch_sample_rows(a, B, st);
+        if (a.params) {
+            hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
+            hipLaunchKernelGGL(sample_rows_kernel<kModeSort>, dim3(B), dim3(kThreads), 0, st, a);
+        }
+        return hipGetLastError();
     }
     hipLaunchKernelGGL(chunk_topk_kernel, dim3(nch, B), dim3(kThreads), 0, st, a, nch, vrow, vidx, vld);
     // the virtual rows go through the small kernel (in order: a fork and
