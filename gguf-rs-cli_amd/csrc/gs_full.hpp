@@ -1050,12 +1050,6 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
     int nan = 0;
     float m0 = 0.0f;
     auto visit1 = [&](int i, float y) {
-#ifdef GS_EXP_P1MIN
-        tmax = fmaxf(tmax, y); return;
-#endif
-#ifdef GS_EXP_P1CNT
-        { tmax = fmaxf(tmax, y); const float dp = y - m0; if (dp >= -kFDLo) atomicAdd(&f.cnt[f_bin(dp)], 1u); return; }
-#endif
         nan |= (int)isnan(y);
         if (y > tmax && !(has_pen && hash_find(sm, (uint32_t)i) >= 0)) tmax = y;
         const float dp = y - m0;
@@ -1275,9 +1269,6 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
 
     // ---- pass 2 (cache): seq-1 record counts; listed bins written ----------
     auto visit2 = [&](int i, float y) {
-#ifdef GS_EXP_P2MIN
-        if (y == 12345.0f) f.fail = 1; return;
-#endif
         const float dp = y - m0;
         if (!(dp <= kFDUp) || dp < -kFDLo) return;
         const int b = f_bin(dp);

@@ -76,11 +76,12 @@ int gs_sampler_get_state(const gs_sampler *s, uint64_t *state);
 int gs_sampler_set_state(gs_sampler *s, uint64_t state);
 
 /* Pre-allocate the full-vocabulary scratch (16*V bytes per row) for batches
- * of up to B rows, and for V > 32768 the buffers of the split top-k path
- * (256 KB per row, at most 32 rows), e.g. before capturing gs_sample_batch
- * into a HIP graph (the batch call otherwise allocates on first use; under
- * capture, rows whose split buffers are missing take the one-workgroup-per-row
- * path instead). */
+ * of up to B rows, and for V > 32768 the virtual rows of the split and
+ * chunked top-k paths (256 KB per row for up to 32 rows, or
+ * ceil(V / 32768) KB per row for B rows, whichever is larger), e.g. before
+ * capturing gs_sample_batch into a HIP graph (the batch call otherwise
+ * allocates on first use; under capture, rows whose buffers are missing
+ * take the one-workgroup-per-row path instead). */
 int gs_sampler_reserve(gs_sampler *s, size_t B, size_t V);
 
 /* ---- single row: sample(logits, recent) -> token -------------------------
