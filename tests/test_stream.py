@@ -146,3 +146,43 @@ def test_stream_largest(gpu, torch, oracle, V):
     u = rng.random(B).astype(np.float32)
     _say("stream largest V", V)
     _check(gpu, torch, oracle, x, params, u, rec)
+
+
+@pytest.mark.parametrize("V,B", [(65544, 520), (152064, 600), (16388, 512)])
+def test_stream_rows_many(gpu, torch, oracle, V, B):
+    """Batches of more than two rows per CU with the sampler's own params: a
+    window of 1024 ids with per-row lengths, ids >= V and duplicates, a row
+    that overflows the candidate list, a NaN row, and k = 256 on rows that
+    fit the registers."""
+    rng = np.random.default_rng(V + B)
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    W = 1024
+    rec = rng.integers(0, V, size=(B, W)).astype(np.uint32)
+    rec[:, 0] = V + 3
+    rec[:, 1:5] = rec[:, 5:9]
+    for b in range(0, B, 7):                                  # spikes that the window penalizes
+        x[b, rec[b, 10:20]] += np.float32(9.0)
+    rl = rng.integers(0, W + 1, size=B).astype(np.uint32)
+    rl[::5] = W
+    x[3] = np.arange(V, dtype=np.float32) * np.float32(1e-3)  # ascending: the list overflows
+    x[11, V // 2] = np.nan
+    u = rng.random(B).astype(np.float32)
+    T, k, p, rep = 0.7, 50, 0.9, 1.3
+    if V == 16388:
+        k = 256
+    d_lg = torch.from_numpy(x).cuda()
+    d_rec = torch.from_numpy(rec.view(np.int32)).cuda()
+    d_rl = torch.from_numpy(rl.view(np.int32)).cuda()
+    tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+    st = torch.full((B,), 99, dtype=torch.int32, device="cuda")
+    s = gpu.Sampler(T, k, p, rep, seed=1)
+    _say("stream many rows V", V, "B", B, "k", k)
+    s.sample_batch(d_lg, tok, recent=d_rec, recent_len=d_rl, u=torch.from_numpy(u).cuda(), status=st)
+    torch.cuda.synchronize()
+    want = oracle.sample_batch(x, [(T, k, p, rep)] * B, u, recent=rec, recent_len=rl, nthreads=16, fast_topk=True)
+    got, stv = tok.cpu().numpy().astype(np.int64), st.cpu().numpy()
+    err = want < 0
+    assert list(np.nonzero(err)[0]) == [11], np.nonzero(err)[0]
+    assert stv[11] == gpu.GS_ERR_NAN and (stv[~err] == 0).all(), stv
+    bad = np.nonzero((got != want) & ~err)[0]
+    assert bad.size == 0, (bad[:8], got[bad[:8]], want[bad[:8]])
