@@ -257,14 +257,16 @@ __device__ __forceinline__ FullRec f_rec_pending(int b, int sq, int e, uint32_t 
 }
 
 // Resolve the pending records [0, nrec) of a classification loop: two
-// threads per record (thr and up), all threads of the block.
+// threads per record, all threads of the block.  The first half of the
+// block finds the thr boundaries and the second half the up boundaries, so
+// that no wave runs both searches one after the other.
 __device__ void f_thresholds(RowSmem &sm, const FSeq &c, float m0, float s2lo, float s2hi)
 {
     FullSmem &f = sm.x.fs;
     const int t = threadIdx.x;
     const int nr = min(f.nrec, kRecCap);
     for (int base = 0; base < nr; base += kThreads / 2) {
-        const int r = base + (t >> 1), which = t & 1;
+        const int r = base + (t % (kThreads / 2)), which = t / (kThreads / 2);
         uint32_t info = 0u, lvl = 0u;
         if (r < nr) {
             info = __float_as_uint(f.u.rec[r].thr);
