@@ -225,6 +225,24 @@ __device__ int f_classify(const FSeq &c, int sq, int e, float ylo, float yhi, fl
     *lvl = d0;
     return u1 == d0 ? 0 : 1;
 }
+// The summand of accumulation sq >= 2 from a = expf(y - m) (f_val's steps).
+__device__ __forceinline__ float f_val_a(const FSeq &c, int sq, float a, float s2)
+{
+    const float p = a / c.S;
+    return (sq == 2 || !c.nuc) ? p : p / s2;
+}
+// f_classify for sq >= 2 with a(ylo), a(yhi) already evaluated (plan B
+// classifies both accumulations at the same edges).
+__device__ __forceinline__ int f_classify_a(const FSeq &c, int sq, int e, float alo, float ahi, float s2lo,
+                                            float s2hi, uint32_t *lvl)
+{
+    uint32_t d0, u0, d1, u1;
+    f_incs(f_val_a(c, sq, alo, s2hi), e, &d0, &u0);
+    f_incs(f_val_a(c, sq, ahi, s2lo), e, &d1, &u1);
+    if (u1 - d0 > 1u || u1 < d0) return 2;
+    *lvl = d0;
+    return u1 == d0 ? 0 : 1;
+}
 // One boundary of a two-increment bin (f_classify returned 1): which == 0
 // gives thr, the smallest y whose increment reaches lvl + 1 with a rounding
 // tie counted as reaching it (for every s2 in the range: at s2lo); which ==
@@ -1448,14 +1466,18 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             const bool listed2 = (f.w1[b] & kW1Listed) != 0u;
             uint32_t cl2 = kCNone, cl3 = kCNone, r2 = kNoRec, r3 = kNoRec, lvl2 = 0u, lvl3 = 0u;
             int e2 = 0, e3 = 0;
-            float ylo = 0.0f, yhi = 0.0f;
-            if (rel2 || rel3) f_range(m0, b, &ylo, &yhi);
+            float ylo = 0.0f, yhi = 0.0f, alo = 0.0f, ahi = 0.0f;
+            if (rel2 || rel3) {
+                f_range(m0, b, &ylo, &yhi);
+                alo = glibc_expf_tab(ylo - c2.m, c2.tab);
+                ahi = glibc_expf_tab(yhi - c2.m, c2.tab);
+            }
             if (rel2) {
                 if (!(c2lo > 0.0) || f_dexp(c2lo * dl) != f_dexp(c2hi * dh) || c2hi * dh >= (double)top_p) {
                     cl2 = kCLst;
                 } else {
                     e2 = f_dexp(c2lo);
-                    const int k = f_classify(c2, 2, e2, ylo, yhi, 1.0f, 1.0f, &lvl2);
+                    const int k = f_classify_a(c2, 2, e2, alo, ahi, 1.0f, 1.0f, &lvl2);
                     cl2 = k == 0 ? kCUni : kCBag;
                     if (k == 1 && !listed2 && n < 65536u) {
                         const int rr = atomicAdd(&f.nrec, 1);
@@ -1468,7 +1490,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                     cl3 = kCLst;
                 } else {
                     e3 = f_dexp(c3lo);
-                    const int k = f_classify(c2, 3, e3, ylo, yhi, s2lo, s2hi, &lvl3);
+                    const int k = f_classify_a(c2, 3, e3, alo, ahi, s2lo, s2hi, &lvl3);
                     cl3 = k == 0 ? kCUni : kCBag;
                     if (k == 1 && !listed2 && n < 65536u) {
                         const int rr = atomicAdd(&f.nrec, 1);
