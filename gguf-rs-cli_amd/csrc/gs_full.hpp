@@ -403,27 +403,39 @@ __device__ __forceinline__ SegFn seg_op(const SegFn &a, const SegFn &b)
     r.f = b.st ? b.f : par_compose(a.f, b.f);
     return r;
 }
-__device__ SegFn f_block_seg_excl(SegFn v, RowSmem &sm, ParFn *wtot, uint32_t *wst)
+// Exclusive segmented scan of the block's SegFn values (thread order),
+// together with an exclusive sum of one count per thread (*cex; *ctot the
+// block's total): one pair of barriers for both.
+__device__ SegFn f_block_seg_excl_cnt(SegFn v, uint32_t cnt, RowSmem &sm, ParFn *wtot, uint32_t *wst,
+                                      uint32_t *cex, uint32_t *ctot)
 {
     const int lane = lane_id(), w = wave_id();
     SegFn incl = v;
+    uint32_t cin = cnt;
     for (int d = 1; d < 64; d <<= 1) {
         SegFn o;
         o.st = __shfl_up(incl.st, d, 64);
         o.f.f0 = __shfl_up(incl.f.f0, d, 64);
         o.f.f1 = __shfl_up(incl.f.f1, d, 64);
-        if (lane >= d) incl = seg_op(o, incl);
+        const uint32_t oc = __shfl_up(cin, d, 64);
+        if (lane >= d) { incl = seg_op(o, incl); cin += oc; }
     }
-    if (lane == 63) { wtot[w] = incl.f; wst[w] = incl.st; }
+    if (lane == 63) { wtot[w] = incl.f; wst[w] = incl.st; sm.red_u32[w] = cin; }
     __syncthreads();
     SegFn pre{0u, f_fn_id()};
-    for (int i = 0; i < w; i++) pre = seg_op(pre, SegFn{wst[i], wtot[i]});
+    uint32_t cpre = 0u, call = 0u;
+    for (int i = 0; i < kWaves; i++) {
+        if (i < w) { pre = seg_op(pre, SegFn{wst[i], wtot[i]}); cpre += sm.red_u32[i]; }
+        call += sm.red_u32[i];
+    }
     __syncthreads();
     SegFn ex;
     ex.st = __shfl_up(incl.st, 1, 64);
     ex.f.f0 = __shfl_up(incl.f.f0, 1, 64);
     ex.f.f1 = __shfl_up(incl.f.f1, 1, 64);
     if (lane == 0) ex = SegFn{0u, f_fn_id()};
+    *cex = cpre + cin - cnt;
+    *ctot = call;
     return seg_op(pre, ex);
 }
 
@@ -586,9 +598,6 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
                     ep = e[q];
                 }
             }
-            uint32_t nseg;
-            const uint32_t ord0 = block_excl_u32(nst, &nseg, sm);   // contains barriers
-            const int nused = (int)min(nseg, (uint32_t)kWSeg);
             SegFn agg{0u, f_fn_id()};
 #pragma unroll
             for (int q = 0; q < kWC; q++) {
@@ -598,7 +607,10 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
                 const ParFn fn = w_fn(f, wa, (isbin >> q) & 1u, v[q], e[q], &bad);
                 agg = seg_op(agg, SegFn{(starts >> q) & 1u, fn});
             }
-            const SegFn carry = f_block_seg_excl(agg, sm, f.wtot, f.wst);   // contains barriers
+            // the segments' composed increments and each thread's first segment ordinal
+            uint32_t nseg, ord0;
+            const SegFn carry = f_block_seg_excl_cnt(agg, nst, sm, f.wtot, f.wst, &ord0, &nseg);   // contains barriers
+            const int nused = (int)min(nseg, (uint32_t)kWSeg);
             F_TS(tsb + 3);
             // segment table: first item and grid of each segment; for each
             // segment followed by another, the prefix before its last item
