@@ -516,6 +516,15 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
     constexpr int kNone = 0x7fffffff;
     float s = 0.0f;
     int pos = 0;
+    // The leading run below almost always ends after item 0: the first
+    // chunk's items (from item 1) are loaded alongside it.
+    const int pend = min(1 + kThreads * kWC, N);
+    uint64_t pf[kWC];
+#pragma unroll
+    for (int q = 0; q < kWC; q++) {
+        const int j = 1 + t * kWC + q;
+        pf[q] = j < pend ? ldg(items + j) : 0ull;
+    }
     // leading items from s == 0 (0 + v == v); every thread does the same
     while (pos < N && s == 0.0f) {
         const uint64_t it = ldg(items + pos);
@@ -530,19 +539,31 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
         }
         pos++;
     }
-    while (pos < N) {
-        const int cend = min(pos + kThreads * kWC, N);
-        const int j0 = pos + t * kWC;
-        float v[kWC];
-        uint32_t isbin = 0u;
+    F_TS(tsb + 7);
+    float v[kWC];
+    uint32_t isbin = 0u;
+    auto take = [&](int q, uint64_t it) {
+        if (f_is_bin(it)) { isbin |= 1u << q; v[q] = __int_as_float((int)(uint32_t)it); }
+        else v[q] = f_val(wa.c, wa.sq, f_entry_y(it), wa.s2);
+    };
+    const bool pf_ok = pos == 1;
+    if (pf_ok) {
 #pragma unroll
         for (int q = 0; q < kWC; q++) {
             v[q] = 0.0f;
-            const int j = j0 + q;
-            if (j < cend) {
-                const uint64_t it = ldg(items + j);
-                if (f_is_bin(it)) { isbin |= 1u << q; v[q] = __int_as_float((int)(uint32_t)it); }
-                else v[q] = f_val(wa.c, wa.sq, f_entry_y(it), wa.s2);
+            if (1 + t * kWC + q < pend) take(q, pf[q]);
+        }
+    }
+    for (bool first = true; pos < N; first = false) {
+        const int cend = min(pos + kThreads * kWC, N);
+        const int j0 = pos + t * kWC;
+        if (!(first && pf_ok)) {
+            isbin = 0u;
+#pragma unroll
+            for (int q = 0; q < kWC; q++) {
+                v[q] = 0.0f;
+                const int j = j0 + q;
+                if (j < cend) take(q, ldg(items + j));
             }
         }
         int start = pos;
