@@ -368,6 +368,24 @@ __device__ __forceinline__ void f_list_for_each(const uint64_t *gl, uint32_t lo,
         }
     }
 }
+// The same scan through the per-wave buffer `buf` (kWaves doubles of LDS),
+// with one barrier: the caller must pass a barrier before `buf` is written
+// again.
+__device__ double f_block_excl_f64_buf(double v, double *tot, double *buf)
+{
+    const int lane = lane_id(), w = wave_id();
+    double incl = v;
+    for (int d = 1; d < 64; d <<= 1) {
+        const double o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) buf[w] = incl;
+    __syncthreads();
+    double pre = 0.0, all = 0.0;
+    for (int i = 0; i < kWaves; i++) { if (i < w) pre += buf[i]; all += buf[i]; }
+    *tot = all;
+    return pre + incl - v;
+}
 __device__ double f_block_excl_f64(double v, double *tot, RowSmem &sm)
 {
     const int lane = lane_id(), w = wave_id();
@@ -601,7 +619,8 @@ __device__ int f_walk(RowSmem &sm, const uint64_t *items, int N, const WArgs &wa
                     }
                     loc += cq;
                 }
-                if (it < 2) tpre = f_block_excl_f64(loc, &tot, sm);
+                // (two buffers: the segment barrier below comes before either is reused)
+                if (it < 2) tpre = f_block_excl_f64_buf(loc, &tot, it == 0 ? sm.red_f64 : sm.red_f64b);
             }
             F_TS(tsb + 2);
             // ---- segments: an item starts one if its grid differs from the item before ----
@@ -1215,7 +1234,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             if (en) osum += (double)glibc_expf_tab(f_entry_y(en) - m, f.exptab);
         }
         double otot;
-        f_block_excl_f64(osum, &otot, sm);
+        f_block_excl_f64_buf(osum, &otot, sm.red_f64);
         osum = otot;
         uint32_t cn[kPer];
         double mb[kPer], ctr[kPer];
@@ -1232,7 +1251,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
         }
         F_TS(1);
         double tot;
-        double pre = f_block_excl_f64(loc, &tot, sm) + osum;
+        double pre = f_block_excl_f64_buf(loc, &tot, sm.red_f64b) + osum;
         double ct[kPer];
         for (int round = 0; round < 2; round++) {
             double lo = pre;
@@ -1248,8 +1267,9 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
                 lo += ct[q];
                 loc += ct[q];
             }
-            pre = f_block_excl_f64(loc, &tot, sm) + osum;
+            pre = f_block_excl_f64_buf(loc, &tot, round == 0 ? sm.red_f64 : sm.red_f64b) + osum;   // (buffers alternate)
         }
+        __syncthreads();
 #if defined(GS_TIMING) || defined(GS_DIAG)
         if (t == 0 && blockIdx.x < 1024) g_vdiag[blockIdx.x * 16 + 14] = __float_as_int((float)(tot + osum));
 #endif
@@ -1421,7 +1441,7 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             if (en) osum += (double)glibc_expf_tab(f_entry_y(en) - m, f.exptab);
         }
         double otot;
-        f_block_excl_f64(osum, &otot, sm);
+        f_block_excl_f64_buf(osum, &otot, sm.red_f64b);
         osum = otot;
         double mass[kPer], loc = 0.0;
         uint32_t cn[kPer], w1[kPer];

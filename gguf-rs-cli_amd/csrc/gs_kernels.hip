@@ -70,6 +70,7 @@ struct RowSmem {
     float red_f32[kWaves];
     int red_i32[kWaves];
     double red_f64[kWaves];
+    double red_f64b[kWaves];      // a second buffer for scans that run back to back
     alignas(16) float fin[256];                 // finish_wave: the values being accumulated
     int tok;
     int flag_snan;                              // a NaN in the streamed part of a row (topk_row_reg)
