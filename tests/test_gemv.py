@@ -292,3 +292,15 @@ def test_gemv_inputs(gpu, torch, oracle):
     _gpu_check(gpu, torch, oracle, Q8_0, 40000, 1024, seed=5)
     _gpu_check(gpu, torch, oracle, Q4_K, 2000, 3584, seed=6, x_kind="spiky")
     _gpu_check(gpu, torch, oracle, Q5_K, 64, 3584, seed=7, B=3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qt,rows,cols", [
+    (Q6_K, 152064, 3584),    # Qwen2.5-7B lm_head (the bench's GEMV)
+    (Q4_K, 152064, 3584),
+    (Q8_0, 128256, 4096),    # Llama-3-8B lm_head shape
+])
+def test_gemv_full_lm_head(gpu, torch, oracle, qt, rows, cols):
+    """Full output-projection shapes, every row against the oracle."""
+    print("gemv full", qt, rows, cols, flush=True)
+    _gpu_check(gpu, torch, oracle, qt, rows, cols, seed=rows % 1000 + qt)
