@@ -129,6 +129,14 @@ __device__ __forceinline__ float4 ldg(const float4 *p)
     const gs_f4 v = *(const __attribute__((address_space(1))) gs_f4 *)p;
     return make_float4(v.x, v.y, v.z, v.w);
 }
+// The same load with the non-temporal hint, for logits read for the last time
+// (a row's single pass, or its last): they then stream past L2 instead of
+// evicting lines still in use (candidate lists, written list entries).
+__device__ __forceinline__ float4 ldg_nt(const float4 *p)
+{
+    const gs_f4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) gs_f4 *)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 typedef uint32_t gs_u4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ldg(const uint4 *p)
 {

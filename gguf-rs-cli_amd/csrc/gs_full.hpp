@@ -1355,8 +1355,11 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             if (slot < lsz) stg(gl + slot, f_entry(y, (uint32_t)i));
         }
     };
-    if (t_one) row_for_each_any(row, V, visit2);
-    else row_for_each_any(row, V, [&](int i, float x) { visit2(i, x / T); });
+    // (non-temporal loads: the row streams past the L2 lines of the list
+    // entries written here instead of evicting them half-written; measured,
+    // the fetches of pass 3 do not grow)
+    if (t_one) row_for_each_any<true>(row, V, visit2);
+    else row_for_each_any<true>(row, V, [&](int i, float x) { visit2(i, x / T); });
     __syncthreads();
     if (has_pen) {
         // the raw values of penalized ids leave: listed entries are zeroed,
@@ -1636,8 +1639,10 @@ __device__ bool full_v2_row(RowSmem &sm, const float *row, int V, float T, float
             }
         }
     };
-    if (t_one) row_for_each_any(row, V, [&](int i, float y) { visit3(i, y, 0u); });
-    else row_for_each_any(row, V, [&](int i, float x) { visit3(i, x / T, 0u); });
+    // (the row's last pass: non-temporal loads, so the row does not push the
+    // partly written list lines out of L2)
+    if (t_one) row_for_each_any<true>(row, V, [&](int i, float y) { visit3(i, y, 0u); });
+    else row_for_each_any<true>(row, V, [&](int i, float x) { visit3(i, x / T, 0u); });
     __syncthreads();
     if (has_pen) {
         for (int s = t; s < kHashSlots; s += kThreads) {

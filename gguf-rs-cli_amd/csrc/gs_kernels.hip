@@ -181,7 +181,7 @@ __device__ int block_or(int v, RowSmem &sm)
 // aligned row the loads are float4 and kUnroll of them are in flight per
 // thread before any is consumed (a row is 1024*16*kUnroll bytes per round).
 constexpr int kUnroll = 4;
-template <class F>
+template <bool NT = false, class F>
 __device__ __forceinline__ void row_for_each(const float *row, int V, bool aligned, F f)
 {
     const int t = threadIdx.x;
@@ -192,7 +192,8 @@ __device__ __forceinline__ void row_for_each(const float *row, int V, bool align
             float4 v[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; u++)
-                v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));   // unconditional: no wait between loads
+                v[u] = NT ? ldg_nt(r4 + min(base + u * kThreads + t, n4 - 1))
+                          : ldg(r4 + min(base + u * kThreads + t, n4 - 1));   // unconditional: no wait between loads
 #pragma unroll
             for (int u = 0; u < kUnroll; u++) {
                 int q = base + u * kThreads + t;
@@ -222,12 +223,12 @@ __device__ __forceinline__ void row_for_each(const float *row, int V, bool align
 // f(i, row[i]) for every element of a row that is only 4-byte aligned: the
 // first h < 4 elements (up to the next 16-byte boundary) one per thread, the
 // body as float4, the last (V - h) % 4 one per thread.
-template <class F>
+template <bool NT = false, class F>
 __device__ __forceinline__ void row_for_each_any(const float *row, int V, F f)
 {
     const int h = min(V, (int)(((16u - ((uint32_t)reinterpret_cast<uintptr_t>(row) & 15u)) & 15u) >> 2));
     if ((int)threadIdx.x < h) f((int)threadIdx.x, ldg(row + threadIdx.x));
-    row_for_each(row + h, V - h, true, [&](int i, float x) { f(i + h, x); });
+    row_for_each<NT>(row + h, V - h, true, [&](int i, float x) { f(i + h, x); });
 }
 
 // Two-phase visit of a 16-byte aligned row: for each float4, cls(y) is
@@ -1036,15 +1037,16 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
         // registers in one pass: slot u is consumed and refilled with the
         // float4 kRegF4 slots ahead, so kRegF4 loads per thread stay in
         // flight.  Elements at or above the bound (rare) join the list as
-        // above; a NaN anywhere makes the row an error.
+        // above; a NaN anywhere makes the row an error.  (Non-temporal
+        // loads: each logit is read once.)
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
         bool snan = false;
-        auto ld = [&](int u) { return ldg(r4 + min(n4r + u * kThreads + t, n4 - 1)); };
+        auto ld = [&](int u) { return ldg_nt(r4 + min(n4r + u * kThreads + t, n4 - 1)); };
         float4 s0 = ld(0), s1 = ld(1), s2 = ld(2), s3 = ld(3), s4 = ld(4), s5 = ld(5), s6 = ld(6), s7 = ld(7);
         auto slot = [&](float4 &r, int base, int u) __attribute__((always_inline)) {
             const float4 v = r;
             const int q = base + u * kThreads + t;
-            r = ldg(r4 + min(q + kRegF4 * kThreads, n4 - 1));
+            r = ldg_nt(r4 + min(q + kRegF4 * kThreads, n4 - 1));
             const bool in = q < n4;
             snan |= in && (__builtin_isunordered(v.x, v.y) || __builtin_isunordered(v.z, v.w));
             const bool hit = in && (v.x >= tf || v.y >= tf || v.z >= tf || v.w >= tf);
@@ -1431,7 +1433,7 @@ __device__ __forceinline__ void sample_row(RowSmem &sm, const RowArgs &a, int b,
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
         const int n4 = V >> 2;
 #pragma unroll
-        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg_nt(r4 + min(u * kThreads + t, n4 - 1));
     }
     if (has_pen && !regpath) pl = pen_load(row, V, a.recent + (size_t)b * a.ld_recent, W, true);
     if (regpath) reg_clear(sm, has_pen, V);   // the register path builds its penalty table itself
@@ -1555,7 +1557,7 @@ reg_row_kernel(RowArgs a)
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
         const int n4 = V >> 2;
 #pragma unroll
-        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg_nt(r4 + min(u * kThreads + t, n4 - 1));
     }
     reg_clear(sm, has_pen, V);
     __syncthreads();
@@ -1858,7 +1860,7 @@ chunk_rows_kernel(RowArgs a)
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
         const int n4 = L >> 2;
 #pragma unroll
-        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg_nt(r4 + min(u * kThreads + t, n4 - 1));
     }
     reg_clear(sm, has_pen, L);
     if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
@@ -1931,7 +1933,7 @@ __device__ void finish_virtual_row(RowSmem &sm, const RowArgs &a, int b, const g
         const float4 *r4 = reinterpret_cast<const float4 *>(vr);
         const int n4 = V2 >> 2;
 #pragma unroll
-        for (int u = 0; u < kRegF4; u++) rv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
+        for (int u = 0; u < kRegF4; u++) rv[u] = ldg_nt(r4 + min(u * kThreads + t, n4 - 1));
     }
     reg_clear(sm, false, V2);
     if (t == 0) { sm.nuniq = 0; sm.flag_nan = 0; }
