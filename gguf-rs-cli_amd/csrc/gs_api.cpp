@@ -664,16 +664,27 @@ int gs_sample_batch_noalloc(gs_sampler *s, const float *d_logits, size_t B, size
     if (rc) return rc;
     // layout: B fallback flags | split top-k buffers (any k, up to
     // kSplitMaxRows rows) | full-vocabulary scratch
+    // Only the buffers of the paths this call can take are counted: the
+    // full-vocabulary scratch when some row may take that path, the chunked
+    // top-k buffers when the batch has fewer rows than CUs, the split
+    // buffers for a few rows with uniform params.  (A path whose buffer is
+    // not given is not taken: sample_batch_bufs falls back to one workgroup
+    // per row for top-k rows.)
+    const bool full = d_params || needs_full_path(s->params, V);
     const size_t fb_bytes = gs::align256((B ? B : 1) * sizeof(int32_t));
-    const size_t split_rows = B < (size_t)gs::kSplitMaxRows ? B : (size_t)gs::kSplitMaxRows;
-    size_t sp_need = split_bytes(split_rows, gs::kSplitMaxWidth);
-    if (gs::chunk_path_ok(V) && chunk_bytes(B, V) > sp_need) sp_need = chunk_bytes(B, V);
-    const size_t sp_bytes = V > gs::kRegMaxV ? gs::align256(sp_need) : 0;
-    const size_t full_bytes = B * gs::scratch_u32_per_row(V) * sizeof(uint32_t);
+    size_t sp_need = 0;
+    if (V > gs::kRegMaxV) {
+        if (!d_params && B <= (size_t)gs::kSplitMaxRows && gs::split_fits(s->params, V))
+            sp_need = split_bytes(B, gs::split_width(s->params, V));
+        if (gs::chunk_path_ok(V) && B < (size_t)num_cus(s) && chunk_bytes(B, V) > sp_need)
+            sp_need = chunk_bytes(B, V);
+    }
+    const size_t sp_bytes = gs::align256(sp_need);
+    const size_t full_bytes = full ? B * gs::scratch_u32_per_row(V) * sizeof(uint32_t) : 0;
     if (fb_bytes + sp_bytes + full_bytes > gs::kStaticScratchBytes) return GS_ERR_UNSUPPORTED;
     char *p = (char *)base;
-    gs::CallBufs bf{true, (uint32_t *)(p + fb_bytes + sp_bytes), (int32_t *)p, sp_bytes ? p + fb_bytes : nullptr,
-                    sp_bytes};
+    gs::CallBufs bf{true, full_bytes ? (uint32_t *)(p + fb_bytes + sp_bytes) : nullptr, (int32_t *)p,
+                    sp_bytes ? p + fb_bytes : nullptr, sp_bytes};
     return gs::sample_batch_bufs(s, d_logits, B, V, ld, d_params, d_recent, ld_recent, d_recent_len, W, d_u,
                                  d_tokens, d_status, nullptr, stream, &bf);
 }

@@ -120,8 +120,11 @@ int gs_sample_mut(gs_sampler *s, float *logits, size_t V,
  * Scratch for rows that need the full-vocabulary path is owned by the
  * sampler and grows on demand (allocation happens outside kernels, before
  * the launch).
- * One sampler serves one stream at a time: its scratch is shared by all its
- * calls, so calls of one sampler on two streams may race.
+ * One sampler serves one stream at a time: its scratch and the chunked
+ * top-k path's per-row counters are shared by all its calls, so its batched
+ * calls must be stream-ordered one after the other, graph replays included
+ * (two streams, or a replay beside an eager call, may race: a row's finish
+ * can then be missed and its token left unwritten).
  * HIP graph capture: call gs_sampler_reserve(s, B, V) before capturing (a
  * call that would have to allocate under capture returns
  * GS_ERR_UNSUPPORTED), and pass d_u (a captured call with d_u == NULL and
@@ -144,13 +147,25 @@ int gs_sample_batch(gs_sampler *s, const float *d_logits, size_t B, size_t V,
  * in one statically sized device array of GS_NOALLOC_SCRATCH_BYTES per GPU,
  * part of the library's code object and held until the process ends.  The
  * call makes no hipMalloc/hipFree and no allocating library call.
- * Limit: fallback flags (4 B per row, 256-byte aligned) + split buffers
- * (V > 32768 only: 256 KB per row for up to 32 rows) + B rows of
- * full-vocabulary scratch must fit; otherwise GS_ERR_UNSUPPORTED.
+ * Limit: the buffers of the paths the call can take must fit, otherwise
+ * GS_ERR_UNSUPPORTED:
+ *   fallback flags, 4 B per row rounded up to 256 B;
+ *   + for V > 32768, the larger of the split top-k buffers (uniform params
+ *     with 0 < top_k <= 128 and at most 32 rows: 8 B * (V/1024) *
+ *     round_up(top_k, 4) per row) and the chunked top-k buffers (fewer
+ *     rows than CUs: 8 B * ceil(V/32768) * 128 per row), rounded up to 256 B;
+ *   + when d_params is given or the sampler's params need the
+ *     full-vocabulary path (T > 0 and top_k == 0, top_k >= V or
+ *     top_k > 1024): B rows of full-vocabulary scratch, about 25 B per
+ *     vocabulary entry (3.8 MB per row at V = 152064, so at most 16 rows).
+ * Top-k-only batches need no full-vocabulary scratch: C5's 1024 rows of
+ * V = 152064, top_k = 50 fit.
  * Every call on one GPU shares that GPU's array (whichever sampler makes
  * it) and the array keeps the last call's contents: calls that overlap on
  * one GPU (two streams, or two threads) race and must be serialised by the
- * caller.  Nothing in the array needs to start at zero.  The chunked top-k
+ * caller.  gs_sampler_fallback_rows reads its flags from the array, so it
+ * reports the last allocation-free call on the GPU, whichever sampler made
+ * it.  Nothing in the array needs to start at zero.  The chunked top-k
  * path's per-row counters (8 KB) are the sampler's own, allocated and
  * cleared by gs_sampler_create, and each call leaves them at zero. */
 #define GS_NOALLOC_SCRATCH_BYTES (64u << 20)

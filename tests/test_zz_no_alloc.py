@@ -75,3 +75,36 @@ def test_noalloc_rejects_oversize(gpu, torch):
     with pytest.raises(gpu.SamplerError) as e:
         s.sample_batch(d_lg, d_tok, u=d_u, noalloc=True)
     assert e.value.code == gpu.GS_ERR_UNSUPPORTED
+
+
+def test_noalloc_topk_large_batch(gpu, torch, oracle):
+    """Top-k rows with the sampler's own params (no d_params) need no
+    full-vocabulary scratch: C5's shape (B = 1024, V = 152064, k = 50,
+    1024-id windows) fits the static array, on two calls in a row, the second
+    smaller, with the same tokens as gs_sample_batch and the oracle."""
+    import workloads
+    V = 152064
+    rng = np.random.default_rng(1024)
+    s_ref = gpu.Sampler(0.7, 50, 0.9, 1.3, seed=1)
+    s_na = gpu.Sampler(0.7, 50, 0.9, 1.3, seed=1)
+    for B in (1024, 300):
+        x = (rng.standard_normal((B, V), dtype=np.float32) * 3.0).astype(np.float32)
+        u = rng.random(B, dtype=np.float32)
+        recent = rng.integers(0, V, size=(B, 1024), dtype=np.uint32)
+        d_lg = torch.from_numpy(x).cuda()
+        d_u = torch.from_numpy(u).cuda()
+        d_rec = torch.from_numpy(recent.view(np.int32)).cuda()
+        _say("noalloc topk V", V, "B", B)
+        out = []
+        for s, na in ((s_ref, False), (s_na, True)):
+            d_tok = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+            d_st = torch.full((B,), 99, dtype=torch.int32, device="cuda")
+            s.sample_batch(d_lg, d_tok, recent=d_rec, u=d_u, status=d_st, noalloc=na)
+            torch.cuda.synchronize()
+            out.append((d_tok.cpu().numpy().astype(np.int64), d_st.cpu().numpy()))
+        (want_tok, want_st), (got_tok, got_st) = out
+        assert (got_st == 0).all() and (want_st == 0).all()
+        assert (got_tok == want_tok).all()
+        params = np.array([(0.7, 50, 0.9, 1.3)] * B, dtype=workloads.PARAMS_DTYPE)
+        ora = oracle.sample_batch(x, params, u, recent=recent, nthreads=8)
+        assert (got_tok == ora).all(), np.nonzero(got_tok != ora)
