@@ -84,4 +84,50 @@ struct FullSmem {
     uint32_t list_end;
 };
 
+// ---------------------------------------------------------------------------
+// LDS of the increment-histogram path (gs_full3.hpp).
+constexpr int kF3Lvl = 12288;       // level counters (+ one slot that absorbs non-counts)
+constexpr int kF3L1 = 4096;         // levels of seq 1 (pass 2)
+constexpr int kF3L23 = 6144;        // levels of each of seqs 2 and 3 (pass 3)
+constexpr int kF3Runs = 64;         // runs per accumulation
+constexpr int kF3Regs = 192;        // regions of one walk
+constexpr int kF3Ties = 64;         // rounding ties per accumulation
+constexpr int kF3Tab = kFBins + 2;  // per-bin words: [0] above the bins, [1 + b] bin b, [kFBins + 1] below
+
+// A run: consecutive bins whose elements the accumulation adds at one grid
+// (2^(e-23)), none of them listed.  Its elements' increments k in [klo, khi]
+// are counted in lvl[off + k].
+struct F3Run {
+    int off;               // level slot of increment k: off + k
+    uint32_t klo, khi;
+    int e;                 // grid exponent
+    uint32_t base;         // first level slot (off + klo)
+    uint32_t span;         // level slots
+};
+struct F3Reg { uint32_t b0, key; };         // first bin, run id or kF3KeyListed / kF3KeyNone
+struct F3Tie { uint32_t run, k; uint64_t A; };   // an element at k + 1/2 grid units; A: the run's levels above it
+
+struct Full3Smem {
+    uint32_t cnt[kFBins];      // exact element count per bin (penalized values moved)
+    uint32_t w[kF3Tab];        // pass 1: raw values of penalized ids per bin; pass 2: role words
+    union {
+        uint64_t mass64[kFMassBins];   // pass 1, plan A
+        uint2 w23[kF3Tab];             // pass 3: role words of seqs 2, 3
+    } u;
+    uint32_t lvl[kF3Lvl + 1];  // level counters (plans: per-bin temporaries; walks: staged summands)
+    float pre[kFBins + 1];     // predicted seq-1 sum before each bin ([kFBins]: the total)
+    uint64_t over[kFOverCap];
+    uint64_t exptab[32];
+    F3Run run[2][kF3Runs];     // seq 1, then seq 2 | seq 3
+    uint64_t rtot[2][kF3Runs]; // run totals of the walk
+    F3Tie tie[2][kF3Ties];
+    F3Reg reg[kF3Regs];
+    uint32_t wlast[kWaves];    // region building: each wave's last key
+    int nrun[2], ntie[2], nreg;
+    uint32_t ltot[2];
+    float m0, m, S, s2, s2lo, s2hi, cb;
+    int nover, fail, namb, ndef, bH, walk_res;
+    uint32_t headend, list_end, cut_arr, cut_pos, tok_pos, tok_arr, list2;
+};
+
 } // namespace gs

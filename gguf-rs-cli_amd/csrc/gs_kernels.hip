@@ -77,6 +77,7 @@ struct RowSmem {
     union {
         TopkSmem tk;
         FullSmem fs;
+        Full3Smem f3;
     } x;
     int clast;                                  // chunk_rows_kernel: this block finishes the row
 };
@@ -1149,6 +1150,7 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
 }
 
 #include "gs_full.hpp"
+#include "gs_full3.hpp"
 
 // --------------------------------------------------------------------------
 // Full-vocabulary path: stable LSD radix sort of (~key, index) in scratch.
@@ -1486,13 +1488,20 @@ __device__ __forceinline__ void sample_row(RowSmem &sm, const RowArgs &a, int b,
         else if (keep == V && ((reinterpret_cast<uintptr_t>(row) & 3u) == 0)) {
             uint64_t *gl = reinterpret_cast<uint64_t *>(a.scratch + (size_t)b * a.scratch_stride);
             const uint32_t lcap = (uint32_t)(a.scratch_stride / 2);
-            done = full_v2_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
+            done = full_v3_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
         }
         if (t == 0) a.fb[b] = done ? 0 : 1;
-        if (!done) return;   // the sort kernel finishes the row
+        if (!done) return;   // the fallback kernel finishes the row
     } else {
-        if (sm.flag_nan) status = GS_ERR_NAN;
-        else {
+        bool done = false;
+        if (sm.flag_nan) { status = GS_ERR_NAN; done = true; }
+        else if (MODE == kModeSort && keep == V && ((reinterpret_cast<uintptr_t>(row) & 3u) == 0)) {
+            // the first binned form (per-bin classes and thresholds), then the sort
+            uint64_t *gl = reinterpret_cast<uint64_t *>(a.scratch + (size_t)b * a.scratch_stride);
+            const uint32_t lcap = (uint32_t)(a.scratch_stride / 2);
+            done = full_v2_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
+        }
+        if (!done) {
             const size_t off = (size_t)b * a.scratch_stride;
             tok = full_row(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, a.scratch + off,
                            a.scratch + off + V, a.scratch + off + 2 * (size_t)V,
@@ -1654,6 +1663,21 @@ extern "C" int gs_debug_fails(int *out)
 }
 #endif
 #if defined(GS_TIMING) || defined(GS_DIAG)
+extern "C" int gs_debug_v3dump(int *out)
+{
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_v3dump), sizeof(int) * 64 * 256) == hipSuccess ? 0 : -5;
+}
+extern "C" int gs_debug_v3diag(int *out, uint32_t *ts, int clear)
+{
+    if (clear) {
+        static int zeros[1024 * 32];
+        static uint32_t z2[256 * 32];
+        if (hipMemcpyToSymbol(HIP_SYMBOL(gs::g_v3diag), zeros, sizeof(zeros)) != hipSuccess) return -5;
+        return hipMemcpyToSymbol(HIP_SYMBOL(gs::g_v3t), z2, sizeof(z2)) == hipSuccess ? 0 : -5;
+    }
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(gs::g_v3diag), sizeof(int) * 1024 * 32) != hipSuccess) return -5;
+    return hipMemcpyFromSymbol(ts, HIP_SYMBOL(gs::g_v3t), sizeof(uint32_t) * 256 * 32) == hipSuccess ? 0 : -5;
+}
 extern "C" int gs_debug_vdiag(int *out, int clear)
 {
     if (clear) {

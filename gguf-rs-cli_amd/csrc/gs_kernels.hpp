@@ -56,9 +56,19 @@ constexpr size_t kChunkSelfMaxN = 2048;   // widest virtual row (chunk_stride) o
 // needs 4V; the exact path its element list and walk items (each V plus
 // room for the overflow, the bins and penalized values, in u64) and its
 // deferred ids.
+// The increment-histogram path (gs_full3.hpp) lists at most f3_list_cap(V)
+// entries per pass; its scratch (u64 words): the unsorted list, the two
+// sorted lists, their summands (two f32 arrays), the ambiguous and deferred
+// entries and two per-bin tables.
+constexpr size_t kF3AmbCap = 4096;
+constexpr size_t kF3DefCap = 8192;
+__host__ __device__ inline size_t f3_list_cap(size_t V) { return ((V < 65536 ? V : 65536) + 256 + 2 * 2048 + 1) & ~(size_t)1; }
+__host__ __device__ inline size_t f3_scratch_u64(size_t V) { return 4 * f3_list_cap(V) + kF3AmbCap + kF3DefCap + 4096; }
 inline size_t scratch_u32_per_row(size_t V)
 {
-    return 6 * V + 2 * (3 * 256 + 2 * 4096 + 6 * 2048) + 16384;
+    const size_t v2 = 6 * V + 2 * (3 * 256 + 2 * 4096 + 6 * 2048) + 16384;
+    const size_t v3 = 2 * f3_scratch_u64(V);
+    return v2 > v3 ? v2 : v3;
 }
 
 // The row kernels of a batch: the small-path rows (and, when a.chunked is
