@@ -64,7 +64,7 @@ constexpr uint32_t kF3KeyListed = 0xffffffffu, kF3KeyNone = 0xfffffffeu;
 // seqs 2 and 3 the roundings of 1/S, of the products and of p and q.
 constexpr float kF3Band1 = 7.62939453125e-6f;      // 2^-17
 constexpr float kF3Band23 = 1.52587890625e-5f;     // 2^-16
-constexpr double kF3Lo = 1.0 - 1.0 / 524288.0, kF3Hi = 1.0 + 1.0 / 524288.0;   // level range margins
+constexpr double kF3Lo = 1.0 - 1.0 / 65536.0, kF3Hi = 1.0 + 1.0 / 65536.0;   // level range margins (2^-16)
 
 // A list entry (key << 32 | ~index) whose element left the list (the raw
 // value of a penalized id): the low word becomes the index itself, which
@@ -74,49 +74,104 @@ __device__ __forceinline__ uint64_t f3_dead(uint64_t en) { return (en & 0xffffff
 
 // Exact sequential f32 adds cum = RN(cum + v[j]) over LDS values v[beg, end)
 // on one wave (every lane calls with the same arguments), stopping at the
-// first j after which pred(cum) holds.  64 values per step: while the sum
+// first j after which pred(cum) holds (pred is monotone: the sums only
+// grow).  256 values per step, four consecutive ones per lane: while the sum
 // stays in one binade each add is an integer increment at its grid (elem_fn,
-// a rounding tie as a function of the parity before it), composed by a wave
-// scan; the first value whose add leaves the binade is added with the
-// reference's own f32 add and the next step starts after it.  Returns j (or
-// end); *cum_io receives the sum there (or at the end).
+// a rounding tie as a function of the parity before it); a lane composes its
+// four, a wave scan composes the lanes.  The first value whose add leaves
+// the binade is added with the reference's own f32 add and the next step
+// starts after it.  Returns j (or end); *cum_io receives the sum there (or
+// at the end).
+//
+// The first nseq values are added one by one instead (every lane runs the
+// same chain, reading broadcasts): the sum crosses binades often while it is
+// small (at the head of the row), and each crossing would cost a step.
 template <class P>
-__device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *cum_io, P pred)
+__device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *cum_io, P pred, uint32_t nseq = 0)
 {
     const int lane = lane_id();
     float cum = *cum_io;
     uint32_t j0 = beg;
+    {
+        const uint32_t js = min(end, beg + nseq);
+        for (; j0 < js; j0 += 8u) {
+            float c[8];
+            float x = cum;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                x = x + (j0 + i < js ? v[j0 + i] : 0.0f);
+                c[i] = x;
+            }
+            if (pred(c[7])) {          // pred is monotone: the first of the 8 that holds
+                int i = 0;
+                while (!pred(c[i])) i++;
+                *cum_io = c[i];
+                return j0 + (uint32_t)i;
+            }
+            cum = c[7];
+        }
+        j0 = js;
+    }
     while (j0 < end) {
-        const uint32_t j = j0 + (uint32_t)lane;
-        const bool live = j < end;
-        const float a = live ? v[j] : 0.0f;
+        const uint32_t jl = j0 + 4u * (uint32_t)lane;
+        float a[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) a[c] = jl + c < end ? v[jl + c] : 0.0f;
         const int e = grid_exp(cum);
-        const ParFn inc = wave_scan_incl(elem_fn(a, e));
+        ParFn fc[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) fc[c] = elem_fn(a[c], e);
+        ParFn loc = fc[0];
+#pragma unroll
+        for (int c = 1; c < 4; c++) loc = par_compose(loc, fc[c]);
+        const ParFn incl = wave_scan_incl(loc);
+        ParFn ex;
+        ex.f0 = __shfl_up(incl.f0, 1, 64);
+        ex.f1 = __shfl_up(incl.f1, 1, 64);
+        if (lane == 0) ex = ParFn{0u, 0u};
         const uint32_t P0 = (uint32_t)ldexpf(cum, 23 - e);      // cum = P0 2^(e-23), P0 < 2^24
-        const uint32_t Pe = P0 + par_apply(inc, P0 & 1u);       // the sum after this lane's value
-        const bool leaves = live && Pe >= (1u << 24);
-        const float sj = ldexpf((float)Pe, e - 23);             // exact where the sum stays
-        const bool stop = live && !leaves && pred(sj);
-        const uint64_t bl = __ballot(leaves), bs = __ballot(stop);
+        const uint32_t Pst = P0 + par_apply(ex, P0 & 1u);       // the sum before this lane's first value
+        // per lane: the first value whose add leaves the binade (fl), the
+        // first after which pred holds (fs), the sums around them
+        uint32_t Pc = Pst, Plast = Pst;
+        int fl = 4, fs = 4;
+        uint32_t Pbef = Pst, Pstop = 0u;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t Pn = Pc + par_apply(fc[c], Pc & 1u);
+            const bool live = jl + c < end;
+            if (fl == 4 && fs == 4) {
+                if (live && (Pc >= (1u << 24) || Pn >= (1u << 24))) { fl = c; Pbef = Pc; }
+                else if (live && pred(ldexpf((float)Pn, e - 23))) { fs = c; Pstop = Pn; }
+            }
+            if (live) Plast = Pn;
+            Pc = Pn;
+        }
+        const uint64_t bl = __ballot(fl < 4), bs = __ballot(fs < 4);
         const int Ll = bl ? (int)__builtin_ctzll(bl) : 64;
         const int Ls = bs ? (int)__builtin_ctzll(bs) : 64;
         if (Ls < Ll) {
-            *cum_io = rdl(sj, Ls);
-            return j0 + (uint32_t)Ls;
+            const int c = __builtin_amdgcn_readlane(fs, Ls);
+            *cum_io = ldexpf((float)(uint32_t)__builtin_amdgcn_readlane((int)Pstop, Ls), e - 23);
+            return j0 + 4u * (uint32_t)Ls + (uint32_t)c;
         }
         if (Ll == 64) {
-            cum = rdl(sj, (int)min(end - j0, 64u) - 1);
-            j0 += 64u;
+            const int last = (int)min(end - j0, 256u) - 1;
+            cum = ldexpf((float)(uint32_t)__builtin_amdgcn_readlane((int)Plast, last >> 2), e - 23);
+            j0 += 256u;
             continue;
         }
-        const float before = Ll ? rdl(sj, Ll - 1) : cum;
-        const float after = before + rdl(a, Ll);
+        const int c = __builtin_amdgcn_readlane(fl, Ll);
+        const uint32_t pb = (uint32_t)__builtin_amdgcn_readlane((int)Pbef, Ll);
+        const float before = pb >= (1u << 24) ? cum : ldexpf((float)pb, e - 23);
+        const uint32_t p = j0 + 4u * (uint32_t)Ll + (uint32_t)c;
+        const float after = before + v[p];
         if (pred(after)) {
             *cum_io = after;
-            return j0 + (uint32_t)Ll;
+            return p;
         }
         cum = after;
-        j0 += (uint32_t)Ll + 1u;
+        j0 = p + 1u;
     }
     *cum_io = cum;
     return end;
@@ -256,7 +311,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
         uint32_t end = f.headend;
         const bool at = lim && lim_arr == 0u;
         if (at) end = lim_pos + 1u;
-        const uint32_t p = f3_chain(st, 0u, end, &cum, pred);
+        const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 256u);
         F3_TS(16 + 5 * s);
         *cum_out = cum;
         if (p < end) { *arr = 0u; *pos = p; return 1; }
@@ -437,6 +492,16 @@ __device__ bool f3_plan_runs(RowSmem &sm, Full3Smem &f, int s, int bH, const uin
 }
 
 
+// The increment every element of a bin adds when its exact summands, in
+// grid units, lie in [xl, xh] (up to the bin edges' rounding): the one
+// integer that [xl, xh] widened by 2^-15 rounds to, or kF3NoU.
+constexpr uint32_t kF3NoU = 0xffffffffu;
+__device__ __forceinline__ uint32_t f3_uniform(double xl, double xh)
+{
+    const double kl = floor(xl * (1.0 - 1.0 / 32768.0) + 0.5), kh = floor(xh * (1.0 + 1.0 / 32768.0) + 0.5);
+    return kl == kh && kl < 1073741824.0 ? (uint32_t)kl : kF3NoU;
+}
+
 // Pass 2's step for one element from its role word w (table index idx):
 // the seq-1 increment k = rint(a~ 2^sh) and its level slot, or a listed or
 // ambiguous element (rare).  The same code serves the batched pass and the
@@ -481,20 +546,23 @@ __device__ __forceinline__ F3K23 f3_k23(uint2 w, float y, float m, float cS, flo
     return r;
 }
 
-// A batched pass over the row's float4 body: kUnroll float4 loads per thread
-// in flight, then for the 4 kUnroll elements: table indices, role words
-// (their LDS reads issued together), the common step's level increments
-// (unconditional: a non-count adds 0 to the spare slot), and the rare
-// elements one by one when the wave has any.  The 0-3 elements before the
-// 16-byte boundary and the ragged end go through `one`.
-template <class YF, class WORD, class COMMON, class RARE, class ONE>
-__device__ __forceinline__ void f3_pass(const float *row, int V, YF yf, WORD word, COMMON common, RARE rare, ONE one)
+// A pass over the row with the elements that need work compacted per wave.
+// Each thread holds 4 kUnroll elements (kUnroll float4 loads in flight); their
+// role words are read together (word), those that ask for work (act) are
+// appended to the wave's ring in LDS (q, QN entries of (y, index)), and each
+// time 64 have gathered every lane of the wave processes one (work).  An
+// element of a bin without work costs its bin lookup only.  The 0-3 elements
+// before the 16-byte boundary and the ragged end go to work directly.
+template <int QN, class YF, class WORD, class ACT, class WORK>
+__device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD word, ACT act, WORK work, uint2 *q)
 {
-    const int t = threadIdx.x;
+    static_assert(QN >= 128 && (QN & (QN - 1)) == 0, "ring");
+    const int t = threadIdx.x, lane = lane_id();
     const int h0 = min(V, (int)(((16u - ((uint32_t)reinterpret_cast<uintptr_t>(row) & 15u)) & 15u) >> 2));
     const float4 *r4 = reinterpret_cast<const float4 *>(row + h0);
     const int n4 = (V - h0) >> 2;
     constexpr int kE = 4 * kUnroll;
+    uint32_t qh = 0, qt = 0;
     for (int base = 0; base < n4; base += kThreads * kUnroll) {
         float4 v[kUnroll];
 #pragma unroll
@@ -512,11 +580,36 @@ __device__ __forceinline__ void f3_pass(const float *row, int V, YF yf, WORD wor
 #pragma unroll
         for (int e = 0; e < kE; e++) w[e] = word(y[e]);
 #pragma unroll
-        for (int e = 0; e < kE; e++)
-            if (common(w[e], y[e])) rare(h0 + 4 * (base + (e >> 2) * kThreads + t) + (e & 3), y[e], w[e]);
+        for (int e = 0; e < kE; e++) {
+            const bool a = act(w[e]);
+            const uint64_t bm = __ballot(a);
+            if (bm) {
+                const uint32_t off =
+                    __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+                if (a)
+                    q[(qt + off) & (QN - 1)] =
+                        make_uint2(__float_as_uint(y[e]), (uint32_t)(h0 + 4 * (base + (e >> 2) * kThreads + t) + (e & 3)));
+                qt += (uint32_t)__popcll(bm);
+                if (qt - qh >= 64u) {
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    const uint2 it = q[(qh + (uint32_t)lane) & (QN - 1)];
+                    work((int)it.y, __uint_as_float(it.x));
+                    qh += 64u;
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                }
+            }
+        }
     }
-    if (t < h0) one(t, yf(ldg(row + t)));
-    for (int i = h0 + (n4 << 2) + t; i < V; i += kThreads) one(i, yf(ldg(row + i)));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if ((uint32_t)lane < qt - qh) {
+        const uint2 it = q[(qh + (uint32_t)lane) & (QN - 1)];
+        work((int)it.y, __uint_as_float(it.x));
+    }
+    if (t < h0) work(t, yf(ldg(row + t)));
+    for (int i = h0 + (n4 << 2) + t; i < V; i += kThreads) work(i, yf(ldg(row + i)));
 }
 
 // The exact full-vocabulary path, increment-histogram form.  Returns true
@@ -662,7 +755,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     const int nover = f.nover;
     const double iw = 1.0 / (double)kFInvW;
     // exp(y - m) at bin position bpos (the centre of bin b at b + 0.5)
-    auto e_at = [&](double bpos) { return exp(((double)cb - bpos) * iw - (double)m); };
+    auto e_at = [&](double bpos) { return (double)f3_exp((float)(((double)cb - bpos) * iw - (double)m)); };
     const double dl = 1.0 - kFDelta, dh = 1.0 + kFDelta;
 
     // ---- plan A: the running seq-1 sum before each bin, predicted from the
@@ -730,7 +823,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         if (im >= 1) bmax = min(im - 1, kFBins - 1);
     }
     {
-        uint32_t key[kPer], klo[kPer], khi[kPer], c[kPer];
+        uint32_t key[kPer], klo[kPer], khi[kPer], c[kPer], ku[kPer];
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
             const int b = kPer * t + q;
@@ -740,14 +833,16 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             key[q] = win ? kF3KeyListed : (uint32_t)(e + 256);
             klo[q] = 1u;
             khi[q] = 0u;
+            ku[q] = kF3NoU;
             if (!win) {
                 float ylo, yhi;
                 f3_range(cb, b, &ylo, &yhi);
                 const double sc = ldexp(1.0, 23 - e);
-                const double xlo = (double)glibc_expf_tab(ylo - m, f.exptab) * sc * kF3Lo;
-                const double xhi = (double)glibc_expf_tab(yhi - m, f.exptab) * sc * kF3Hi;
-                klo[q] = (uint32_t)fmin(floor(xlo), 1073741824.0);
-                khi[q] = (uint32_t)fmin(floor(xhi + 0.5), 1073741824.0);
+                const double xl = (double)f3_exp(ylo - m) * sc;      // (within 2^-18.5: the margins hold it)
+                const double xh = (double)f3_exp(yhi - m) * sc;
+                klo[q] = (uint32_t)fmin(floor(xl * kF3Lo), 1073741824.0);
+                khi[q] = (uint32_t)fmin(floor(xh * kF3Hi + 0.5), 1073741824.0);
+                ku[q] = f3_uniform(xl, xh);
             }
             f.lvl[b] = key[q];
             f.lvl[kFBins + b] = khi[q];
@@ -768,6 +863,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             }
             ssum += c[q];
         }
+        F3_TS(26);
         uint32_t call;
         const uint32_t sp = block_excl_u32(ssum, &call, sm);
         if (t == 0) f.bH = kFBins;
@@ -788,7 +884,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
 #pragma unroll
         for (int q = 0; q < kPer; q++) if (kPer * t + q < bH) key[q] = kF3KeyListed;
         int rid[kPer];
+        F3_TS(27);
         if (!f3_plan_runs(sm, f, 0, bH, key, klo, khi, rid, 0u, (uint32_t)kF3L1)) F3_FAIL();
+        F3_TS(28);
         uint32_t capv[kPer], capl = 0;
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
@@ -806,7 +904,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             if (key[q] == kF3KeyListed) {
                 wv[q] = kF3Listed | o;
                 stg(segst + b, o);
-            } else if (khi[q] >= 1u) {
+            } else if (khi[q] >= 1u && ku[q] == kF3NoU) {
                 const F3Run &R = f.run[0][rid[q]];
                 wv[q] = kF3In2 | ((uint32_t)(23 - R.e) << 24) | (uint32_t)(R.off + (1 << 23));
             }
@@ -821,7 +919,18 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         if (t == 0) { f.w[0] = 0u; f.w[kFBins + 1] = 0u; f.list_end = (uint32_t)nover + ltot; f.bH = bH; }
         for (int j = t; j <= kF3Lvl; j += kThreads) f.lvl[j] = 0u;
         __syncthreads();
-        if (f.list_end > cap) F3_FAIL();
+        // uniform bins: every element adds ku (the count is exact)
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            if (key[q] != kF3KeyListed && ku[q] != kF3NoU && ku[q] != 0u && f.cnt[b]) {
+                const F3Run &R = f.run[0][rid[q]];
+                if (ku[q] - R.klo < R.span) atomicAdd(&f.lvl[R.off + (int)ku[q]], f.cnt[b]);
+                else f.fail = 1;
+            }
+        }
+        __syncthreads();
+        if (f.list_end > cap || f.fail) F3_FAIL();
     }
     const int bH = f.bH;
     F3_STAT(1, bH);
@@ -852,8 +961,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const uint32_t w = word(y);
             if (common(w, y)) rare(i, y, w);
         };
-        if (t_one) f3_pass(row, V, [](float x) { return x; }, word, common, rare, one);
-        else f3_pass(row, V, [&](float x) { return x / T; }, word, common, rare, one);
+        auto act = [](uint32_t w) { return w != 0u; };
+        uint2 *ring = reinterpret_cast<uint2 *>(f.u.w23) + 256 * wave_id();
+        if (t_one) f3_qpass<256>(row, V, [](float x) { return x; }, word, act, one, ring);
+        else f3_qpass<256>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
         __syncthreads();
         if (has_pen) {
             // the raw values of penalized ids leave (listed and ambiguous
@@ -911,12 +1022,14 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
 
     // ---- walk S (src/sampler.rs:54) ----------------------------------------
     f3_totals(sm, f, 0);
+    F3_TS(29);
     {
         const uint32_t n = f.list_end;
         if (n > (uint32_t)kF3Lvl) F3_FAIL();
         for (uint32_t j = t; j < n; j += kThreads) stg_lds[j] = ldg(sa1 + j);
     }
     if (!f3_regions(sm, f, bH, [&](int b) { return ldg(role + b); })) F3_FAIL();
+    F3_TS(30);
     if (wave_id() == 0) {
         float S;
         uint32_t arr, pos;
@@ -967,7 +1080,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         cS3lo = __double2float_rd(iS / s2hi);
         band3 = (float)((double)kF3Band23 * 2.0 + (s2hi / s2lo - 1.0));
         __syncthreads();
-        uint32_t key2[kPer], key3[kPer], klo2[kPer], khi2[kPer], klo3[kPer], khi3[kPer], rl[kPer];
+        uint32_t key2[kPer], key3[kPer], klo2[kPer], khi2[kPer], klo3[kPer], khi3[kPer], rl[kPer], ku2[kPer],
+            ku3[kPer];
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
             const int b = kPer * t + q;
@@ -975,6 +1089,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             key2[q] = key3[q] = kF3KeyNone;
             klo2[q] = klo3[q] = 1u;
             khi2[q] = khi3[q] = 0u;
+            ku2[q] = ku3[q] = kF3NoU;
             rl[q] = 0u;
             if (b < bH) continue;
             const bool past = nuc && lo2 * dl >= tp;
@@ -982,8 +1097,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const bool cw = nuc && hi2 * dh >= tp;
             float ylo, yhi;
             f3_range(cb, b, &ylo, &yhi);
-            const double plo = (double)glibc_expf_tab(ylo - m, f.exptab) * iS * kF3Lo;
-            const double phi = (double)glibc_expf_tab(yhi - m, f.exptab) * iS * kF3Hi;
+            const double pl = (double)f3_exp(ylo - m) * iS;
+            const double ph = (double)f3_exp(yhi - m) * iS;
+            const double plo = pl * kF3Lo, phi = ph * kF3Hi;
             if (nuc) {
                 if (cw || !(lo2 > 0.0) || f_dexp(lo2 * dl) != f_dexp(hi2 * dh)) {
                     key2[q] = kF3KeyListed;
@@ -994,6 +1110,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                     const double sc = ldexp(1.0, 23 - e2);
                     klo2[q] = (uint32_t)fmin(floor(plo * sc), 1073741824.0);
                     khi2[q] = (uint32_t)fmin(floor(phi * sc + 0.5), 1073741824.0);
+                    ku2[q] = f3_uniform(pl * sc, ph * sc);
                 }
             }
             const double c3lo = lo2 / s2hi, c3hi = hi2 / s2lo;
@@ -1007,8 +1124,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 const double sc = ldexp(1.0, 23 - e3);
                 klo3[q] = (uint32_t)fmin(floor(plo / s2hi * sc), 1073741824.0);
                 khi3[q] = (uint32_t)fmin(floor(phi / s2lo * sc + 0.5), 1073741824.0);
+                ku3[q] = f3_uniform(pl / s2hi * sc, ph / s2lo * sc);
             }
         }
+        F3_TS(31);
         int rid2[kPer], rid3[kPer];
         if (!f3_plan_runs(sm, f, 0, bH, key2, klo2, khi2, rid2, 0u, (uint32_t)kF3L23)) F3_FAIL();
         if (!f3_plan_runs(sm, f, 1, bH, key3, klo3, khi3, rid3, (uint32_t)kF3L23, (uint32_t)kF3L23)) F3_FAIL();
@@ -1047,11 +1166,11 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 wv[q].x = kF3Listed | o;
                 stg(segst + b, o);
             } else {
-                if (rid2[q] >= 0 && khi2[q] >= 1u) {
+                if (rid2[q] >= 0 && khi2[q] >= 1u && ku2[q] == kF3NoU) {
                     const F3Run &R = f.run[0][rid2[q]];
                     wv[q].x = kF3In2 | ((uint32_t)(23 - R.e) << 24) | (uint32_t)(R.off + (1 << 23));
                 }
-                if (rid3[q] >= 0 && khi3[q] >= 1u) {
+                if (rid3[q] >= 0 && khi3[q] >= 1u && ku3[q] == kF3NoU) {
                     const F3Run &R = f.run[1][rid3[q]];
                     wv[q].y = kF3W3 | ((uint32_t)(23 - R.e) << 24) | (uint32_t)(R.off + (1 << 23));
                 }
@@ -1074,7 +1193,24 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         for (int j = t; j <= kF3Lvl; j += kThreads) f.lvl[j] = 0u;
         __syncthreads();
-        if (ltot > (uint32_t)cap) F3_FAIL();
+        // uniform bins of the runs (not listed): every element adds ku
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int b = kPer * t + q;
+            if (rl[q] || !f.cnt[b]) continue;
+            if (rid2[q] >= 0 && ku2[q] != kF3NoU && ku2[q] != 0u) {
+                const F3Run &R = f.run[0][rid2[q]];
+                if (ku2[q] - R.klo < R.span) atomicAdd(&f.lvl[R.off + (int)ku2[q]], f.cnt[b]);
+                else f.fail = 1;
+            }
+            if (rid3[q] >= 0 && ku3[q] != kF3NoU && ku3[q] != 0u) {
+                const F3Run &R = f.run[1][rid3[q]];
+                if (ku3[q] - R.klo < R.span) atomicAdd(&f.lvl[R.off + (int)ku3[q]], f.cnt[b]);
+                else f.fail = 1;
+            }
+        }
+        __syncthreads();
+        if (ltot > (uint32_t)cap || f.fail) F3_FAIL();
     }
     F3_TS(6);
 
@@ -1109,8 +1245,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const uint2 w = word(y);
             if (common(w, y)) rare(i, y, w);
         };
-        if (t_one) f3_pass(row, V, [](float x) { return x; }, word, common, rare, one);
-        else f3_pass(row, V, [&](float x) { return x / T; }, word, common, rare, one);
+        auto act = [](uint2 w) { return (w.x | w.y) != 0u; };
+        uint2 *ring = reinterpret_cast<uint2 *>(f.pre) + 128 * wave_id();
+        if (t_one) f3_qpass<128>(row, V, [](float x) { return x; }, word, act, one, ring);
+        else f3_qpass<128>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
         __syncthreads();
         F3_TS(10);
         if (has_pen) {

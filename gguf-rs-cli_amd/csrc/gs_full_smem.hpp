@@ -115,7 +115,7 @@ struct Full3Smem {
         uint2 w23[kF3Tab];             // pass 3: role words of seqs 2, 3
     } u;
     uint32_t lvl[kF3Lvl + 1];  // level counters (plans: per-bin temporaries; walks: staged summands)
-    float pre[kFBins + 1];     // predicted seq-1 sum before each bin ([kFBins]: the total)
+    alignas(16) float pre[kFBins + 1];   // predicted seq-1 sum before each bin ([kFBins]: the total); pass 3: element rings
     uint64_t over[kFOverCap];
     uint64_t exptab[32];
     F3Run run[2][kF3Runs];     // seq 1, then seq 2 | seq 3
