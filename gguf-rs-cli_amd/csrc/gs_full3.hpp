@@ -348,6 +348,8 @@ __device__ __forceinline__ int f3_tidx(float y, float cb)
     const float tb = __builtin_amdgcn_fmed3f(fmaf(y, -kFInvW, cb), -1.0f, (float)kFBins);
     return (int)floorf(tb) + 1;
 }
+// The bin of y clamped to [0, kFBins) (for entries known to lie in a bin).
+__device__ __forceinline__ int f3_bin(float y, float cb) { return min(max(f3_tidx(y, cb) - 1, 0), kFBins - 1); }
 // A y-interval holding every element of bin b (the index is computed in f32;
 // the margin covers its rounding).
 __device__ __forceinline__ void f3_range(float cb, int b, float *ylo, float *yhi)
@@ -364,8 +366,10 @@ __device__ __forceinline__ void f3_range(float cb, int b, float *ylo, float *yhi
 // start plus its rank there (the number of greater entries: key descending,
 // then index ascending).  sa gets its summand a = expf(y - m), 0 for an
 // entry that left the list.  cend(b): the segment's end.
+// Every position is checked to lie in [0, n) before it is read or written
+// (a segment that the pass did not fill as planned fails the row instead).
 template <class CE>
-__device__ void f3_sort_list(const Full3Smem &f, const uint64_t *lst, uint32_t n, uint32_t nover,
+__device__ void f3_sort_list(Full3Smem &f, const uint64_t *lst, uint32_t n, uint32_t nover,
                              const uint32_t *segst, CE cend, uint64_t *se, float *sa)
 {
     for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
@@ -374,9 +378,11 @@ __device__ void f3_sort_list(const Full3Smem &f, const uint64_t *lst, uint32_t n
         uint32_t st = 0, end = nover;
         if (j >= nover) {
             const int b = f3_tidx(y, f.cb) - 1;
+            if (b < 0 || b >= kFBins) { f.fail = 1; continue; }
             st = ldg(segst + b);
             end = cend(b);
         }
+        if (!(st <= j && j < end && end <= n)) { f.fail = 1; continue; }
         uint32_t rank = 0;
         uint32_t q = st;
         for (; q + 8 <= end; q += 8) {
@@ -387,6 +393,7 @@ __device__ void f3_sort_list(const Full3Smem &f, const uint64_t *lst, uint32_t n
             for (int u = 0; u < 8; u++) rank += e8[u] > en ? 1u : 0u;
         }
         for (; q < end; q++) rank += ldg(lst + q) > en ? 1u : 0u;
+        if (st + rank >= end) { f.fail = 1; continue; }
         stg(se + st + rank, en);
         stg(sa + st + rank, f3_live(en) ? glibc_expf_tab(y - f.m, f.exptab) : 0.0f);
     }
@@ -403,6 +410,7 @@ __device__ __forceinline__ void f3_exact_k(float x, uint32_t *k, bool *tie)
 // Count an exactly known increment of run r (table s): a level, or a tie.
 __device__ __forceinline__ void f3_count_exact(Full3Smem &f, int s, int r, float x)
 {
+    if ((uint32_t)r >= (uint32_t)f.nrun[s]) { f.fail = 1; return; }
     uint32_t k;
     bool tie;
     f3_exact_k(x, &k, &tie);
@@ -1008,7 +1016,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const uint64_t en = ldg(amb + j);
             if (!f3_live(en)) continue;
             const float y = f_entry_y(en);
-            const int run = (int)ldg(role + f3_tidx(y, cb) - 1);
+            const int run = (int)ldg(role + f3_bin(y, cb));
             f3_count_exact(f, 0, run, ldexpf(glibc_expf_tab(y - m, f.exptab), 23 - f.run[0][run].e));
         }
     }
@@ -1302,7 +1310,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const uint64_t en = ldg(amb + j);
             if (!f3_live(en)) continue;
             const float y = f_entry_y(en);
-            const int rr = (int)((ldg(role + f3_tidx(y, cb) - 1) >> 8) & 63u);
+            const int rr = (int)((ldg(role + f3_bin(y, cb)) >> 8) & 63u);
             const float p = glibc_expf_tab(y - m, f.exptab) / S;
             f3_count_exact(f, 0, rr, ldexpf(p, 23 - f.run[0][rr].e));
         }
@@ -1312,7 +1320,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             for (uint32_t j = t; j < f.list_end; j += kThreads) {
                 const uint64_t en = ldg(se3 + j);
                 if (!f3_live(en)) continue;
-                const uint32_t rw = ldg(role + f3_tidx(f_entry_y(en), cb) - 1);
+                const uint32_t rw = ldg(role + f3_bin(f_entry_y(en), cb));
                 if (!(rw & kF3In2)) continue;
                 const int rr = (int)((rw >> 8) & 63u);
                 const float p = ldg(sa3 + j) / S;
@@ -1356,9 +1364,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         cut_arr = f.cut_arr;
         cut_pos = f.cut_pos;
         // the cut must not lie inside a run of seq 3 (walk 3 stops there)
+        if (cut_arr == 1u ? cut_pos >= nl3 : cut_pos >= headend) F3_FAIL();
         if (cut_arr == 1u) {
             const uint64_t en = ldg(se3 + cut_pos);
-            if (ldg(role + f3_tidx(f_entry_y(en), cb) - 1) & kF3In3) F3_FAIL();
+            if (ldg(role + f3_bin(f_entry_y(en), cb)) & kF3In3) F3_FAIL();
         }
         if (!(s2 >= f.s2lo && s2 <= f.s2hi)) F3_FAIL();
     }
@@ -1372,13 +1381,13 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const uint64_t en = ldg(def + j);
             if (!f3_live(en)) continue;
             const float y = f_entry_y(en);
-            const int rr = (int)(ldg(role + f3_tidx(y, cb) - 1) & 63u);
+            const int rr = (int)(ldg(role + f3_bin(y, cb)) & 63u);
             f3_count_exact(f, 1, rr, ldexpf(qv(glibc_expf_tab(y - m, f.exptab)), 23 - f.run[1][rr].e));
         }
         for (uint32_t j = t; j < nl3; j += kThreads) {
             const uint64_t en = ldg(se3 + j);
             if (!f3_live(en)) continue;
-            const uint32_t rw = ldg(role + f3_tidx(f_entry_y(en), cb) - 1);
+            const uint32_t rw = ldg(role + f3_bin(f_entry_y(en), cb));
             if (!(rw & kF3In3)) continue;
             const int rr = (int)(rw & 63u);
             f3_count_exact(f, 1, rr, ldexpf(qv(ldg(sa3 + j)), 23 - f.run[1][rr].e));
@@ -1410,6 +1419,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         __syncthreads();
         if (f.walk_res != 1 && f.walk_res != 2) F3_FAIL();
+        if (f.tok_arr ? f.tok_pos >= nl3 : f.tok_pos >= headend) F3_FAIL();
         const uint64_t en = ldg((f.tok_arr ? se3 : se1) + f.tok_pos);
         if (!f3_live(en)) F3_FAIL();
         *tok = (int)f_entry_id(en);
