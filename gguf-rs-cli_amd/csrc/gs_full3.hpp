@@ -72,6 +72,49 @@ constexpr double kF3Lo = 1.0 - 1.0 / 65536.0, kF3Hi = 1.0 + 1.0 / 65536.0;   // 
 __device__ __forceinline__ bool f3_live(uint64_t en) { return ((uint32_t)en & 0x80000000u) != 0u; }
 __device__ __forceinline__ uint64_t f3_dead(uint64_t en) { return (en & 0xffffffff00000000ull) | (uint64_t)(~(uint32_t)en); }
 
+// 16-bit level counters, two per LDS word: slot j is the low (j even) or
+// high half of word j / 2.  f.lcount[s] counts every increment, so that a
+// counter that wrapped shows as a total that does not match.
+__device__ __forceinline__ void f3_lvl_add(Full3Smem &f, int slot, uint32_t n)
+{
+    atomicAdd(&f.lvl[slot >> 1], n << ((slot & 1) << 4));
+}
+__device__ __forceinline__ uint32_t f3_lvl_get(const Full3Smem &f, uint32_t slot)
+{
+    return (f.lvl[slot >> 1] >> ((slot & 1u) << 4)) & 0xffffu;
+}
+// Add every thread's count n to f.lcount[s] (one atomic per wave; all
+// threads call).
+__device__ __forceinline__ void f3_lcount(Full3Smem &f, int s, uint32_t n)
+{
+    for (int d = 32; d > 0; d >>= 1) n += __shfl_xor(n, d, 64);
+    if (lane_id() == 0 && n) atomicAdd(&f.lcount[s], n);
+}
+
+// Wave64 inclusive scan of ParFn with DPP moves, without branches (the
+// lower lane's value is always the left operand).
+template <int CTRL>
+__device__ __forceinline__ void f3_dpp_step(ParFn &v, bool take)
+{
+    ParFn o;
+    o.f0 = dpp_mov<CTRL>(v.f0);
+    o.f1 = dpp_mov<CTRL>(v.f1);
+    const ParFn c = par_compose(o, v);
+    v.f0 = take ? c.f0 : v.f0;
+    v.f1 = take ? c.f1 : v.f1;
+}
+__device__ __forceinline__ ParFn f3_wave_scan(ParFn v)
+{
+    const int lane = lane_id(), rl = lane & 15;
+    f3_dpp_step<0x111>(v, rl >= 1);      // row_shr:1
+    f3_dpp_step<0x112>(v, rl >= 2);      // row_shr:2
+    f3_dpp_step<0x114>(v, rl >= 4);      // row_shr:4
+    f3_dpp_step<0x118>(v, rl >= 8);      // row_shr:8
+    f3_dpp_step<0x142>(v, (lane & 31) >= 16);   // row_bcast:15
+    f3_dpp_step<0x143>(v, lane >= 32);          // row_bcast:31
+    return v;
+}
+
 // Exact sequential f32 adds cum = RN(cum + v[j]) over LDS values v[beg, end)
 // on one wave (every lane calls with the same arguments), stopping at the
 // first j after which pred(cum) holds (pred is monotone: the sums only
@@ -93,24 +136,34 @@ __device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *
     float cum = *cum_io;
     uint32_t j0 = beg;
     {
-        const uint32_t js = min(end, beg + nseq);
-        for (; j0 < js; j0 += 8u) {
-            float c[8];
-            float x = cum;
+        // eight values per group; the next group's LDS reads are issued
+        // before the current group's adds
+        const uint32_t js = (beg & 3u) ? beg : beg + (min(end - beg, nseq) & ~7u);
+        if (j0 < js) {
+            float4 n0 = *reinterpret_cast<const float4 *>(v + j0), n1 = *reinterpret_cast<const float4 *>(v + j0 + 4);
+            for (; j0 < js; j0 += 8u) {
+                const float cur[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+                if (j0 + 8u < js) {
+                    n0 = *reinterpret_cast<const float4 *>(v + j0 + 8);
+                    n1 = *reinterpret_cast<const float4 *>(v + j0 + 12);
+                }
+                float c[8];
+                float x = cum;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                x = x + (j0 + i < js ? v[j0 + i] : 0.0f);
-                c[i] = x;
+                for (int i = 0; i < 8; i++) {
+                    x = x + cur[i];
+                    c[i] = x;
+                }
+                if (pred(c[7])) {          // pred is monotone: the first of the 8 that holds
+                    int i = 0;
+                    while (!pred(c[i])) i++;
+                    *cum_io = c[i];
+                    return j0 + (uint32_t)i;
+                }
+                cum = c[7];
             }
-            if (pred(c[7])) {          // pred is monotone: the first of the 8 that holds
-                int i = 0;
-                while (!pred(c[i])) i++;
-                *cum_io = c[i];
-                return j0 + (uint32_t)i;
-            }
-            cum = c[7];
+            j0 = js;
         }
-        j0 = js;
     }
     while (j0 < end) {
         const uint32_t jl = j0 + 4u * (uint32_t)lane;
@@ -124,7 +177,7 @@ __device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *
         ParFn loc = fc[0];
 #pragma unroll
         for (int c = 1; c < 4; c++) loc = par_compose(loc, fc[c]);
-        const ParFn incl = wave_scan_incl(loc);
+        const ParFn incl = f3_wave_scan(loc);
         ParFn ex;
         ex.f0 = __shfl_up(incl.f0, 1, 64);
         ex.f1 = __shfl_up(incl.f1, 1, 64);
@@ -215,6 +268,7 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
     const uint32_t lb = s ? (uint32_t)kF3L23 : 0u;
     const uint32_t per = (ltot + kThreads - 1) / kThreads;
     const uint32_t j0 = lb + min((uint32_t)t * per, ltot), j1 = min(j0 + per, lb + ltot);
+    uint32_t ncount = 0;
     if (j0 < j1) {
         int r = 0;
         while (r + 1 < nrun && f.run[s][r + 1].base <= j0) r++;
@@ -226,20 +280,25 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
                 r++;
             }
             const uint32_t k = (uint32_t)((int)j - f.run[s][r].off);
-            part += (uint64_t)k * f.lvl[j];
+            const uint32_t n = f3_lvl_get(f, j);
+            part += (uint64_t)k * n;
+            ncount += n;
         }
         if (part) atomicAdd((unsigned long long *)&f.rtot[s][r], (unsigned long long)part);
     }
+    for (int d = 32; d > 0; d >>= 1) ncount += __shfl_xor(ncount, d, 64);
+    if (lane_id() == 0 && ncount) atomicSub(&f.lcount[s], ncount);
     for (int i = 0; i < nt; i++) {
         const F3Tie T = f.tie[s][i];
         const F3Run &R = f.run[s][T.run];
         const uint32_t a0 = max(j0, (uint32_t)(R.off + (int)T.k + 1)), a1 = min(j1, R.base + R.span);
         uint64_t part = 0;
-        for (uint32_t j = a0; j < a1; j++) part += (uint64_t)((int)j - R.off) * f.lvl[j];
+        for (uint32_t j = a0; j < a1; j++) part += (uint64_t)((int)j - R.off) * f3_lvl_get(f, j);
         for (int d = 32; d > 0; d >>= 1) part += __shfl_xor(part, d, 64);
         if (lane_id() == 0 && part) atomicAdd((unsigned long long *)&f.tie[s][i].A, (unsigned long long)part);
     }
     __syncthreads();
+    if (f.lcount[s] != 0u) f.fail = 1;    // a 16-bit counter wrapped
     if (t == 0) {
         for (int i = 1; i < nt; i++) {
             const F3Tie x = f.tie[s][i];
@@ -258,7 +317,7 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
 // the same key (a run id, kF3KeyListed or kF3KeyNone).  False if more than
 // kF3Regs.
 template <class K>
-__device__ bool f3_regions(RowSmem &sm, Full3Smem &f, int bH, K key)
+__device__ bool f3_regions(RowSmem &sm, Full3Smem &f, int bH, const uint32_t *segst, K key)
 {
     constexpr int kPer = kFBins / kThreads;
     const int t = threadIdx.x;
@@ -285,7 +344,9 @@ __device__ bool f3_regions(RowSmem &sm, Full3Smem &f, int bH, K key)
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         if (st[q]) {
-            if (o < (uint32_t)kF3Regs) f.reg[o] = F3Reg{(uint32_t)(kPer * t + q), kk[q]};
+            if (o < (uint32_t)kF3Regs)
+                f.reg[o] = F3Reg{(uint32_t)(kPer * t + q), kk[q],
+                                 kk[q] == kF3KeyListed ? ldg(segst + kPer * t + q) : 0u};
             o++;
         }
     }
@@ -311,7 +372,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
         uint32_t end = f.headend;
         const bool at = lim && lim_arr == 0u;
         if (at) end = lim_pos + 1u;
-        const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 256u);
+        const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 64u);
         F3_TS(16 + 5 * s);
         *cum_out = cum;
         if (p < end) { *arr = 0u; *pos = p; return 1; }
@@ -323,7 +384,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
         if (R.key == kF3KeyNone) break;
         if (R.key == kF3KeyListed) {
             const uint32_t b1 = g + 1 < nreg ? f.reg[g + 1].b0 - 1u : (uint32_t)kFBins - 1u;
-            const uint32_t beg = ldg(segst + R.b0);
+            const uint32_t beg = R.beg;
             uint32_t end = cend(b1);
             const bool at = lim && lim_arr == 1u && lim_pos >= beg && lim_pos < end;
             if (at) end = lim_pos + 1u;
@@ -422,7 +483,8 @@ __device__ __forceinline__ void f3_count_exact(Full3Smem &f, int s, int r, float
     }
     if (k == 0u) return;
     if (k - R.klo >= R.span) { f.fail = 1; return; }
-    atomicAdd(&f.lvl[R.off + (int)k], 1u);
+    f3_lvl_add(f, R.off + (int)k, 1u);
+    atomicAdd(&f.lcount[s], 1u);
 }
 
 // Plan of one accumulation's runs over bins [bH, kFBins).  Per bin (kPer per
@@ -524,7 +586,7 @@ __device__ __forceinline__ F3K f3_k1(uint32_t w, float y, float m)
     const bool in = (w & kF3In2) != 0u;
     F3K r;
     r.slot = (int)(w & kF3Cur) - (1 << 23) + (int)k;
-    r.ok = in && !amb && (uint32_t)r.slot < (uint32_t)kF3Lvl;
+    r.ok = in && !amb && (uint32_t)r.slot < (uint32_t)kF3H;
     r.rare = (w & kF3Listed) || (in && !r.ok);
     return r;
 }
@@ -540,7 +602,7 @@ __device__ __forceinline__ F3K23 f3_k23(uint2 w, float y, float m, float cS, flo
         const float k = rintf(x);
         const bool amb = fabsf(x - k) >= fmaf(-x, kF3Band23, 0.5f);
         r.slot2 = (int)(w.x & kF3Cur) - (1 << 23) + (int)k;
-        r.ok2 = (w.x & kF3In2) && !amb && (uint32_t)r.slot2 < (uint32_t)kF3Lvl;
+        r.ok2 = (w.x & kF3In2) && !amb && (uint32_t)r.slot2 < (uint32_t)kF3H;
     }
     {
         // x over the range of s2 lies in [x0, x0 (1 + band3 - kF3Band23)]
@@ -548,7 +610,7 @@ __device__ __forceinline__ F3K23 f3_k23(uint2 w, float y, float m, float cS, flo
         const float k = rintf(x0);
         const bool amb = fabsf(x0 - k) >= fmaf(-x0, band3, 0.5f);
         r.slot3 = (int)(w.y & kF3Cur) - (1 << 23) + (int)k;
-        r.ok3 = (w.y & kF3W3) && !amb && (uint32_t)r.slot3 < (uint32_t)kF3Lvl;
+        r.ok3 = (w.y & kF3W3) && !amb && (uint32_t)r.slot3 < (uint32_t)kF3H;
     }
     r.rare = (w.x & kF3Listed) || ((w.x & kF3In2) && !r.ok2) || ((w.y & kF3W3) && !r.ok3);
     return r;
@@ -924,19 +986,31 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < kPer; q++) f.w[1 + kPer * t + q] = wv[q];
-        if (t == 0) { f.w[0] = 0u; f.w[kFBins + 1] = 0u; f.list_end = (uint32_t)nover + ltot; f.bH = bH; }
+        if (t == 0) {
+            f.w[0] = 0u;
+            f.w[kFBins + 1] = 0u;
+            f.list_end = (uint32_t)nover + ltot;
+            f.bH = bH;
+            f.lcount[0] = 0u;
+        }
         for (int j = t; j <= kF3Lvl; j += kThreads) f.lvl[j] = 0u;
         __syncthreads();
         // uniform bins: every element adds ku (the count is exact)
+        uint32_t nadd = 0;
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
             const int b = kPer * t + q;
             if (key[q] != kF3KeyListed && ku[q] != kF3NoU && ku[q] != 0u && f.cnt[b]) {
                 const F3Run &R = f.run[0][rid[q]];
-                if (ku[q] - R.klo < R.span) atomicAdd(&f.lvl[R.off + (int)ku[q]], f.cnt[b]);
-                else f.fail = 1;
+                if (ku[q] - R.klo < R.span && f.cnt[b] < 65536u) {
+                    f3_lvl_add(f, R.off + (int)ku[q], f.cnt[b]);
+                    nadd += f.cnt[b];
+                } else {
+                    f.fail = 1;
+                }
             }
         }
+        f3_lcount(f, 0, nadd);
         __syncthreads();
         if (f.list_end > cap || f.fail) F3_FAIL();
     }
@@ -950,10 +1024,12 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
 
     // ---- pass 2 (cache): seq-1 levels; listed bins written ------------------
     {
+        uint32_t nok = 0;      // level increments of this thread
         auto word = [&](float y) { return f.w[f3_tidx(y, cb)]; };
         auto common = [&](uint32_t w, float y) {
             const F3K k = f3_k1(w, y, m);
-            if (k.ok) atomicAdd(&f.lvl[k.slot], 1u);
+            if (k.ok) f3_lvl_add(f, k.slot, 1u);
+            nok += k.ok ? 1u : 0u;
             return k.rare;
         };
         auto rare = [&](int i, float y, uint32_t w) {
@@ -991,7 +1067,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                     continue;
                 }
                 const F3K k = f3_k1(w, y, m);
-                if (k.ok) atomicSub(&f.lvl[k.slot], 1u);
+                if (k.ok) {
+                    f3_lvl_add(f, k.slot, 0xffffffffu);
+                    nok--;
+                }
                 else if (k.rare) {
                     const uint32_t na = min((uint32_t)f.namb, (uint32_t)kF3AmbCap);
                     for (uint32_t p = 0; p < na; p++)
@@ -1005,6 +1084,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             __threadfence_block();
             __syncthreads();
         }
+        f3_lcount(f, 0, nok);
     }
     F3_STAT(4, f.namb);
     if (f.fail || (uint32_t)f.namb > kF3AmbCap) F3_FAIL();
@@ -1036,7 +1116,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         if (n > (uint32_t)kF3Lvl) F3_FAIL();
         for (uint32_t j = t; j < n; j += kThreads) stg_lds[j] = ldg(sa1 + j);
     }
-    if (!f3_regions(sm, f, bH, [&](int b) { return ldg(role + b); })) F3_FAIL();
+    if (!f3_regions(sm, f, bH, segst, [&](int b) { return ldg(role + b); })) F3_FAIL();
     F3_TS(30);
     if (wave_id() == 0) {
         float S;
@@ -1198,25 +1278,38 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             f.ntie[1] = 0;
             f.namb = 0;
             f.ndef = 0;
+            f.lcount[0] = 0u;
+            f.lcount[1] = 0u;
         }
         for (int j = t; j <= kF3Lvl; j += kThreads) f.lvl[j] = 0u;
         __syncthreads();
         // uniform bins of the runs (not listed): every element adds ku
+        uint32_t nadd2 = 0, nadd3 = 0;
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
             const int b = kPer * t + q;
             if (rl[q] || !f.cnt[b]) continue;
             if (rid2[q] >= 0 && ku2[q] != kF3NoU && ku2[q] != 0u) {
                 const F3Run &R = f.run[0][rid2[q]];
-                if (ku2[q] - R.klo < R.span) atomicAdd(&f.lvl[R.off + (int)ku2[q]], f.cnt[b]);
-                else f.fail = 1;
+                if (ku2[q] - R.klo < R.span && f.cnt[b] < 65536u) {
+                    f3_lvl_add(f, R.off + (int)ku2[q], f.cnt[b]);
+                    nadd2 += f.cnt[b];
+                } else {
+                    f.fail = 1;
+                }
             }
             if (rid3[q] >= 0 && ku3[q] != kF3NoU && ku3[q] != 0u) {
                 const F3Run &R = f.run[1][rid3[q]];
-                if (ku3[q] - R.klo < R.span) atomicAdd(&f.lvl[R.off + (int)ku3[q]], f.cnt[b]);
-                else f.fail = 1;
+                if (ku3[q] - R.klo < R.span && f.cnt[b] < 65536u) {
+                    f3_lvl_add(f, R.off + (int)ku3[q], f.cnt[b]);
+                    nadd3 += f.cnt[b];
+                } else {
+                    f.fail = 1;
+                }
             }
         }
+        f3_lcount(f, 0, nadd2);
+        f3_lcount(f, 1, nadd3);
         __syncthreads();
         if (ltot > (uint32_t)cap || f.fail) F3_FAIL();
     }
@@ -1225,11 +1318,14 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     // ---- pass 3 (cache): seq-2 and seq-3 levels above the cut; bins listed,
     // ambiguous seq-2 and undecided seq-3 elements set aside -----------------
     {
+        uint32_t nok2 = 0, nok3 = 0;
         auto word = [&](float y) { return f.u.w23[f3_tidx(y, cb)]; };
         auto common = [&](uint2 w, float y) {
             const F3K23 k = f3_k23(w, y, m, cS, cS3lo, band3);
-            if (k.ok2) atomicAdd(&f.lvl[k.slot2], 1u);
-            if (k.ok3) atomicAdd(&f.lvl[k.slot3], 1u);
+            if (k.ok2) f3_lvl_add(f, k.slot2, 1u);
+            if (k.ok3) f3_lvl_add(f, k.slot3, 1u);
+            nok2 += k.ok2 ? 1u : 0u;
+            nok3 += k.ok3 ? 1u : 0u;
             return k.rare;
         };
         auto rare = [&](int i, float y, uint2 w) {
@@ -1273,13 +1369,19 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                     continue;
                 }
                 const F3K23 k = f3_k23(w, y, m, cS, cS3lo, band3);
-                if (k.ok2) atomicSub(&f.lvl[k.slot2], 1u);
+                if (k.ok2) {
+                    f3_lvl_add(f, k.slot2, 0xffffffffu);
+                    nok2--;
+                }
                 else if (w.x & kF3In2) {
                     const uint32_t na = min((uint32_t)f.namb, (uint32_t)kF3AmbCap);
                     for (uint32_t p = 0; p < na; p++)
                         if (ldg(amb + p) == en) stg(amb + p, f3_dead(en));
                 }
-                if (k.ok3) atomicSub(&f.lvl[k.slot3], 1u);
+                if (k.ok3) {
+                    f3_lvl_add(f, k.slot3, 0xffffffffu);
+                    nok3--;
+                }
                 else if (w.y & kF3W3) {
                     const uint32_t nd = min((uint32_t)f.ndef, (uint32_t)kF3DefCap);
                     for (uint32_t p = 0; p < nd; p++)
@@ -1293,6 +1395,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             __threadfence_block();
             __syncthreads();
         }
+        f3_lcount(f, 0, nok2);
+        f3_lcount(f, 1, nok3);
         F3_STAT(7, f.list_end);
         F3_STAT(8, f.ndef);
         F3_STAT(9, f.namb);
@@ -1340,10 +1444,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     if (nuc) {
         f3_totals(sm, f, 0);
         F3_TS(12);
-        if (headend + nl3 > (uint32_t)kF3L23) F3_FAIL();
+        if (headend + nl3 > (uint32_t)kF3L23 / 2u) F3_FAIL();   // (the words of the seq-2 levels)
         for (uint32_t j = t; j < headend; j += kThreads) stg_lds[j] = ldg(sa1 + j) / S;
         for (uint32_t j = t; j < nl3; j += kThreads) stg_lds[headend + j] = ldg(sa3 + j) / S;
-        if (!f3_regions(sm, f, bH, [&](int b) {
+        if (!f3_regions(sm, f, bH, segst, [&](int b) {
                 const uint32_t rw = ldg(role + b);
                 return (rw & kF3L2Bit) ? kF3KeyListed : (rw & kF3In2) ? ((rw >> 8) & 63u) : kF3KeyNone;
             }))
@@ -1400,7 +1504,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         if (headend + nl3 > (uint32_t)kF3Lvl) F3_FAIL();
         for (uint32_t j = t; j < headend; j += kThreads) stg_lds[j] = qv(ldg(sa1 + j));
         for (uint32_t j = t; j < nl3; j += kThreads) stg_lds[headend + j] = qv(ldg(sa3 + j));
-        if (!f3_regions(sm, f, bH, [&](int b) {
+        if (!f3_regions(sm, f, bH, segst, [&](int b) {
                 const uint32_t rw = ldg(role + b);
                 return (rw & kF3L3Bit) ? kF3KeyListed : (rw & kF3In3) ? (rw & 63u) : kF3KeyNone;
             }))

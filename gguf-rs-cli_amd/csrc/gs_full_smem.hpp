@@ -86,9 +86,10 @@ struct FullSmem {
 
 // ---------------------------------------------------------------------------
 // LDS of the increment-histogram path (gs_full3.hpp).
-constexpr int kF3Lvl = 12288;       // level counters (+ one slot that absorbs non-counts)
-constexpr int kF3L1 = 4096;         // levels of seq 1 (pass 2)
-constexpr int kF3L23 = 6144;        // levels of each of seqs 2 and 3 (pass 3)
+constexpr int kF3Lvl = 12288;       // words of 16-bit level counters (two per word)
+constexpr int kF3H = 2 * kF3Lvl;    // level counters
+constexpr int kF3L1 = 8192;         // levels of seq 1 (pass 2)
+constexpr int kF3L23 = 12288;       // levels of each of seqs 2 and 3 (pass 3)
 constexpr int kF3Runs = 64;         // runs per accumulation
 constexpr int kF3Regs = 192;        // regions of one walk
 constexpr int kF3Ties = 64;         // rounding ties per accumulation
@@ -104,7 +105,7 @@ struct F3Run {
     uint32_t base;         // first level slot (off + klo)
     uint32_t span;         // level slots
 };
-struct F3Reg { uint32_t b0, key; };         // first bin, run id or kF3KeyListed / kF3KeyNone
+struct F3Reg { uint32_t b0, key, beg; };    // first bin, run id or kF3KeyListed / kF3KeyNone, list start
 struct F3Tie { uint32_t run, k; uint64_t A; };   // an element at k + 1/2 grid units; A: the run's levels above it
 
 struct Full3Smem {
@@ -114,7 +115,7 @@ struct Full3Smem {
         uint64_t mass64[kFMassBins];   // pass 1, plan A
         uint2 w23[kF3Tab];             // pass 3: role words of seqs 2, 3
     } u;
-    uint32_t lvl[kF3Lvl + 1];  // level counters (plans: per-bin temporaries; walks: staged summands)
+    alignas(16) uint32_t lvl[kF3Lvl + 1];  // level counters (plans: per-bin temporaries; walks: staged summands)
     alignas(16) float pre[kFBins + 1];   // predicted seq-1 sum before each bin ([kFBins]: the total); pass 3: element rings
     uint64_t over[kFOverCap];
     uint64_t exptab[32];
@@ -125,6 +126,7 @@ struct Full3Smem {
     uint32_t wlast[kWaves];    // region building: each wave's last key
     int nrun[2], ntie[2], nreg;
     uint32_t ltot[2];
+    uint32_t lcount[2];        // increments counted into each level table (checks the 16-bit counters)
     float m0, m, S, s2, s2lo, s2hi, cb;
     int nover, fail, namb, ndef, bH, walk_res;
     uint32_t headend, list_end, cut_arr, cut_pos, tok_pos, tok_arr, list2;
