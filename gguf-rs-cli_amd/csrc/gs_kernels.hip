@@ -1336,12 +1336,12 @@ __host__ __device__ __forceinline__ bool is_full_path(const gs_params &p, int V)
 
 // The row kernel's modes.  kModeSmall: greedy, degenerate and top-k rows
 // (and the virtual rows of chunked top-k rows); kModeBins: full-vocabulary
-// rows by the exact binned path; kModeSort: the full-vocabulary rows whose
-// binned checks failed (fb[b] = 1), by the sort path; kModeDetail: every
+// rows by the exact binned path, and in the same block, when its checks fail
+// (fb[b] = 1), the first binned form and then the sort path; kModeDetail: every
 // row sorted, with the diagnostic outputs.  (A kernel that runs both kinds
 // of rows in one launch was measured: instantiating it raises the binned
 // kernel's register spills from 5 to 72, and c3 by 7%.)
-enum { kModeSmall = 0, kModeBins = 1, kModeSort = 2, kModeDetail = 3 };
+enum { kModeSmall = 0, kModeBins = 1, kModeDetail = 3 };
 
 // A row of the chunked top-k path (gs_kernels.hpp: chunk_count etc.).
 __device__ __forceinline__ bool chunk_row(const gs_params &p, int V)
@@ -1381,7 +1381,6 @@ __device__ __forceinline__ void sample_row(RowSmem &sm, const RowArgs &a, int b,
         if (t == 0) a.fb[b] = 0;
         return;
     }
-    if (MODE == kModeSort && (!full || a.fb[b] == 0)) return;
     GS_STAMP(8 * MODE);
 #ifdef GS_TIMING
     if (MODE == kModeSmall && blockIdx.x == g_row && (threadIdx.x & 63) == 0)
@@ -1491,16 +1490,23 @@ __device__ __forceinline__ void sample_row(RowSmem &sm, const RowArgs &a, int b,
             done = full_v3_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
         }
         if (t == 0) a.fb[b] = done ? 0 : 1;
-        if (!done) return;   // the fallback kernel finishes the row
-    } else {
-        bool done = false;
-        if (sm.flag_nan) { status = GS_ERR_NAN; done = true; }
-        else if (MODE == kModeSort && keep == V && ((reinterpret_cast<uintptr_t>(row) & 3u) == 0)) {
-            // the first binned form (per-bin classes and thresholds), then the sort
+        if (!done && keep == V && ((reinterpret_cast<uintptr_t>(row) & 3u) == 0)) {
+            // the first binned form (per-bin classes and thresholds)
+            __syncthreads();
             uint64_t *gl = reinterpret_cast<uint64_t *>(a.scratch + (size_t)b * a.scratch_stride);
             const uint32_t lcap = (uint32_t)(a.scratch_stride / 2);
             done = full_v2_row(sm, row, V, p.temperature, p.top_p, has_pen, r, gl, lcap, &tok, &status);
         }
+        if (!done) {
+            __syncthreads();
+            const size_t off = (size_t)b * a.scratch_stride;
+            tok = full_row(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, a.scratch + off,
+                           a.scratch + off + V, a.scratch + off + 2 * (size_t)V,
+                           a.scratch + off + 3 * (size_t)V, &status, nullptr);
+        }
+    } else {
+        bool done = false;
+        if (sm.flag_nan) { status = GS_ERR_NAN; done = true; }
         if (!done) {
             const size_t off = (size_t)b * a.scratch_stride;
             tok = full_row(sm, row, V, keep, p.temperature, p.top_p, has_pen, r, a.scratch + off,
@@ -1991,24 +1997,20 @@ hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st)
     const bool full = a.params || is_full_path(a.uparams, a.V);
     const bool small = a.params || !full;
     if (small) hipLaunchKernelGGL(sample_rows_kernel<kModeSmall>, dim3(B), dim3(kThreads), 0, st, a);
-    if (full) {
-        hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
-        hipLaunchKernelGGL(sample_rows_kernel<kModeSort>, dim3(B), dim3(kThreads), 0, st, a);
-    }
+    if (full) hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 hipError_t launch_sample_rows_forked(const RowArgs &a, int B, hipStream_t st, hipStream_t side, hipEvent_t fork,
                                     hipEvent_t join)
 {
     // the full-vocabulary rows on st; the small-path rows on `side` at the
-    // same time (the CUs the full rows leave idle); the sort path after both
+    // same time (the CUs the full rows leave idle); st waits for both
     if (hipEventRecord(fork, st) != hipSuccess || hipStreamWaitEvent(side, fork, 0) != hipSuccess)
         return hipGetLastError();
     hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
     hipLaunchKernelGGL(sample_rows_kernel<kModeSmall>, dim3(B), dim3(kThreads), 0, side, a);
     if (hipEventRecord(join, side) != hipSuccess || hipStreamWaitEvent(st, join, 0) != hipSuccess)
         return hipGetLastError();
-    hipLaunchKernelGGL(sample_rows_kernel<kModeSort>, dim3(B), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 hipError_t launch_detail_rows(const RowArgs &a, int B, hipStream_t st)
@@ -2065,10 +2067,7 @@ hipError_t launch_chunked(RowArgs a, int B, float *vrow, uint32_t *vidx, uint32_
         a.chunked = kChunkedSelf;
         a.csync = csync;
         hipLaunchKernelGGL(chunk_rows_kernel, dim3(nch, B), dim3(kThreads), 0, st, a);
-        if (a.params) {
-            hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
-            hipLaunchKernelGGL(sample_rows_kernel<kModeSort>, dim3(B), dim3(kThreads), 0, st, a);
-        }
+        if (a.params) hipLaunchKernelGGL(sample_rows_kernel<kModeBins>, dim3(B), dim3(kThreads), 0, st, a);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(chunk_topk_kernel, dim3(nch, B), dim3(kThreads), 0, st, a, nch, vrow, vidx, vld);
