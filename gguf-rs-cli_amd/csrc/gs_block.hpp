@@ -90,6 +90,42 @@ __device__ __forceinline__ uint32_t dpp_mov(uint32_t v)
 {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
+// Wave64 inclusive sums with DPP moves (no LDS round trips): row_shr 1, 2,
+// 4, 8 inside each 16-lane row (lanes without a source read 0), then
+// row_bcast:15 and row_bcast:31 across rows.
+__device__ __forceinline__ uint32_t wave_incl_u32(uint32_t v)
+{
+    const int lane = lane_id();
+    v += dpp_mov<0x111>(v);
+    v += dpp_mov<0x112>(v);
+    v += dpp_mov<0x114>(v);
+    v += dpp_mov<0x118>(v);
+    uint32_t o = dpp_mov<0x142>(v);
+    if ((lane & 31) >= 16) v += o;
+    o = dpp_mov<0x143>(v);
+    if (lane >= 32) v += o;
+    return v;
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_f64(double v)
+{
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = dpp_mov<CTRL>((uint32_t)u), hi = dpp_mov<CTRL>((uint32_t)(u >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_incl_f64(double v)
+{
+    const int lane = lane_id();
+    v += dpp_mov_f64<0x111>(v);      // (a lane without a source reads +0.0)
+    v += dpp_mov_f64<0x112>(v);
+    v += dpp_mov_f64<0x114>(v);
+    v += dpp_mov_f64<0x118>(v);
+    double o = dpp_mov_f64<0x142>(v);
+    if ((lane & 31) >= 16) v += o;
+    o = dpp_mov_f64<0x143>(v);
+    if (lane >= 32) v += o;
+    return v;
+}
 template <int CTRL>
 __device__ __forceinline__ void dpp_step(ParFn &v, bool take)
 {

@@ -374,11 +374,7 @@ __device__ __forceinline__ void f_list_for_each(const uint64_t *gl, uint32_t lo,
 __device__ double f_block_excl_f64_buf(double v, double *tot, double *buf)
 {
     const int lane = lane_id(), w = wave_id();
-    double incl = v;
-    for (int d = 1; d < 64; d <<= 1) {
-        const double o = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += o;
-    }
+    const double incl = wave_incl_f64(v);
     if (lane == 63) buf[w] = incl;
     __syncthreads();
     double pre = 0.0, all = 0.0;
@@ -389,11 +385,7 @@ __device__ double f_block_excl_f64_buf(double v, double *tot, double *buf)
 __device__ double f_block_excl_f64(double v, double *tot, RowSmem &sm)
 {
     const int lane = lane_id(), w = wave_id();
-    double incl = v;
-    for (int d = 1; d < 64; d <<= 1) {
-        const double o = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += o;
-    }
+    const double incl = wave_incl_f64(v);
     if (lane == 63) sm.red_f64[w] = incl;
     __syncthreads();
     double pre = 0.0, all = 0.0;

@@ -46,6 +46,13 @@ __device__ int g_v3dump[64 * 256];
 #define F3_DUMP(k, v) do { } while (0)
 #define F3_TS(k) do { } while (0)
 #endif
+#ifdef GS_TIMING
+#define F3_CLK(v) const uint64_t v = clock64()
+#define F3_CSTAT(k, v) F3_STAT(k, v)
+#else
+#define F3_CLK(v) do { } while (0)
+#define F3_CSTAT(k, v) do { } while (0)
+#endif
 #define F3_FAIL() do { F3_STAT(0, __LINE__); return false; } while (0)
 
 constexpr uint32_t kF3Listed = 0x80000000u;   // role word: a listed bin; bits 0-23: its list cursor
@@ -398,6 +405,18 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
             *cum_out = cum;
             if (pred(cum)) return -1;
         }
+#ifdef GS_TIMING
+        {
+            // the predicted sums' relative error at region ends (2^-30 units)
+            const uint32_t b1 = g + 1 < nreg ? f.reg[g + 1].b0 : (uint32_t)kFBins;
+            const double pr = roff == 0u ? (double)f.pre[b1] : (double)f.pre[b1] / (double)f.pre[kFBins];
+            const double er = fabs((double)cum / pr - 1.0) * 1073741824.0;
+            if (threadIdx.x == 0 && blockIdx.x < 1024 && pr > 0.0) {
+                int &slot = g_v3diag[blockIdx.x * 32 + (roff == 0u ? 28 : 29)];
+                slot = max(slot, (int)fmin(er, 2e9));
+            }
+        }
+#endif
     }
     return 0;
 }
@@ -431,8 +450,16 @@ __device__ __forceinline__ void f3_range(float cb, int b, float *ylo, float *yhi
 // (a segment that the pass did not fill as planned fails the row instead).
 template <class CE>
 __device__ void f3_sort_list(Full3Smem &f, const uint64_t *lst, uint32_t n, uint32_t nover,
-                             const uint32_t *segst, CE cend, uint64_t *se, float *sa)
+                             const uint32_t *segst, CE cend, uint64_t *se, float *sa, uint32_t *stage, uint32_t scap)
 {
+    // the entries' high words (the value keys) staged in LDS when they fit:
+    // a rank counts the higher keys there, and only an element whose key
+    // another entry of its segment shares compares the full entries
+    const bool staged = n <= scap;
+    if (staged) {
+        for (uint32_t j = threadIdx.x; j < n; j += kThreads) stage[j] = (uint32_t)(ldg(lst + j) >> 32);
+        __syncthreads();
+    }
     for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
         const uint64_t en = ldg(lst + j);
         const float y = f_entry_y(en);
@@ -446,14 +473,39 @@ __device__ void f3_sort_list(Full3Smem &f, const uint64_t *lst, uint32_t n, uint
         if (!(st <= j && j < end && end <= n)) { f.fail = 1; continue; }
         uint32_t rank = 0;
         uint32_t q = st;
-        for (; q + 8 <= end; q += 8) {
+        bool full = !staged;
+        if (staged) {
+            const uint32_t hi = (uint32_t)(en >> 32);
+            uint32_t eq = 0;
+            for (; q + 8 <= end; q += 8) {
+                uint32_t k8[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) k8[u] = stage[q + u];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    rank += k8[u] > hi ? 1u : 0u;
+                    eq += k8[u] == hi ? 1u : 0u;
+                }
+            }
+            for (; q < end; q++) {
+                const uint32_t k = stage[q];
+                rank += k > hi ? 1u : 0u;
+                eq += k == hi ? 1u : 0u;
+            }
+            if (eq > 1u) {
+                full = true;
+                rank = 0;
+                q = st;
+            }
+        }
+        for (; full && q + 8 <= end; q += 8) {
             uint64_t e8[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) e8[u] = ldg(lst + q + u);
 #pragma unroll
             for (int u = 0; u < 8; u++) rank += e8[u] > en ? 1u : 0u;
         }
-        for (; q < end; q++) rank += ldg(lst + q) > en ? 1u : 0u;
+        for (; full && q < end; q++) rank += ldg(lst + q) > en ? 1u : 0u;
         if (st + rank >= end) { f.fail = 1; continue; }
         stg(se + st + rank, en);
         stg(sa + st + rank, f3_live(en) ? glibc_expf_tab(y - f.m, f.exptab) : 0.0f);
@@ -498,15 +550,13 @@ __device__ bool f3_plan_runs(RowSmem &sm, Full3Smem &f, int s, int bH, const uin
 {
     constexpr int kPer = kFBins / kThreads;
     const int t = threadIdx.x;
-    uint32_t prev = __shfl_up(key[kPer - 1], 1, 64);
-    uint32_t nxt = __shfl_down(key[0], 1, 64);
-    if (lane_id() == 63) f.wlast[wave_id()] = key[kPer - 1];
+    // the neighbouring threads' edge keys (through the free top of lvl)
+    uint32_t *kx = f.lvl + 2 * kFBins;
+    kx[kPer * t] = key[0];
+    kx[kPer * t + kPer - 1] = key[kPer - 1];
     __syncthreads();
-    if (lane_id() == 0) prev = wave_id() ? f.wlast[wave_id() - 1] : kF3KeyNone;
-    __syncthreads();
-    if (lane_id() == 0) f.wlast[wave_id()] = key[0];
-    __syncthreads();
-    if (lane_id() == 63) nxt = wave_id() + 1 < kWaves ? f.wlast[wave_id() + 1] : kF3KeyNone;
+    const uint32_t prev = t ? kx[kPer * t - 1] : kF3KeyNone;
+    const uint32_t nxt = t + 1 < kThreads ? kx[kPer * t + kPer] : kF3KeyNone;
     uint32_t st[kPer], n = 0;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -623,7 +673,7 @@ __device__ __forceinline__ F3K23 f3_k23(uint2 w, float y, float m, float cS, flo
 // time 64 have gathered every lane of the wave processes one (work).  An
 // element of a bin without work costs its bin lookup only.  The 0-3 elements
 // before the 16-byte boundary and the ragged end go to work directly.
-template <int QN, class YF, class WORD, class ACT, class WORK>
+template <int QN, bool NT, class YF, class WORD, class ACT, class WORK>
 __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD word, ACT act, WORK work, uint2 *q)
 {
     static_assert(QN >= 128 && (QN & (QN - 1)) == 0, "ring");
@@ -633,10 +683,26 @@ __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD wo
     const int n4 = (V - h0) >> 2;
     constexpr int kE = 4 * kUnroll;
     uint32_t qh = 0, qt = 0;
+#ifdef GS_TIMING
+    uint64_t c_work = 0, n_fl = 0;
+    const uint64_t c_beg = clock64();
+#endif
+    // software-pipelined: the next round's loads are in flight while this
+    // round's words are looked up and its active elements processed
+    float4 nv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) nv[u] = NT ? ldg_nt(r4 + min(u * kThreads + t, n4 - 1)) : ldg(r4 + min(u * kThreads + t, n4 - 1));
     for (int base = 0; base < n4; base += kThreads * kUnroll) {
         float4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) v[u] = ldg_nt(r4 + min(base + u * kThreads + t, n4 - 1));
+        for (int u = 0; u < kUnroll; u++) v[u] = nv[u];
+        if (base + kThreads * kUnroll < n4) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                const float4 *pa = r4 + min(base + kThreads * kUnroll + u * kThreads + t, n4 - 1);
+                nv[u] = NT ? ldg_nt(pa) : ldg(pa);
+            }
+        }
         float y[kE];
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
@@ -664,7 +730,14 @@ __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD wo
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                     __builtin_amdgcn_wave_barrier();
                     const uint2 it = q[(qh + (uint32_t)lane) & (QN - 1)];
+#ifdef GS_TIMING
+                    const uint64_t c0 = clock64();
+#endif
                     work((int)it.y, __uint_as_float(it.x));
+#ifdef GS_TIMING
+                    c_work += clock64() - c0;
+                    n_fl++;
+#endif
                     qh += 64u;
                     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                     __builtin_amdgcn_wave_barrier();
@@ -680,6 +753,12 @@ __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD wo
     }
     if (t < h0) work(t, yf(ldg(row + t)));
     for (int i = h0 + (n4 << 2) + t; i < V; i += kThreads) work(i, yf(ldg(row + i)));
+#ifdef GS_TIMING
+    const int sb = QN == 256 ? 20 : 23;
+    F3_STAT(sb, (clock64() - c_beg) / 100);
+    F3_STAT(sb + 1, c_work / 100);
+    F3_STAT(sb + 2, n_fl);
+#endif
 }
 
 // The exact full-vocabulary path, increment-histogram form.  Returns true
@@ -744,10 +823,20 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
     };
     auto pass1 = [&](auto yf) -> bool {
+#ifdef GS_TIMING
+        const uint64_t c_beg = clock64();
+#endif
+        float4 nv[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) nv[u] = ldg(r4 + min(u * kThreads + t, n4 - 1));
         for (int base = 0; base < n4; base += kThreads * kUnroll) {
             float4 v[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; u++) v[u] = ldg(r4 + min(base + u * kThreads + t, n4 - 1));
+            for (int u = 0; u < kUnroll; u++) v[u] = nv[u];
+            if (base + kThreads * kUnroll < n4) {
+#pragma unroll
+                for (int u = 0; u < kUnroll; u++) nv[u] = ldg(r4 + min(base + kThreads * kUnroll + u * kThreads + t, n4 - 1));
+            }
             if (base == 0) {
                 float lm = -INFINITY;
 #pragma unroll
@@ -756,6 +845,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 m0 = ydiv(f_block_max(lm, sm));
                 if (!isfinite(m0)) return false;
                 cb = (float)(((double)m0 + (double)kFDUp) * (double)kFInvW);
+#ifdef GS_TIMING
+                F3_STAT(26, (clock64() - c_beg) / 100);
+#endif
             }
 #pragma unroll
             for (int u = 0; u < kUnroll; u++) {
@@ -768,6 +860,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 }
             }
         }
+#ifdef GS_TIMING
+        F3_STAT(27, (clock64() - c_beg) / 100);
+#endif
         return true;
     };
     if (!(t_one ? pass1([](float x) { return x; }) : pass1([&](float x) { return x / T; }))) F3_FAIL();
@@ -864,8 +959,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 const int b = kPer * t + q;
                 ct[q] = mb[q];
                 if (b >= kFMassBins && cn[q] && lo > 0.0) {
-                    const double g = ldexp(1.0, f_dexp(lo) - 23);
-                    ct[q] = (double)cn[q] * rint(ctr[q] / g) * g;
+                    const int ge = f_dexp(lo) - 23;      // the grid 2^ge
+                    ct[q] = (double)cn[q] * ldexp(rint(ldexp(ctr[q], -ge)), ge);
                 }
                 lo += ct[q];
                 loc += ct[q];
@@ -1047,8 +1142,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         };
         auto act = [](uint32_t w) { return w != 0u; };
         uint2 *ring = reinterpret_cast<uint2 *>(f.u.w23) + 256 * wave_id();
-        if (t_one) f3_qpass<256>(row, V, [](float x) { return x; }, word, act, one, ring);
-        else f3_qpass<256>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
+        if (t_one) f3_qpass<256, false>(row, V, [](float x) { return x; }, word, act, one, ring);
+        else f3_qpass<256, false>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
         __syncthreads();
         if (has_pen) {
             // the raw values of penalized ids leave (listed and ambiguous
@@ -1102,7 +1197,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     }
     __threadfence_block();
     __syncthreads();
-    f3_sort_list(f, lst, f.list_end, (uint32_t)nover, segst, [&](int b) { return f.w[1 + b] & kF3Cur; }, se1, sa1);
+    f3_sort_list(f, lst, f.list_end, (uint32_t)nover, segst, [&](int b) { return f.w[1 + b] & kF3Cur; }, se1, sa1,
+                 reinterpret_cast<uint32_t *>(f.u.w23), 2u * kF3Tab);
     __threadfence_block();
     __syncthreads();
     if (f.fail || f.ntie[0] > kF3Ties) F3_FAIL();
@@ -1168,6 +1264,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         cS3lo = __double2float_rd(iS / s2hi);
         band3 = (float)((double)kF3Band23 * 2.0 + (s2hi / s2lo - 1.0));
         __syncthreads();
+        const double is2hi = 1.0 / s2hi, is2lo = 1.0 / s2lo;
         uint32_t key2[kPer], key3[kPer], klo2[kPer], khi2[kPer], klo3[kPer], khi3[kPer], rl[kPer], ku2[kPer],
             ku3[kPer];
 #pragma unroll
@@ -1201,7 +1298,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                     ku2[q] = f3_uniform(pl * sc, ph * sc);
                 }
             }
-            const double c3lo = lo2 / s2hi, c3hi = hi2 / s2lo;
+            // (reciprocals: the bounds below hold margins far above an ulp)
+            const double c3lo = lo2 * is2hi, c3hi = hi2 * is2lo;
             if (c3lo * dl > rd) continue;
             if (cw || !(c3lo > 0.0) || c3hi * dh > rd || f_dexp(c3lo * dl) != f_dexp(c3hi * dh)) {
                 key3[q] = kF3KeyListed;
@@ -1210,9 +1308,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 const int e3 = f_dexp(c3lo);
                 key3[q] = (uint32_t)(e3 + 256);
                 const double sc = ldexp(1.0, 23 - e3);
-                klo3[q] = (uint32_t)fmin(floor(plo / s2hi * sc), 1073741824.0);
-                khi3[q] = (uint32_t)fmin(floor(phi / s2lo * sc + 0.5), 1073741824.0);
-                ku3[q] = f3_uniform(pl / s2hi * sc, ph / s2lo * sc);
+                klo3[q] = (uint32_t)fmin(floor(plo * is2hi * sc), 1073741824.0);
+                khi3[q] = (uint32_t)fmin(floor(phi * is2lo * sc + 0.5), 1073741824.0);
+                ku3[q] = f3_uniform(pl * is2hi * sc, ph * is2lo * sc);
             }
         }
         F3_TS(31);
@@ -1351,8 +1449,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         };
         auto act = [](uint2 w) { return (w.x | w.y) != 0u; };
         uint2 *ring = reinterpret_cast<uint2 *>(f.pre) + 128 * wave_id();
-        if (t_one) f3_qpass<128>(row, V, [](float x) { return x; }, word, act, one, ring);
-        else f3_qpass<128>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
+        if (t_one) f3_qpass<128, true>(row, V, [](float x) { return x; }, word, act, one, ring);
+        else f3_qpass<128, true>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
         __syncthreads();
         F3_TS(10);
         if (has_pen) {
@@ -1405,7 +1503,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         F3_STAT(12, f.ltot[0]);
         F3_STAT(13, f.ltot[1]);
         if (f.fail || (uint32_t)f.namb > kF3AmbCap || (uint32_t)f.ndef > kF3DefCap) F3_FAIL();
-        f3_sort_list(f, lst, f.list_end, 0u, segst, [&](int b) { return f.u.w23[1 + b].x & kF3Cur; }, se3, sa3);
+        f3_sort_list(f, lst, f.list_end, 0u, segst, [&](int b) { return f.u.w23[1 + b].x & kF3Cur; }, se3, sa3,
+                     reinterpret_cast<uint32_t *>(f.pre), (uint32_t)kFBins + 1u);
         F3_TS(11);
         // seq 2: exact increments of the ambiguous elements and of the listed
         // elements of bins listed for seq 3 only

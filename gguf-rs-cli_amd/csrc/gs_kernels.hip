@@ -472,11 +472,7 @@ __device__ __forceinline__ uint64_t cand_of(uint32_t key, uint32_t idx)
 __device__ uint32_t block_excl_u32(uint32_t v, uint32_t *tot, RowSmem &sm)
 {
     const int lane = lane_id(), w = wave_id();
-    uint32_t incl = v;
-    for (int d = 1; d < 64; d <<= 1) {
-        uint32_t o = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += o;
-    }
+    const uint32_t incl = wave_incl_u32(v);
     if (lane == 63) sm.red_u32[w] = incl;
     __syncthreads();
     uint32_t pre = 0, all = 0;
