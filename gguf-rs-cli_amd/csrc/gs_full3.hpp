@@ -1127,11 +1127,17 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             nok += k.ok ? 1u : 0u;
             return k.rare;
         };
+        // the raw values of penalized ids are not set aside (their penalized
+        // values are visited after the pass); listed ones take their slot,
+        // marked dead
+        bool pen_raw = has_pen;
         auto rare = [&](int i, float y, uint32_t w) {
             if (w & kF3Listed) {
                 const uint32_t slot = atomicAdd(&f.w[f3_tidx(y, cb)], 1u) & kF3Cur;
-                stg(lst + slot, f_entry(y, (uint32_t)i));
+                const uint64_t en = f_entry(y, (uint32_t)i);
+                stg(lst + slot, pen_raw && hash_find(sm, (uint32_t)i) >= 0 ? f3_dead(en) : en);
             } else {
+                if (pen_raw && hash_find(sm, (uint32_t)i) >= 0) return;
                 const uint32_t s = atomicAdd((uint32_t *)&f.namb, 1u);
                 if (s < kF3AmbCap) stg(amb + s, f_entry(y, (uint32_t)i));
             }
@@ -1146,34 +1152,25 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         else f3_qpass<256, false>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
         __syncthreads();
         if (has_pen) {
-            // the raw values of penalized ids leave (listed and ambiguous
-            // entries are marked, levels uncounted), then the penalized values
-            // are visited
+            // the raw values of penalized ids leave (the pass marked their
+            // listed entries and set none aside; their levels are uncounted
+            // here), then the penalized values are visited
             for (int s = t; s < kHashSlots; s += kThreads) {
                 const uint32_t id = sm.hkey[s];
                 if (id == kEmpty) continue;
                 const float y = ydiv(ldg(row + id));
                 const int ix = f3_tidx(y, cb);
                 const uint32_t w = f.w[ix];
-                const uint64_t en = f_entry(y, id);
-                if (w & kF3Listed) {
-                    for (uint32_t p = ldg(segst + ix - 1); p < (w & kF3Cur); p++)
-                        if (ldg(lst + p) == en) stg(lst + p, f3_dead(en));
-                    continue;
-                }
+                if (w & kF3Listed) continue;
                 const F3K k = f3_k1(w, y, m);
                 if (k.ok) {
                     f3_lvl_add(f, k.slot, 0xffffffffu);
                     nok--;
                 }
-                else if (k.rare) {
-                    const uint32_t na = min((uint32_t)f.namb, (uint32_t)kF3AmbCap);
-                    for (uint32_t p = 0; p < na; p++)
-                        if (ldg(amb + p) == en) stg(amb + p, f3_dead(en));
-                }
             }
             __threadfence_block();
             __syncthreads();
+            pen_raw = false;
             for (int s = t; s < kHashSlots; s += kThreads)
                 if (sm.hkey[s] != kEmpty) one((int)sm.hkey[s], pen_y(s));
             __threadfence_block();
@@ -1426,13 +1423,16 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             nok3 += k.ok3 ? 1u : 0u;
             return k.rare;
         };
+        bool pen_raw = has_pen;      // (as in pass 2)
         auto rare = [&](int i, float y, uint2 w) {
             const uint64_t en = f_entry(y, (uint32_t)i);
+            const bool raw = pen_raw && hash_find(sm, (uint32_t)i) >= 0;
             if (w.x & kF3Listed) {
                 const uint32_t slot = atomicAdd(&f.u.w23[f3_tidx(y, cb)].x, 1u) & kF3Cur;
-                stg(lst + slot, en);
+                stg(lst + slot, raw ? f3_dead(en) : en);
                 return;
             }
+            if (raw) return;
             const F3K23 k = f3_k23(w, y, m, cS, cS3lo, band3);
             if ((w.x & kF3In2) && !k.ok2) {
                 const uint32_t s = atomicAdd((uint32_t *)&f.namb, 1u);
@@ -1460,34 +1460,20 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 const float y = ydiv(ldg(row + id));
                 const int ix = f3_tidx(y, cb);
                 const uint2 w = f.u.w23[ix];
-                const uint64_t en = f_entry(y, id);
-                if (w.x & kF3Listed) {
-                    for (uint32_t p = ldg(segst + ix - 1); p < (w.x & kF3Cur); p++)
-                        if (ldg(lst + p) == en) stg(lst + p, f3_dead(en));
-                    continue;
-                }
+                if (w.x & kF3Listed) continue;
                 const F3K23 k = f3_k23(w, y, m, cS, cS3lo, band3);
                 if (k.ok2) {
                     f3_lvl_add(f, k.slot2, 0xffffffffu);
                     nok2--;
                 }
-                else if (w.x & kF3In2) {
-                    const uint32_t na = min((uint32_t)f.namb, (uint32_t)kF3AmbCap);
-                    for (uint32_t p = 0; p < na; p++)
-                        if (ldg(amb + p) == en) stg(amb + p, f3_dead(en));
-                }
                 if (k.ok3) {
                     f3_lvl_add(f, k.slot3, 0xffffffffu);
                     nok3--;
                 }
-                else if (w.y & kF3W3) {
-                    const uint32_t nd = min((uint32_t)f.ndef, (uint32_t)kF3DefCap);
-                    for (uint32_t p = 0; p < nd; p++)
-                        if (ldg(def + p) == en) stg(def + p, f3_dead(en));
-                }
             }
             __threadfence_block();
             __syncthreads();
+            pen_raw = false;
             for (int s = t; s < kHashSlots; s += kThreads)
                 if (sm.hkey[s] != kEmpty) one((int)sm.hkey[s], pen_y(s));
             __threadfence_block();
