@@ -269,10 +269,11 @@ def bench_gemv(gs, torch, steps=50, warmup=5, cpu=True):
                                "sample": "oracle matvec (src/tensor/dequant.rs:277-318 restated) on %d "
                                          "random rows of the %d, %d threads" % (len(sample), rows, nthr)}
     m.close()
-    # the other K-quant output types at the same shape (timing only; parity
+    # the other output block types at the same shape (timing only; parity
     # is tests/test_gemv.py's)
     out["other_qtypes"] = {}
-    for name, qk in (("Q4_K", workloads.Q4_K), ("Q5_K", workloads.Q5_K)):
+    for name, qk in (("Q4_K", workloads.Q4_K), ("Q5_K", workloads.Q5_K), ("Q8_0", workloads.Q8_0),
+                     ("Q4_0", workloads.Q4_0), ("Q4_1", workloads.Q4_1), ("Q3_K", workloads.Q3_K)):
         bk = workloads.synth_qblocks(qk, rows, cols, seed=13)
         mk = gs.QMatrix(qk, bk, rows, cols)
         del bk
@@ -659,6 +660,9 @@ def main():
     if args.gemv_only:
         g = bench_gemv(gs, torch, steps=args.steps, warmup=args.warmup, cpu=False)
         log("gemv: %.1f us, %.0f GB/s" % (g["us"], g["roofline"]["achieved"]))
+        for name, r in g["other_qtypes"].items():
+            log("gemv %s: %.1f us, %.0f GB/s (%.0f%% of peak)" % (name, r["us"], r["GB_per_s"],
+                                                                  100 * r["frac_of_hbm_peak"]))
         return
     if args.configs_only:
         for name, r in bench_configs(gs, torch).items():

@@ -1,7 +1,7 @@
 // gs_gemv.hip -- gfx950 quantized matrix-vector product that produces the
 // logits (the reference's output projection, src/model/llama.rs:333-334 on
-// the GPU path, :405-407 on the CPU path), for Q8_0, Q4_K, Q5_K and Q6_K
-// weights.
+// the GPU path, :405-407 on the CPU path), for Q4_0, Q4_1, Q8_0, Q3_K, Q4_K,
+// Q5_K and Q6_K weights.
 //
 // HBM-bound: every weight byte is read once per call and nothing else of
 // size moves.  Device layout (rearranged at upload from the GGUF blocks, the
@@ -172,18 +172,28 @@ __device__ __forceinline__ void q6_xslice(const float *x, int j, int h, int l0, 
     }
 }
 
+// A block format whose lanes take quarters: 64 weights of block j at
+// 256 j + 128 h + 32 g + l0 + (0..15), g = 0..3 (Q6_K, Q3_K).
+struct Q6Fmt {
+    typedef Q6Planes Planes;
+    typedef Q6Quarter Unit;
+    static __device__ __forceinline__ Unit load(const Planes &P, uint32_t e) { return q6_load(P, e); }
+    static __device__ __forceinline__ float dot(const Unit &u, const float (&xg)[4][16], const float (&sx)[4])
+    {
+        return q6_dot(u, xg, sx);
+    }
+};
+
 // Rows of up to 16 blocks (cols <= 4096): one quarter per lane, x in
 // registers.  One NT-thread workgroup per CU stages x in LDS once; each wave
 // then takes a contiguous run of rows and keeps the loads of the next PF rows
 // in flight while it computes one (PF divides kRB, so the ring of row
 // buffers is indexed statically).
-template <int kRB, int PF, int NT>
-__global__ void __launch_bounds__(NT)
-q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
+template <class F, int kRB, int PF, int NT>
+__device__ __forceinline__ void quarter_rows_xreg(const typename F::Planes &P, const float *x, float *out, int rows,
+                                                  int nb, float *xs, float (*tiles)[kRB * 64])
 {
     static_assert(kRB % PF == 0, "ring of PF row buffers, kRB rows per batch");
-    __shared__ float xs[4096];
-    __shared__ float tiles[NT / 64][kRB * 64];
     const int cols = 256 * nb;
     for (int i = threadIdx.x; i < cols; i += NT) xs[i] = x[i];
     __syncthreads();
@@ -202,16 +212,16 @@ q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
     float *tile = tiles[threadIdx.x >> 6];
     const uint32_t e1 = (uint32_t)(r1 - 1) * NQ + qi;
     auto row_e = [&](int r) { return min((uint32_t)r * NQ + qi, e1); };   // past the run: its last row
-    Q6Quarter buf[PF];
+    typename F::Unit buf[PF];
 #pragma unroll
-    for (int i = 0; i < PF; i++) buf[i] = q6_load(P, row_e(r0 + i));
+    for (int i = 0; i < PF; i++) buf[i] = F::load(P, row_e(r0 + i));
     int rb = r0;
     for (; rb + kRB <= r1; rb += kRB) {        // full batches
         float part[kRB];
 #pragma unroll
         for (int k = 0; k < kRB; k++) {
-            const Q6Quarter nxt = q6_load(P, row_e(rb + k + PF));
-            part[k] = act ? q6_dot(buf[k % PF], xg, sx) : 0.0f;
+            const typename F::Unit nxt = F::load(P, row_e(rb + k + PF));
+            part[k] = act ? F::dot(buf[k % PF], xg, sx) : 0.0f;
             buf[k % PF] = nxt;
         }
         const float v = rows_sum<kRB>(part, tile);
@@ -222,22 +232,30 @@ q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
 #pragma unroll
         for (int k = 0; k < kRB; k++) {
             part[k] = 0.0f;
-            if (rb + k < r1 && act) part[k] = q6_dot(buf[k % PF], xg, sx);   // rows rb .. r1-1 are in the ring
+            if (rb + k < r1 && act) part[k] = F::dot(buf[k % PF], xg, sx);   // rows rb .. r1-1 are in the ring
             if (k + 1 < kRB && (k + 1) % PF == 0 && rb + k + 1 < r1) {
 #pragma unroll
-                for (int i = 0; i < PF; i++) buf[i] = q6_load(P, row_e(rb + k + 1 + i));
+                for (int i = 0; i < PF; i++) buf[i] = F::load(P, row_e(rb + k + 1 + i));
             }
         }
         const float v = rows_sum<kRB>(part, tile);
         if (lane < kRB && rb + lane < r1) out[rb + lane] = v;
     }
 }
+template <int kRB, int PF, int NT>
+__global__ void __launch_bounds__(NT)
+q6k_gemv_xreg(Q6Planes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[4096];
+    __shared__ float tiles[NT / 64][kRB * 64];
+    quarter_rows_xreg<Q6Fmt, kRB, PF, NT>(P, x, out, rows, nb, xs, tiles);
+}
 
 // Any row length up to kMaxCols: x staged in LDS, lanes loop over quarters.
-__global__ void __launch_bounds__(kGemvThreads)
-q6k_gemv_lds(Q6Planes P, const float *x, float *out, int rows, int nb)
+template <class F>
+__device__ __forceinline__ void quarter_rows_lds(const typename F::Planes &P, const float *x, float *out, int rows,
+                                                 int nb, float *xs)
 {
-    __shared__ float xs[kMaxCols];
     const int cols = 256 * nb;
     for (int i = threadIdx.x; i < cols; i += kGemvThreads) xs[i] = x[i];
     __syncthreads();
@@ -251,11 +269,92 @@ q6k_gemv_lds(Q6Planes P, const float *x, float *out, int rows, int nb)
             const int j = qi >> 2, h = (qi >> 1) & 1, l0 = (qi & 1) * 16;
             float xg[4][16], sx[4];
             q6_xslice(xs, j, h, l0, xg, sx);
-            v += q6_dot(q6_load(P, (uint32_t)r * NQ + qi), xg, sx);
+            v += F::dot(F::load(P, (uint32_t)r * NQ + qi), xg, sx);
         }
         v = wave_sum(v);
         if (lane == 0) out[r] = v;
     }
+}
+__global__ void __launch_bounds__(kGemvThreads)
+q6k_gemv_lds(Q6Planes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[kMaxCols];
+    quarter_rows_lds<Q6Fmt>(P, x, out, rows, nb, xs);
+}
+
+// ---------------------------------------------------------------- Q3_K -----
+// The GGUF layout (110 bytes: hmask[32], qs[64], scales[12], f16 d): weight
+// 128 n + 32 j + l has low bits (qs[32 n + l] >> 2 j) & 3, third bit
+// (hmask[l] >> (4 n + j)) & 1, value q = bits - 4, and scale (16 sub-blocks
+// of 16, 6 bits each, minus 32).  A quarter (n, l0) is the Q6_K quarter
+// (h = n, g = j).  Planes, element e = 4 block + 2 n + l0 / 16:
+//   q: 16 bytes per quarter, qs[32 n + l0 ..]; h: two words per quarter,
+//   bits 16 (j & 1) + k of word j >> 1 = the third bit of weight l0 + k of
+//   group j; s: one word per quarter, byte j = the signed scale of group j;
+//   d: the f16 d per block.
+struct Q3Planes {
+    const uint8_t *q;
+    const uint2 *h;
+    const uint32_t *s;
+    const uint16_t *d;
+};
+struct Q3Quarter {
+    uint4 q;
+    uint2 h;
+    uint32_t s;
+    uint16_t d;
+};
+struct Q3Fmt {
+    typedef Q3Planes Planes;
+    typedef Q3Quarter Unit;
+    static __device__ __forceinline__ Unit load(const Planes &P, uint32_t e)
+    {
+        Unit u;
+        u.q = ntl4(P.q + e * 16u);
+        u.h = ntl2(P.h + e);
+        u.s = __builtin_nontemporal_load(P.s + e);
+        u.d = __builtin_nontemporal_load(P.d + (e >> 2));
+        return u;
+    }
+    // sum over the groups of (d * scale_j) * (sum u x - 4 sum x), u = q + 4
+    static __device__ __forceinline__ float dot(const Unit &u, const float (&xg)[4][16], const float (&sx)[4])
+    {
+        const uint32_t W[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+        float dt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t hw = j < 2 ? u.h.x : u.h.y;
+                const uint32_t nib = (hw >> (16 * (j & 1) + 4 * w)) & 0xFu;
+                const uint32_t v = ((W[w] >> (2 * j)) & 0x03030303u) | (((nib * 0x00204081u) & 0x01010101u) << 2);
+#pragma unroll
+                for (int t = 0; t < 4; t++) dt[j] = fmaf(ub(v, t), xg[j][4 * w + t], dt[j]);
+            }
+        }
+        const float d = h2f(u.d);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float scl = d * (float)(int8_t)(uint8_t)(u.s >> (8 * j));   // (d * sc), as the reference
+            acc = fmaf(scl, fmaf(-4.0f, sx[j], dt[j]), acc);
+        }
+        return acc;
+    }
+};
+template <int kRB, int PF, int NT>
+__global__ void __launch_bounds__(NT)
+q3k_gemv_xreg(Q3Planes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[4096];
+    __shared__ float tiles[NT / 64][kRB * 64];
+    quarter_rows_xreg<Q3Fmt, kRB, PF, NT>(P, x, out, rows, nb, xs, tiles);
+}
+__global__ void __launch_bounds__(kGemvThreads)
+q3k_gemv_lds(Q3Planes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[kMaxCols];
+    quarter_rows_lds<Q3Fmt>(P, x, out, rows, nb, xs);
 }
 
 // ---------------------------------------------------------------- Q8_0 -----
@@ -390,6 +489,156 @@ q80_gemv_lds(const uint8_t *bits, const uint16_t *dq, const float *x, float *out
             float s = 0.0f;
             for (int i = 0; i < 16; i++) s += xp[i];
             v += q8_dot(q, __builtin_nontemporal_load(dq + blk), xp, s);
+        }
+        v = wave_sum(v);
+        if (lane == 0) out[r] = v;
+    }
+}
+
+// ---------------------------------------------------------- Q4_0 / Q4_1 -----
+// Block j of a row (src/tensor/dequant.rs:26-54): byte l of its 16 bytes of
+// nibbles holds weight 32 j + l (low nibble) and 32 j + 16 + l (high).
+// Q4_0: w = (q - 8) d; Q4_1: w = q d + m.  Planes: qs, 16 bytes per block;
+// Q4_0 the f16 d per block, Q4_1 one word per block, d | m << 16.
+struct Q4Planes {
+    const uint8_t *qs;
+    const uint16_t *d;      // Q4_0
+    const uint32_t *dm;     // Q4_1
+};
+constexpr int kQ4Blocks = 2;            // blocks per lane on the register path (cols <= 4096)
+constexpr int kRB4 = 8, kPF4 = 4, kNT4 = 768;   // rows per batch, rows in flight, threads
+
+template <bool Q41>
+__device__ __forceinline__ uint32_t q4_dm(const Q4Planes &P, uint32_t blk)
+{
+    return Q41 ? __builtin_nontemporal_load(P.dm + blk) : (uint32_t)__builtin_nontemporal_load(P.d + blk);
+}
+// Q4_0: d (sum q x - 8 sum x); Q4_1: d sum q x + m sum x.  xv: the block's
+// 32 values of x, sx their sum.
+template <bool Q41>
+__device__ __forceinline__ float q4_dot(uint4 q, uint32_t dm, const float *xv, float sx)
+{
+    const uint32_t W[4] = {q.x, q.y, q.z, q.w};
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t a = W[w] & 0x0F0F0F0Fu, b = (W[w] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            lo = fmaf(ub(a, t), xv[4 * w + t], lo);
+            hi = fmaf(ub(b, t), xv[16 + 4 * w + t], hi);
+        }
+    }
+    const float d = h2f((uint16_t)(dm & 0xffffu));
+    if (Q41) return fmaf(d, lo + hi, h2f((uint16_t)(dm >> 16)) * sx);
+    return d * fmaf(-8.0f, sx, lo + hi);
+}
+
+// As q80_gemv_xreg: kQ4Blocks blocks per lane, x (64 values) in registers,
+// PF rows in flight.
+template <bool Q41, int kRB, int PF, int NT>
+__global__ void __launch_bounds__(NT)
+q4_gemv_xreg(Q4Planes P, const float *x, float *out, int rows, int nb)
+{
+    static_assert(kRB % PF == 0, "ring of PF row buffers, kRB rows per batch");
+    __shared__ float xs[4096];
+    __shared__ float tiles[NT / 64][kRB * 64];
+    const int cols = 32 * nb;
+    for (int i = threadIdx.x; i < cols; i += NT) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (NT / 64);
+    const int gw = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    float xv[kQ4Blocks][32], sx[kQ4Blocks];
+    bool act[kQ4Blocks];
+    int bk[kQ4Blocks];
+#pragma unroll
+    for (int k = 0; k < kQ4Blocks; k++) {
+        act[k] = lane + 64 * k < nb;
+        bk[k] = act[k] ? lane + 64 * k : 0;
+        const float4 *p = reinterpret_cast<const float4 *>(xs + 32 * bk[k]);
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = p[i];
+            xv[k][4 * i] = v.x; xv[k][4 * i + 1] = v.y; xv[k][4 * i + 2] = v.z; xv[k][4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; i++) s += xv[k][i];
+        sx[k] = s;
+    }
+    const int rpw = (rows + nw - 1) / nw;
+    const int r0 = gw * rpw, r1 = min(rows, r0 + rpw);
+    if (r0 >= r1) return;
+    float *tile = tiles[threadIdx.x >> 6];
+    struct Row { uint4 q[kQ4Blocks]; uint32_t dm[kQ4Blocks]; };
+    auto load = [&](int r) {                   // rows past the run read its last row
+        const uint32_t rr = (uint32_t)min(r, r1 - 1);
+        Row w;
+#pragma unroll
+        for (int k = 0; k < kQ4Blocks; k++) {
+            const uint32_t e = rr * (uint32_t)nb + (uint32_t)bk[k];
+            w.q[k] = ntl4(P.qs + e * 16u);
+            w.dm[k] = q4_dm<Q41>(P, e);
+        }
+        return w;
+    };
+    auto dot = [&](const Row &w) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kQ4Blocks; k++)
+            if (act[k]) v += q4_dot<Q41>(w.q[k], w.dm[k], xv[k], sx[k]);
+        return v;
+    };
+    Row buf[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) buf[i] = load(r0 + i);
+    int rb = r0;
+    for (; rb + kRB <= r1; rb += kRB) {        // full batches
+        float part[kRB];
+#pragma unroll
+        for (int k = 0; k < kRB; k++) {
+            const Row nxt = load(rb + k + PF);
+            part[k] = dot(buf[k % PF]);
+            buf[k % PF] = nxt;
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB) out[rb + lane] = v;
+    }
+    if (rb < r1) {                             // the last, partial batch
+        float part[kRB];
+#pragma unroll
+        for (int k = 0; k < kRB; k++) {
+            part[k] = rb + k < r1 ? dot(buf[k % PF]) : 0.0f;
+            if (k + 1 < kRB && (k + 1) % PF == 0 && rb + k + 1 < r1) {
+#pragma unroll
+                for (int i = 0; i < PF; i++) buf[i] = load(rb + k + 1 + i);
+            }
+        }
+        const float v = rows_sum<kRB>(part, tile);
+        if (lane < kRB && rb + lane < r1) out[rb + lane] = v;
+    }
+}
+
+template <bool Q41>
+__global__ void __launch_bounds__(kGemvThreads)
+q4_gemv_lds(Q4Planes P, const float *x, float *out, int rows, int nb)
+{
+    __shared__ float xs[kMaxCols];
+    const int cols = 32 * nb;
+    for (int i = threadIdx.x; i < cols; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * (kGemvThreads / 64);
+    const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+    for (int r = gw; r < rows; r += nw) {
+        float v = 0.0f;
+        for (int b = lane; b < nb; b += 64) {
+            const uint32_t e = (uint32_t)r * (uint32_t)nb + (uint32_t)b;
+            const float *xp = xs + 32 * b;
+            float s = 0.0f;
+            for (int i = 0; i < 32; i++) s += xp[i];
+            v += q4_dot<Q41>(ntl4(P.qs + e * 16u), q4_dm<Q41>(P, e), xp, s);
         }
         v = wave_sum(v);
         if (lane == 0) out[r] = v;
@@ -565,6 +814,8 @@ struct gs_qmatrix {
     uint8_t *base;             // one device allocation holding the planes
     gs::Q6Planes q6;           // Q6_K
     gs::KPlanes kq;            // Q4_K / Q5_K
+    gs::Q3Planes q3;           // Q3_K
+    gs::Q4Planes q4;           // Q4_0 / Q4_1
     const uint8_t *q8;         // Q8_0: int8 quants
     const uint16_t *d;         // f16 d per block (Q8_0, Q6_K)
 };
@@ -628,6 +879,82 @@ int upload_kquant(bool q5, const uint8_t *src, size_t rows, size_t nb, gs_qmatri
                         (const uint32_t *)(m->base + off_sm), (const uint32_t *)(m->base + off_dd)};
     return GS_OK;
 }
+// Q4_0 (18-byte blocks) / Q4_1 (20) to the Q4 planes (see Q4Planes).
+int upload_q4(bool q41, const uint8_t *src, size_t rows, size_t nb, gs_qmatrix *m)
+{
+    const size_t n = rows * nb;
+    const size_t off_d = (n * 16 + 255) & ~(size_t)255;
+    const size_t total = off_d + n * (q41 ? 4 : 2);
+    uint8_t *h = new (std::nothrow) uint8_t[total];
+    if (!h) return GS_ERR_NOMEM;
+    const size_t bb = q41 ? 20 : 18;
+    for (size_t i = 0; i < n; i++) {
+        const uint8_t *b = src + i * bb;
+        memcpy(h + i * 16, b + (q41 ? 4 : 2), 16);
+        memcpy(h + off_d + i * (q41 ? 4 : 2), b, q41 ? 4 : 2);   // d (, m): f16 each
+    }
+    if (hipMalloc((void **)&m->base, total) != hipSuccess) {
+        (void)hipGetLastError();
+        delete[] h;
+        return GS_ERR_NOMEM;
+    }
+    const hipError_t ce = hipMemcpy(m->base, h, total, hipMemcpyHostToDevice);
+    delete[] h;
+    if (ce != hipSuccess) { (void)hipFree(m->base); m->base = nullptr; return GS_ERR_HIP; }
+    m->q4 = gs::Q4Planes{m->base, q41 ? nullptr : (const uint16_t *)(m->base + off_d),
+                         q41 ? (const uint32_t *)(m->base + off_d) : nullptr};
+    return GS_OK;
+}
+
+// The signed 6-bit scale of sub-block is of a Q3_K block in the GGUF
+// packing: low nibble from byte is % 8 (bits 0-3 for is < 8, 4-7 above),
+// top two bits from bits 2 (is / 4) of byte 8 + is % 4; minus 32.
+int q3k_scale(const uint8_t *sc, int is)
+{
+    const int k = is >> 2, j = is & 3;
+    const uint8_t nb = sc[(k & 1) * 4 + j];
+    const int low = k < 2 ? (nb & 0xF) : (nb >> 4);
+    return (low | (((sc[8 + j] >> (2 * k)) & 3) << 4)) - 32;
+}
+
+// Q3_K (110-byte blocks) to the Q3 planes (see Q3Planes).
+int upload_q3k(const uint8_t *src, size_t rows, size_t nb, gs_qmatrix *m)
+{
+    const size_t n = rows * nb, np = 4 * n;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const size_t off_h = al(np * 16), off_s = off_h + al(np * 8), off_d = off_s + al(np * 4);
+    const size_t total = off_d + n * 2;
+    uint8_t *h = new (std::nothrow) uint8_t[total];
+    if (!h) return GS_ERR_NOMEM;
+    for (size_t i = 0; i < n; i++) {
+        const uint8_t *b = src + i * 110;
+        const uint8_t *hm = b, *qs = b + 32, *sc = b + 96;
+        for (int qq = 0; qq < 4; qq++) {
+            const int nn = qq >> 1, l0 = (qq & 1) * 16;
+            const size_t e = 4 * i + qq;
+            memcpy(h + e * 16, qs + 32 * nn + l0, 16);
+            uint32_t hw[2] = {0u, 0u};
+            for (int j = 0; j < 4; j++)
+                for (int k = 0; k < 16; k++)
+                    hw[j >> 1] |= (uint32_t)((hm[l0 + k] >> (4 * nn + j)) & 1u) << (16 * (j & 1) + k);
+            memcpy(h + off_h + e * 8, hw, 8);
+            for (int j = 0; j < 4; j++)
+                h[off_s + e * 4 + j] = (uint8_t)(int8_t)q3k_scale(sc, 8 * nn + 2 * j + l0 / 16);
+        }
+        memcpy(h + off_d + i * 2, b + 108, 2);
+    }
+    if (hipMalloc((void **)&m->base, total) != hipSuccess) {
+        (void)hipGetLastError();
+        delete[] h;
+        return GS_ERR_NOMEM;
+    }
+    const hipError_t ce = hipMemcpy(m->base, h, total, hipMemcpyHostToDevice);
+    delete[] h;
+    if (ce != hipSuccess) { (void)hipFree(m->base); m->base = nullptr; return GS_ERR_HIP; }
+    m->q3 = gs::Q3Planes{m->base, (const uint2 *)(m->base + off_h), (const uint32_t *)(m->base + off_s),
+                         (const uint16_t *)(m->base + off_d)};
+    return GS_OK;
+}
 } // namespace
 
 extern "C" {
@@ -637,20 +964,27 @@ int gs_qmatrix_upload(uint32_t qtype, const void *blocks, size_t rows, size_t co
     if (!out) return GS_ERR_INVALID;
     *out = nullptr;
     if (!blocks || rows == 0 || cols == 0) return GS_ERR_INVALID;
-    if (qtype != GS_QTYPE_Q8_0 && qtype != GS_QTYPE_Q6_K && qtype != GS_QTYPE_Q4_K && qtype != GS_QTYPE_Q5_K)
+    if (qtype != GS_QTYPE_Q8_0 && qtype != GS_QTYPE_Q6_K && qtype != GS_QTYPE_Q4_K && qtype != GS_QTYPE_Q5_K &&
+        qtype != GS_QTYPE_Q4_0 && qtype != GS_QTYPE_Q4_1 && qtype != GS_QTYPE_Q3_K)
         return GS_ERR_UNSUPPORTED;
-    if (qtype == GS_QTYPE_Q4_K || qtype == GS_QTYPE_Q5_K) {
-        if (cols % 256 != 0 || cols > (size_t)gs::kMaxCols || rows > 0x7fffffffu) return GS_ERR_UNSUPPORTED;
-        if (rows * (cols / 64) >= (1ull << 27)) return GS_ERR_UNSUPPORTED;   // 32-bit byte offsets of the qs plane
+    if (qtype == GS_QTYPE_Q4_K || qtype == GS_QTYPE_Q5_K || qtype == GS_QTYPE_Q4_0 || qtype == GS_QTYPE_Q4_1 ||
+        qtype == GS_QTYPE_Q3_K) {
+        const bool q4 = qtype == GS_QTYPE_Q4_0 || qtype == GS_QTYPE_Q4_1;
+        const size_t bw = q4 ? 32 : 256;
+        if (cols % bw != 0 || cols > (size_t)gs::kMaxCols || rows > 0x7fffffffu) return GS_ERR_UNSUPPORTED;
+        // 32-bit byte offsets of the widest plane
+        if (rows * (cols / 64) >= (q4 ? (1ull << 29) : (1ull << 27))) return GS_ERR_UNSUPPORTED;
         gs_qmatrix *m = new (std::nothrow) gs_qmatrix();
         if (!m) return GS_ERR_NOMEM;
-        m->qtype = qtype; m->rows = rows; m->cols = cols; m->nb = cols / 256;
+        m->qtype = qtype; m->rows = rows; m->cols = cols; m->nb = cols / bw;
         if (hipGetDevice(&m->device) != hipSuccess ||
             hipDeviceGetAttribute(&m->cus, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess) {
             delete m; return GS_ERR_HIP;
         }
         if (m->cus <= 0) m->cus = 256;
-        const int rc = upload_kquant(qtype == GS_QTYPE_Q5_K, (const uint8_t *)blocks, rows, cols / 256, m);
+        const int rc = q4 ? upload_q4(qtype == GS_QTYPE_Q4_1, (const uint8_t *)blocks, rows, cols / 32, m)
+                       : qtype == GS_QTYPE_Q3_K ? upload_q3k((const uint8_t *)blocks, rows, cols / 256, m)
+                       : upload_kquant(qtype == GS_QTYPE_Q5_K, (const uint8_t *)blocks, rows, cols / 256, m);
         if (rc != GS_OK) { delete m; return rc; }
         *out = m;
         return GS_OK;
@@ -750,6 +1084,20 @@ int gs_gemv(const gs_qmatrix *m, const float *d_x, size_t B, float *d_out, void 
                 if (q5) hipLaunchKernelGGL(gs::kq_gemv_lds<true>, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->kq, x, o, rows, nb);
                 else hipLaunchKernelGGL(gs::kq_gemv_lds<false>, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->kq, x, o, rows, nb);
             }
+        } else if (m->qtype == GS_QTYPE_Q4_0 || m->qtype == GS_QTYPE_Q4_1) {
+            const bool q41 = m->qtype == GS_QTYPE_Q4_1;
+            if (nb <= 64 * gs::kQ4Blocks) {
+                if (q41) hipLaunchKernelGGL((gs::q4_gemv_xreg<true, gs::kRB4, gs::kPF4, gs::kNT4>), dim3(m->cus), dim3(gs::kNT4), 0, st, m->q4, x, o, rows, nb);
+                else hipLaunchKernelGGL((gs::q4_gemv_xreg<false, gs::kRB4, gs::kPF4, gs::kNT4>), dim3(m->cus), dim3(gs::kNT4), 0, st, m->q4, x, o, rows, nb);
+            } else {
+                if (q41) hipLaunchKernelGGL(gs::q4_gemv_lds<true>, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q4, x, o, rows, nb);
+                else hipLaunchKernelGGL(gs::q4_gemv_lds<false>, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q4, x, o, rows, nb);
+            }
+        } else if (m->qtype == GS_QTYPE_Q3_K) {
+            if (4 * nb <= 64)
+                hipLaunchKernelGGL((gs::q3k_gemv_xreg<gs::kRB6, gs::kPF6, gs::kNT6>), dim3(m->cus), dim3(gs::kNT6), 0, st, m->q3, x, o, rows, nb);
+            else
+                hipLaunchKernelGGL(gs::q3k_gemv_lds, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q3, x, o, rows, nb);
         } else if (m->qtype == GS_QTYPE_Q6_K) {
             if (4 * nb <= 64)
                 hipLaunchKernelGGL((gs::q6k_gemv_xreg<gs::kRB6, gs::kPF6, gs::kNT6>), dim3(m->cus), dim3(gs::kNT6), 0, st, m->q6, x, o, rows, nb);

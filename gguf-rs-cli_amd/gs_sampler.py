@@ -456,13 +456,18 @@ def sample_mut(logits, temperature, top_k, top_p, rep_penalty, recent):
 
 
 # ---- quantized output projection (include/gs_gemv.h) --------------------------
-QTYPE_Q8_0 = 8     # GgmlType::Q8_0 (src/gguf/types.rs:45)
-QTYPE_Q6_K = 14    # GgmlType::Q6K  (src/gguf/types.rs:47)
+QTYPE_Q4_0 = 2     # GgmlType::Q4_0 (src/gguf/types.rs:42)
+QTYPE_Q4_1 = 3     # GgmlType::Q4_1
+QTYPE_Q8_0 = 8     # GgmlType::Q8_0 (src/gguf/types.rs:43)
+QTYPE_Q3_K = 11    # GgmlType::Q3K  (src/gguf/types.rs:44)
+QTYPE_Q4_K = 12    # GgmlType::Q4K
+QTYPE_Q5_K = 13    # GgmlType::Q5K
+QTYPE_Q6_K = 14    # GgmlType::Q6K
 
 
 class QMatrix:
     """A quantized matrix on the device: Gpu::upload (src/gpu/mod.rs:222-238)
-    of a Q8_0 / Q6_K GGUF tensor.  `blocks` are the tensor's raw bytes (a
+    of a Q4_0 / Q4_1 / Q8_0 / Q3_K / Q4_K / Q5_K / Q6_K GGUF tensor.  `blocks` are the tensor's raw bytes (a
     numpy uint8 array or bytes), rows x cols weights, cols = dims[0].
     gemv(x, out) is Gpu::cmd_gemv (src/gpu/mod.rs:438-443): out = W x for
     device f32 vectors (torch tensors or device addresses), B = len(x) / cols

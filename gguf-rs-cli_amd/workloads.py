@@ -102,8 +102,9 @@ def algorithmic_bytes_per_row(V, W, hetero=False, window_append=False):
 # ---- quantized output matrices (the logits projection) ------------------------
 # GGUF block sizes (src/gguf/types.rs:62-71): Q8_0 34 bytes / 32 weights,
 # Q4_K 144, Q5_K 176 and Q6_K 210 bytes / 256 weights.
-Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
-QBLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+Q4_0, Q4_1, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K = 2, 3, 8, 11, 12, 13, 14
+QBLOCK = {Q4_0: (32, 18), Q4_1: (32, 20), Q8_0: (32, 34), Q3_K: (256, 110), Q4_K: (256, 144),
+          Q5_K: (256, 176), Q6_K: (256, 210)}
 
 
 def qmatrix_bytes(qtype, rows, cols):
@@ -120,8 +121,13 @@ def synth_qblocks(qtype, rows, cols, seed=0, dscale=0.002):
     n = rows * (cols // w)
     blk = rng.integers(0, 256, size=(n, nb), dtype=np.uint8)
     d = (rng.random(n) * dscale + dscale / 4).astype(np.float16).view(np.uint8).reshape(n, 2)
-    if qtype == Q8_0:
+    if qtype in (Q8_0, Q4_0):
         blk[:, 0:2] = d
+    elif qtype == Q4_1:
+        blk[:, 0:2] = d                                       # d; m about -8 d (a centred range)
+        blk[:, 2:4] = (-(rng.random(n) * 8 + 4) * dscale / 2).astype(np.float16).view(np.uint8).reshape(n, 2)
+    elif qtype == Q3_K:
+        blk[:, 108:110] = d
     elif qtype in (Q4_K, Q5_K):
         blk[:, 0:2] = d                                       # d; dmin about a tenth of it
         blk[:, 2:4] = (rng.random(n) * dscale / 10).astype(np.float16).view(np.uint8).reshape(n, 2)

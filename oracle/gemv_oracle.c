@@ -1,15 +1,22 @@
 /* gemv_oracle.c -- CPU restatement of gguf-rs-cli's quantized matrix-vector
- * product for the Q8_0, Q4_K, Q5_K and Q6_K block types (the logits projection,
+ * product for the Q4_0, Q4_1, Q8_0, Q3_K, Q4_K, Q5_K and Q6_K block types
+ * (the logits projection,
  * src/model/llama.rs:405-407 on the CPU path).
  * TEST INFRASTRUCTURE ONLY (parity checker); never linked into the product.
  *
  * Follows src/tensor/dequant.rs:
+ *   dq40      :26-41   Q4_0 dequantization, w = ((q - 8) as f32) * d
+ *   dq41      :42-54   Q4_1 dequantization, w = (q as f32) * d + m
  *   dq80      :86-94   Q8_0 dequantization, w = (q as f32) * d
+ *   Q3_K      the GGUF format (see oracle_dequant_q3_k: the reference's
+ *             dq3k :120-140 decodes another layout), w = (d * sc) * q
  *   dq6k      :197-219 Q6_K dequantization, w = (d * (scale as f32)) * q
  *   get_scale_min_k4 :141-148, dq4k :149-170, dq5k :171-196
  *                      Q4_K / Q5_K, w = (d * sc) * q - dmin * m
  *   row_dot   :277-313 Q8_0: per block a sequential f32 sum of (q * d) * x,
- *                      then a sequential sum of the block sums;
+ *                      then a sequential sum of the block sums; Q4_0: per
+ *                      block a sequential sum over j of (lo_j + hi_j), lo_j =
+ *                      ((q_j - 8) * d) * x_j, hi_j the same for weight j + 16;
  *                      other types (K-quants): dequantize the row, then a
  *                      sequential f32 sum of w * x
  *   matvec    :315-318 out[i] = row_dot(i, x), rows in parallel
@@ -23,7 +30,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#define QT_Q4_0 2u
+#define QT_Q4_1 3u
 #define QT_Q8_0 8u
+#define QT_Q3_K 11u
 #define QT_Q4_K 12u
 #define QT_Q5_K 13u
 #define QT_Q6_K 14u
@@ -61,6 +71,73 @@ void oracle_dequant_q8_0(const uint8_t *data, size_t n, float *o)
         const uint8_t *d = data + b * 34;
         const float sc = oracle_f16_to_f32(rd16(d));
         for (int i = 0; i < 32; i++) o[b * 32 + i] = (float)(int8_t)d[2 + i] * sc;
+    }
+}
+
+/* dq40 (dequant.rs:26-41): n weights from n/32 blocks of 18 bytes; byte
+ * 2 + j holds weight j (low nibble) and weight j + 16 (high). */
+void oracle_dequant_q4_0(const uint8_t *data, size_t n, float *o)
+{
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *d = data + b * 18;
+        const float sc = oracle_f16_to_f32(rd16(d));
+        for (int j = 0; j < 16; j++) {
+            o[b * 32 + j] = (float)((int)(d[2 + j] & 0xF) - 8) * sc;
+            o[b * 32 + j + 16] = (float)((int)(d[2 + j] >> 4) - 8) * sc;
+        }
+    }
+}
+
+/* dq41 (dequant.rs:42-54): n/32 blocks of 20 bytes (f16 d, f16 m, 16 bytes
+ * of nibbles as Q4_0), w = q * d + m. */
+void oracle_dequant_q4_1(const uint8_t *data, size_t n, float *o)
+{
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *d = data + b * 20;
+        const float sc = oracle_f16_to_f32(rd16(d)), mn = oracle_f16_to_f32(rd16(d + 2));
+        for (int j = 0; j < 16; j++) {
+            o[b * 32 + j] = (float)(d[4 + j] & 0xF) * sc + mn;
+            o[b * 32 + j + 16] = (float)(d[4 + j] >> 4) * sc + mn;
+        }
+    }
+}
+
+/* The 6-bit scale of sub-block is (0..15) of a Q3_K block, as GGUF packs
+ * them in 12 bytes: bytes 0-7 hold the low nibbles (scales 0-7 low, 8-15
+ * high nibbles), bytes 8-11 the top two bits (bits 2k..2k+1 of byte 8 + j
+ * for scale 4k + j).  Returns the signed scale, value - 32. */
+static int q3k_scale(const uint8_t *s, int is)
+{
+    const int k = is >> 2, j = is & 3;
+    const int low = k == 0 ? (s[j] & 0xF) : k == 1 ? (s[4 + j] & 0xF) : k == 2 ? (s[j] >> 4) : (s[4 + j] >> 4);
+    const int high = (s[8 + j] >> (2 * k)) & 3;
+    return (low | (high << 4)) - 32;
+}
+
+/* Q3_K: n/256 blocks of 110 bytes (hmask[32], qs[64], scales[12], f16 d), in
+ * the GGUF format: weight i = 128 n + 32 j + l (n < 2, j < 4, l < 32) has the
+ * low two bits (qs[32 n + l] >> 2 j) & 3, the third bit (hmask[l] >> (4 n +
+ * j)) & 1, value q = bits - 4, and sub-block scale i / 16.  w = (d * sc) * q
+ * as the reference's dq3k evaluates it (dequant.rs:136).
+ * Deviation: the reference's dq3k reads the low bits of weight i from
+ * qs[i / 4] >> 2 (i % 4) (:134), and scale j < 4 as the low six bits of
+ * byte j, scale 8 + j as those of byte 8 + j, the others from nibble pairs
+ * (:126-131); its GPU shader (q3k_gemv.glsl) decodes the scales another way
+ * again.  The GGUF layout is the one files carry, so Q3_K is pinned to the
+ * format by bit probes, not to either reference path. */
+void oracle_dequant_q3_k(const uint8_t *data, size_t n, float *o)
+{
+    for (size_t b = 0; b < n / 256; b++) {
+        const uint8_t *d = data + b * 110;
+        const uint8_t *hm = d, *qs = d + 32, *sc = d + 96;
+        const float df = oracle_f16_to_f32(rd16(d + 108));
+        for (int i = 0; i < 256; i++) {
+            const int nn = i >> 7, j = (i >> 5) & 3, l = i & 31;
+            const int lo = (qs[32 * nn + l] >> (2 * j)) & 3;
+            const int hi = (hm[l] >> (4 * nn + j)) & 1;
+            const int q = (lo | (hi << 2)) - 4;
+            o[b * 256 + i] = df * (float)q3k_scale(sc, i >> 4) * (float)q;
+        }
     }
 }
 
@@ -165,6 +242,9 @@ void oracle_dequant_q5_k(const uint8_t *data, size_t n, float *o)
 static size_t row_bytes(uint32_t qt, size_t cols)
 {
     switch (qt) {
+    case QT_Q4_0: return cols / 32 * 18;
+    case QT_Q4_1: return cols / 32 * 20;
+    case QT_Q3_K: return cols / 256 * 110;
     case QT_Q8_0: return cols / 32 * 34;
     case QT_Q4_K: return cols / 256 * 144;
     case QT_Q5_K: return cols / 256 * 176;
@@ -175,6 +255,9 @@ static size_t row_bytes(uint32_t qt, size_t cols)
 static void dequant(uint32_t qt, const uint8_t *d, size_t n, float *w)
 {
     switch (qt) {
+    case QT_Q4_0: oracle_dequant_q4_0(d, n, w); break;
+    case QT_Q4_1: oracle_dequant_q4_1(d, n, w); break;
+    case QT_Q3_K: oracle_dequant_q3_k(d, n, w); break;
     case QT_Q8_0: oracle_dequant_q8_0(d, n, w); break;
     case QT_Q4_K: oracle_dequant_q4_k(d, n, w); break;
     case QT_Q5_K: oracle_dequant_q5_k(d, n, w); break;
@@ -197,7 +280,22 @@ static float row_dot(uint32_t qt, const uint8_t *d, size_t cols, const float *x,
         }
         return acc;
     }
-    dequant(qt, d, cols, w);      /* K-quants: the row dequantized, then one sequential sum */
+    if (qt == QT_Q4_0) {
+        float acc = 0.0f;
+        for (size_t blk = 0; blk < cols / 32; blk++) {
+            const uint8_t *db = d + blk * 18;
+            const float sc = oracle_f16_to_f32(rd16(db));
+            float s = 0.0f;
+            for (int j = 0; j < 16; j++) {
+                const float lo = (float)((int)(db[2 + j] & 0xF) - 8) * sc * x[blk * 32 + j];
+                const float hi = (float)((int)(db[2 + j] >> 4) - 8) * sc * x[blk * 32 + j + 16];
+                s += lo + hi;
+            }
+            acc += s;
+        }
+        return acc;
+    }
+    dequant(qt, d, cols, w);      /* the others: the row dequantized, then one sequential sum */
     float acc = 0.0f;
     for (size_t i = 0; i < cols; i++) acc += w[i] * x[i];
     return acc;
@@ -256,7 +354,9 @@ static void *run_rows(void *arg)
 int oracle_matvec(uint32_t qtype, const uint8_t *blocks, size_t rows, size_t cols, const float *x,
                   float *out, double *exact, double *abs_sum, int nthreads)
 {
-    if (qtype != QT_Q8_0 && qtype != QT_Q6_K && qtype != QT_Q4_K && qtype != QT_Q5_K) return -1;
+    if (qtype != QT_Q8_0 && qtype != QT_Q6_K && qtype != QT_Q4_K && qtype != QT_Q5_K && qtype != QT_Q4_0 &&
+        qtype != QT_Q4_1 && qtype != QT_Q3_K)
+        return -1;
     if (nthreads < 1) nthreads = 1;
     if ((size_t)nthreads > rows) nthreads = rows ? (int)rows : 1;
     pthread_t th[64];

@@ -67,6 +67,9 @@ def load(build_if_missing=True):
     lib.oracle_dequant_q6_k.argtypes = [P, SZ, P]
     lib.oracle_dequant_q4_k.argtypes = [P, SZ, P]
     lib.oracle_dequant_q5_k.argtypes = [P, SZ, P]
+    lib.oracle_dequant_q4_0.argtypes = [P, SZ, P]
+    lib.oracle_dequant_q4_1.argtypes = [P, SZ, P]
+    lib.oracle_dequant_q3_k.argtypes = [P, SZ, P]
     lib.oracle_row_dot.argtypes = [ctypes.c_uint32, P, SZ, P]
     lib.oracle_row_dot.restype = F
     lib.oracle_matvec.argtypes = [ctypes.c_uint32, P, SZ, SZ, P, P, P, P, ctypes.c_int]
@@ -232,20 +235,25 @@ def now():
 
 
 # ---- quantized matvec (src/tensor/dequant.rs) -------------------------------
+QT_Q4_0 = 2
+QT_Q4_1 = 3
 QT_Q8_0 = 8
+QT_Q3_K = 11
 QT_Q4_K = 12
 QT_Q5_K = 13
 QT_Q6_K = 14
 
 
 def dequant(qtype, blocks, n):
-    """dq80 / dq4k / dq5k / dq6k (src/tensor/dequant.rs:86-94, 141-196,
-    197-219): n f32 weights."""
+    """dq40 / dq41 / dq80 / dq4k / dq5k / dq6k (src/tensor/dequant.rs:26-54,
+    86-94, 141-219) and Q3_K in the GGUF layout: n f32 weights."""
     lib = load()
     b = np.ascontiguousarray(blocks, dtype=np.uint8)
     out = np.empty(n, np.float32)
     f = {QT_Q8_0: lib.oracle_dequant_q8_0, QT_Q4_K: lib.oracle_dequant_q4_k,
-         QT_Q5_K: lib.oracle_dequant_q5_k, QT_Q6_K: lib.oracle_dequant_q6_k}[qtype]
+         QT_Q5_K: lib.oracle_dequant_q5_k, QT_Q6_K: lib.oracle_dequant_q6_k,
+         QT_Q4_0: lib.oracle_dequant_q4_0, QT_Q4_1: lib.oracle_dequant_q4_1,
+         QT_Q3_K: lib.oracle_dequant_q3_k}[qtype]
     f(b.ctypes.data, n, out.ctypes.data)
     return out
 

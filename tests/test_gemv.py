@@ -1,10 +1,12 @@
 """The quantized output projection (the logits producer, src/model/llama.rs:333-334):
-CPU pins of the oracle's Q8_0 / Q4_K / Q5_K / Q6_K dequantization and matvec
-(src/tensor/dequant.rs:86-94, 141-219, 277-318), and GPU parity of gs_gemv
-(include/gs_gemv.h) against it.  Q5_K follows the GGUF format where the
-reference cannot (its dq5k indexes past its 32-byte qh slice from the third
-step on, src/tensor/dequant.rs:177,192): its pins are the format's bit
-layout, not reference outputs.
+CPU pins of the oracle's Q4_0 / Q4_1 / Q8_0 / Q3_K / Q4_K / Q5_K / Q6_K
+dequantization and matvec (src/tensor/dequant.rs:26-54, 86-94, 141-219,
+277-318), and GPU parity of gs_gemv (include/gs_gemv.h) against it.  Q5_K
+follows the GGUF format where the reference cannot (its dq5k indexes past its
+32-byte qh slice from the third step on, src/tensor/dequant.rs:177,192), and
+Q3_K where the reference's two paths disagree with each other and with the
+format (dq3k :120-140, q3k_gemv.glsl): their pins are the format's bit layout,
+not reference outputs.
 
 The GPU sums in its own order, so parity is a tolerance: with exact the
 float64 value of the reference's f32 weights times x (oracle.matvec exact=True),
@@ -16,7 +18,7 @@ above the bound.
 import numpy as np
 import pytest
 
-Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+Q4_0, Q4_1, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K = 2, 3, 8, 11, 12, 13, 14
 
 
 def _f32_bits(a):
@@ -177,13 +179,128 @@ def test_q8_0_bytes_and_scale(oracle):
     assert np.array_equal(w, q.astype(np.float32) * np.float32(0.125))
 
 
+def test_q4_0_q4_1_nibbles(oracle):
+    """dq40 / dq41: byte 2 + l (Q4_1: 4 + l) holds weight l in its low nibble
+    and weight l + 16 in its high nibble; Q4_0 w = (q - 8) d, Q4_1 w = q d + m."""
+    q = np.arange(32) % 16
+    nib = (q[:16] | (q[16:][::-1] << 4)).astype(np.uint8)      # high nibbles reversed
+    want_q = np.concatenate([q[:16], q[16:][::-1]]).astype(np.float32)
+    d = np.array([0.375], np.float16)
+    b0 = np.concatenate([d.view(np.uint8), nib])
+    assert np.array_equal(oracle.dequant(Q4_0, b0, 32), (want_q - 8) * np.float32(0.375))
+    m = np.array([-2.5], np.float16)
+    b1 = np.concatenate([d.view(np.uint8), m.view(np.uint8), nib])
+    assert np.array_equal(oracle.dequant(Q4_1, b1, 32), want_q * np.float32(0.375) + np.float32(-2.5))
+
+
+def _q3_block(hmask=None, qs=None, scales=None, d=1.0):
+    b = np.zeros(110, np.uint8)
+    if hmask is not None:
+        b[0:32] = hmask
+    if qs is not None:
+        b[32:96] = qs
+    if scales is not None:
+        b[96:108] = scales
+    b[108:110] = np.array([d], np.float16).view(np.uint8)
+    return b
+
+
+# GGUF's packing of the sixteen 6-bit Q3_K scales in 12 bytes, bit by bit:
+# (byte, bit) -> (sub-block of 16 weights, bit of the value).
+def _q3_scale_bits():
+    tab = {}
+    for j in range(4):
+        for bit in range(4):
+            tab[(j, bit)] = (j, bit)                    # bytes 0-3 low nibbles: scales 0-3
+            tab[(j, bit + 4)] = (8 + j, bit)            # high nibbles: scales 8-11
+            tab[(4 + j, bit)] = (4 + j, bit)            # bytes 4-7: scales 4-7
+            tab[(4 + j, bit + 4)] = (12 + j, bit)       # and 12-15
+        for k in range(4):
+            for hb in range(2):
+                tab[(8 + j, 2 * k + hb)] = (4 * k + j, 4 + hb)   # bytes 8-11: top two bits
+    return tab
+
+
+def test_q3k_scale_bit_probes(oracle):
+    """Every bit of the 12 scale bytes moves exactly the 16 weights of the
+    sub-block GGUF's layout gives it, by the bit's value times d q; all quants
+    1 (low bits 01, third bit set), scales 0 (value -32), d = 0.5."""
+    hm = np.full(32, 0xFF, np.uint8)
+    qs = np.full(64, 0x55, np.uint8)
+    base = oracle.dequant(Q3_K, _q3_block(hm, qs, d=0.5), 256)
+    assert np.all(base == np.float32(-16.0))
+    tab = _q3_scale_bits()
+    assert len(tab) == 96
+    for (byte, bit), (sub, vbit) in tab.items():
+        sc = np.zeros(12, np.uint8)
+        sc[byte] = 1 << bit
+        w = oracle.dequant(Q3_K, _q3_block(hm, qs, sc, d=0.5), 256)
+        diff = np.nonzero(w != base)[0]
+        assert list(diff) == list(range(16 * sub, 16 * sub + 16)), (byte, bit, diff[:4])
+        assert np.all(w[diff] == np.float32(0.5 * ((1 << vbit) - 32))), (byte, bit, w[diff[0]])
+
+
+def test_q3k_quant_bit_probes(oracle):
+    """Bits 2j, 2j+1 of qs[32 n + l] are the low bits (1, 2) of weight
+    128 n + 32 j + l, bit 4 n + j of hmask[l] its third bit (4); with all
+    bits clear every weight is q = -4.  Scales 1..16 (bytes give value
+    s + 32), d = 0.25."""
+    sc_val = np.arange(1, 17)
+    raw = sc_val + 32                                   # 6-bit stored values
+    sc = np.zeros(12, np.uint8)
+    for i, v in enumerate(raw):
+        k, j = i >> 2, i & 3
+        lo, hi = v & 0xF, v >> 4
+        sc[(k & 1) * 4 + j] |= lo << (0 if k < 2 else 4)
+        sc[8 + j] |= hi << (2 * k)
+    base = oracle.dequant(Q3_K, _q3_block(scales=sc, d=0.25), 256)
+    assert np.array_equal(base, (-4.0 * 0.25 * np.repeat(sc_val, 16)).astype(np.float32))
+    for n in range(2):
+        for j in range(4):
+            for l in (0, 5, 16, 31):
+                pos = 128 * n + 32 * j + l
+                for c in range(2):
+                    qs = np.zeros(64, np.uint8)
+                    qs[32 * n + l] = 1 << (2 * j + c)
+                    w = oracle.dequant(Q3_K, _q3_block(qs=qs, scales=sc, d=0.25), 256)
+                    diff = np.nonzero(w != base)[0]
+                    assert list(diff) == [pos], (n, j, l, c, diff)
+                    assert w[pos] == np.float32(0.25 * sc_val[pos // 16] * ((1 << c) - 4))
+                hm = np.zeros(32, np.uint8)
+                hm[l] = 1 << (4 * n + j)
+                w = oracle.dequant(Q3_K, _q3_block(hmask=hm, scales=sc, d=0.25), 256)
+                diff = np.nonzero(w != base)[0]
+                assert list(diff) == [pos], (n, j, l, diff)
+                assert w[pos] == np.float32(0.0)
+
+
+def test_q4_0_row_dot_order(oracle):
+    """row_dot's Q4_0 arm (dequant.rs:289-298): per block a sequential f32 sum
+    over j of (lo_j + hi_j), lo_j = ((q_j - 8) d) x_j, hi_j the same for weight
+    j + 16; then a sequential sum of the block sums."""
+    import workloads
+    rng = np.random.default_rng(11)
+    cols = 160
+    blocks = workloads.synth_qblocks(Q4_0, 1, cols, seed=12)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = oracle.dequant(Q4_0, blocks, cols)
+    acc = np.float32(0.0)
+    for b in range(cols // 32):
+        s = np.float32(0.0)
+        for j in range(16):
+            s = np.float32(s + np.float32(np.float32(w[32 * b + j] * x[32 * b + j])
+                                          + np.float32(w[32 * b + 16 + j] * x[32 * b + 16 + j])))
+        acc = np.float32(acc + s)
+    assert np.float32(oracle.row_dot(Q4_0, blocks, cols, x)) == acc
+
+
 def test_row_dot_order_and_unit_vectors(oracle):
     """row_dot: Q6_K sums w * x left to right in f32 (numpy's sequential
     accumulate); Q8_0 sums each block left to right, then the block sums.
     A unit vector picks one weight exactly."""
     import workloads
     rng = np.random.default_rng(3)
-    for qt, cols in ((Q6_K, 512), (Q8_0, 96), (Q4_K, 512), (Q5_K, 512)):
+    for qt, cols in ((Q6_K, 512), (Q8_0, 96), (Q4_K, 512), (Q5_K, 512), (Q4_1, 96), (Q3_K, 512)):
         blocks = workloads.synth_qblocks(qt, 1, cols, seed=5)
         w = oracle.dequant(qt, blocks, cols)
         x = rng.standard_normal(cols).astype(np.float32)
@@ -209,7 +326,8 @@ def test_matvec_exact_bound(oracle):
     the exact value; matvec rows equal row_dot."""
     import workloads
     rng = np.random.default_rng(4)
-    for qt, rows, cols in ((Q6_K, 20, 1024), (Q8_0, 20, 1024), (Q4_K, 20, 1024), (Q5_K, 20, 1024)):
+    for qt, rows, cols in ((Q6_K, 20, 1024), (Q8_0, 20, 1024), (Q4_K, 20, 1024), (Q5_K, 20, 1024),
+                           (Q4_0, 20, 1024), (Q4_1, 20, 1024), (Q3_K, 20, 1024)):
         blocks = workloads.synth_qblocks(qt, rows, cols, seed=6)
         x = rng.standard_normal(cols).astype(np.float32)
         f32 = oracle.matvec(qt, blocks, rows, cols, x, nthreads=2)
@@ -247,6 +365,14 @@ def _gpu_check(gpu, torch, oracle, qt, rows, cols, seed, B=1, x_kind="normal"):
         kb = blocks.reshape(-1, 176 if qt == Q5_K else 144)
         dd = kb[:, 0:4].copy().view(np.float16).astype(np.float64)
         smax = 63.0 * (dd[:, 0].max() + dd[:, 1].max())
+    elif qt in (Q4_0, Q4_1):
+        # d (sum q x - 8 sum x) / d sum q x + m sum x per block
+        kb = blocks.reshape(-1, 20 if qt == Q4_1 else 18)
+        dd = np.abs(kb[:, 0:4 if qt == Q4_1 else 2].copy().view(np.float16).astype(np.float64))
+        smax = 16.0 * dd[:, 0].max() + (dd[:, 1].max() if qt == Q4_1 else 0.0)
+    elif qt == Q3_K:
+        # (d sc) (sum u x - 4 sum x) per 16 weights, |sc| <= 32
+        smax = 32.0 * blocks.reshape(-1, 110)[:, 108:110].copy().view(np.float16).astype(np.float64).max()
     else:
         smax = blocks.reshape(-1, 34)[:, :2].copy().view(np.float16).astype(np.float64).max()
     for b in range(B):
@@ -276,6 +402,17 @@ def _gpu_check(gpu, torch, oracle, qt, rows, cols, seed, B=1, x_kind="normal"):
     (Q5_K, 517, 4096),
     (Q5_K, 37, 256),
     (Q5_K, 300, 8192),
+    (Q4_0, 1000, 3584),      # register path: 112 blocks, 2 per lane
+    (Q4_0, 517, 4096),
+    (Q4_0, 77, 32),          # one block per row
+    (Q4_0, 200, 8192),       # LDS path
+    (Q4_1, 1000, 3584),
+    (Q4_1, 77, 32),
+    (Q4_1, 200, 8192),
+    (Q3_K, 1000, 3584),      # register path, 56 of 64 lanes
+    (Q3_K, 517, 4096),
+    (Q3_K, 37, 256),
+    (Q3_K, 300, 8192),       # LDS path
 ])
 def test_gemv_parity(gpu, torch, oracle, qt, rows, cols):
     _gpu_check(gpu, torch, oracle, qt, rows, cols, seed=rows + cols)
@@ -292,6 +429,9 @@ def test_gemv_inputs(gpu, torch, oracle):
     _gpu_check(gpu, torch, oracle, Q8_0, 40000, 1024, seed=5)
     _gpu_check(gpu, torch, oracle, Q4_K, 2000, 3584, seed=6, x_kind="spiky")
     _gpu_check(gpu, torch, oracle, Q5_K, 64, 3584, seed=7, B=3)
+    _gpu_check(gpu, torch, oracle, Q4_0, 2000, 3584, seed=8, x_kind="spiky")
+    _gpu_check(gpu, torch, oracle, Q4_1, 64, 3584, seed=9, B=3)
+    _gpu_check(gpu, torch, oracle, Q3_K, 2000, 3584, seed=10, x_kind="sparse")
 
 
 @pytest.mark.gpu
@@ -299,6 +439,8 @@ def test_gemv_inputs(gpu, torch, oracle):
     (Q6_K, 152064, 3584),    # Qwen2.5-7B lm_head (the bench's GEMV)
     (Q4_K, 152064, 3584),
     (Q8_0, 128256, 4096),    # Llama-3-8B lm_head shape
+    (Q4_0, 152064, 3584),
+    (Q3_K, 152064, 3584),
 ])
 def test_gemv_full_lm_head(gpu, torch, oracle, qt, rows, cols):
     """Full output-projection shapes, every row against the oracle."""
