@@ -287,20 +287,21 @@ q6k_gemv_lds(Q6Planes P, const float *x, float *out, int rows, int nb)
 // 128 n + 32 j + l has low bits (qs[32 n + l] >> 2 j) & 3, third bit
 // (hmask[l] >> (4 n + j)) & 1, value q = bits - 4, and scale (16 sub-blocks
 // of 16, 6 bits each, minus 32).  A quarter (n, l0) is the Q6_K quarter
-// (h = n, g = j).  Planes, element e = 4 block + 2 n + l0 / 16:
-//   q: 16 bytes per quarter, qs[32 n + l0 ..]; h: two words per quarter,
-//   bits 16 (j & 1) + k of word j >> 1 = the third bit of weight l0 + k of
-//   group j; s: one word per quarter, byte j = the signed scale of group j;
-//   d: the f16 d per block.
+// (h = n, g = j).  The upload merges the three bits of a weight into a
+// nibble, u = q + 4 (the decode is then Q4_K's: 146 bytes per block on the
+// device for the file's 110, and about half the instructions per weight).
+// Planes, element e = 4 block + 2 n + l0 / 16:
+//   q: 32 bytes per quarter: byte k of the first 16 holds u of weight
+//   l0 + k of group 0 (low nibble) and group 1 (high), of the second 16
+//   groups 2 and 3; s: one word per quarter, byte j = the signed scale of
+//   group j; d: the f16 d per block.
 struct Q3Planes {
     const uint8_t *q;
-    const uint2 *h;
     const uint32_t *s;
     const uint16_t *d;
 };
 struct Q3Quarter {
-    uint4 q;
-    uint2 h;
+    uint4 a, b;
     uint32_t s;
     uint16_t d;
 };
@@ -310,8 +311,8 @@ struct Q3Fmt {
     static __device__ __forceinline__ Unit load(const Planes &P, uint32_t e)
     {
         Unit u;
-        u.q = ntl4(P.q + e * 16u);
-        u.h = ntl2(P.h + e);
+        u.a = ntl4(P.q + e * 32u);
+        u.b = ntl4(P.q + e * 32u + 16u);
         u.s = __builtin_nontemporal_load(P.s + e);
         u.d = __builtin_nontemporal_load(P.d + (e >> 2));
         return u;
@@ -319,18 +320,16 @@ struct Q3Fmt {
     // sum over the groups of (d * scale_j) * (sum u x - 4 sum x), u = q + 4
     static __device__ __forceinline__ float dot(const Unit &u, const float (&xg)[4][16], const float (&sx)[4])
     {
-        const uint32_t W[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+        const uint32_t A[4] = {u.a.x, u.a.y, u.a.z, u.a.w}, B[4] = {u.b.x, u.b.y, u.b.z, u.b.w};
         float dt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int w = 0; w < 4; w++) {
+            const uint32_t v[4] = {A[w] & 0x0F0F0F0Fu, (A[w] >> 4) & 0x0F0F0F0Fu, B[w] & 0x0F0F0F0Fu,
+                                   (B[w] >> 4) & 0x0F0F0F0Fu};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t hw = j < 2 ? u.h.x : u.h.y;
-                const uint32_t nib = (hw >> (16 * (j & 1) + 4 * w)) & 0xFu;
-                const uint32_t v = ((W[w] >> (2 * j)) & 0x03030303u) | (((nib * 0x00204081u) & 0x01010101u) << 2);
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-                for (int t = 0; t < 4; t++) dt[j] = fmaf(ub(v, t), xg[j][4 * w + t], dt[j]);
-            }
+                for (int t = 0; t < 4; t++) dt[j] = fmaf(ub(v[j], t), xg[j][4 * w + t], dt[j]);
         }
         const float d = h2f(u.d);
         float acc = 0.0f;
@@ -342,6 +341,7 @@ struct Q3Fmt {
         return acc;
     }
 };
+constexpr int kRB3 = 8, kPF3 = 2, kNT3 = 768;   // Q3_K: the Q6_K structure
 template <int kRB, int PF, int NT>
 __global__ void __launch_bounds__(NT)
 q3k_gemv_xreg(Q3Planes P, const float *x, float *out, int rows, int nb)
@@ -922,7 +922,7 @@ int upload_q3k(const uint8_t *src, size_t rows, size_t nb, gs_qmatrix *m)
 {
     const size_t n = rows * nb, np = 4 * n;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    const size_t off_h = al(np * 16), off_s = off_h + al(np * 8), off_d = off_s + al(np * 4);
+    const size_t off_s = al(np * 32), off_d = off_s + al(np * 4);
     const size_t total = off_d + n * 2;
     uint8_t *h = new (std::nothrow) uint8_t[total];
     if (!h) return GS_ERR_NOMEM;
@@ -932,12 +932,13 @@ int upload_q3k(const uint8_t *src, size_t rows, size_t nb, gs_qmatrix *m)
         for (int qq = 0; qq < 4; qq++) {
             const int nn = qq >> 1, l0 = (qq & 1) * 16;
             const size_t e = 4 * i + qq;
-            memcpy(h + e * 16, qs + 32 * nn + l0, 16);
-            uint32_t hw[2] = {0u, 0u};
             for (int j = 0; j < 4; j++)
-                for (int k = 0; k < 16; k++)
-                    hw[j >> 1] |= (uint32_t)((hm[l0 + k] >> (4 * nn + j)) & 1u) << (16 * (j & 1) + k);
-            memcpy(h + off_h + e * 8, hw, 8);
+                for (int k = 0; k < 16; k++) {
+                    const int l = l0 + k;
+                    const uint8_t u = (uint8_t)(((qs[32 * nn + l] >> (2 * j)) & 3u) | (((hm[l] >> (4 * nn + j)) & 1u) << 2));
+                    uint8_t &dst = h[e * 32 + 16 * (j >> 1) + k];
+                    dst = (j & 1) ? (uint8_t)(dst | (u << 4)) : u;
+                }
             for (int j = 0; j < 4; j++)
                 h[off_s + e * 4 + j] = (uint8_t)(int8_t)q3k_scale(sc, 8 * nn + 2 * j + l0 / 16);
         }
@@ -951,8 +952,7 @@ int upload_q3k(const uint8_t *src, size_t rows, size_t nb, gs_qmatrix *m)
     const hipError_t ce = hipMemcpy(m->base, h, total, hipMemcpyHostToDevice);
     delete[] h;
     if (ce != hipSuccess) { (void)hipFree(m->base); m->base = nullptr; return GS_ERR_HIP; }
-    m->q3 = gs::Q3Planes{m->base, (const uint2 *)(m->base + off_h), (const uint32_t *)(m->base + off_s),
-                         (const uint16_t *)(m->base + off_d)};
+    m->q3 = gs::Q3Planes{m->base, (const uint32_t *)(m->base + off_s), (const uint16_t *)(m->base + off_d)};
     return GS_OK;
 }
 } // namespace
@@ -1095,7 +1095,7 @@ int gs_gemv(const gs_qmatrix *m, const float *d_x, size_t B, float *d_out, void 
             }
         } else if (m->qtype == GS_QTYPE_Q3_K) {
             if (4 * nb <= 64)
-                hipLaunchKernelGGL((gs::q3k_gemv_xreg<gs::kRB6, gs::kPF6, gs::kNT6>), dim3(m->cus), dim3(gs::kNT6), 0, st, m->q3, x, o, rows, nb);
+                hipLaunchKernelGGL((gs::q3k_gemv_xreg<gs::kRB3, gs::kPF3, gs::kNT3>), dim3(m->cus), dim3(gs::kNT3), 0, st, m->q3, x, o, rows, nb);
             else
                 hipLaunchKernelGGL(gs::q3k_gemv_lds, dim3(2 * m->cus), dim3(gs::kGemvThreads), 0, st, m->q3, x, o, rows, nb);
         } else if (m->qtype == GS_QTYPE_Q6_K) {
