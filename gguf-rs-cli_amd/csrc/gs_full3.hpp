@@ -380,7 +380,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
         const bool at = lim && lim_arr == 0u;
         if (at) end = lim_pos + 1u;
         const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 64u);
-        F3_TS(16 + 5 * s);
+        if (s == 1) F3_TS(16 + 5 * s);
         *cum_out = cum;
         if (p < end) { *arr = 0u; *pos = p; return 1; }
         if (at) return 2;
@@ -396,7 +396,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
             const bool at = lim && lim_arr == 1u && lim_pos >= beg && lim_pos < end;
             if (at) end = lim_pos + 1u;
             const uint32_t p = f3_chain(st, roff + beg, roff + end, &cum, pred);
-            F3_TS(17 + 5 * s + min(g, 3));
+            if (s == 1) F3_TS(17 + 5 * s + min(g, 3));
             *cum_out = cum;
             if (p < roff + end) { *arr = 1u; *pos = p - roff; return 1; }
             if (at) return 2;
@@ -541,12 +541,13 @@ __device__ __forceinline__ void f3_count_exact(Full3Smem &f, int s, int r, float
 
 // Plan of one accumulation's runs over bins [bH, kFBins).  Per bin (kPer per
 // thread, from the caller): key[q] = grid exponent + 256 for a bin of a run,
-// kF3KeyListed or kF3KeyNone; klo / khi its level range.  Writes the run
+// kF3KeyListed or kF3KeyNone; KL[b] / KH[b] (LDS, by bin) its level range,
+// read at the runs' ends only.  Writes the run
 // table s (runs numbered in bin order; level slots from lbase) and rid[q]
 // (the bin's run, or -1).  False if there are more than kF3Runs runs or
 // their levels exceed lcap.
-__device__ bool f3_plan_runs(RowSmem &sm, Full3Smem &f, int s, int bH, const uint32_t *key, const uint32_t *klo,
-                             const uint32_t *khi, int *rid, uint32_t lbase, uint32_t lcap)
+__device__ bool f3_plan_runs(RowSmem &sm, Full3Smem &f, int s, int bH, const uint32_t *key, const uint32_t *KL,
+                             const uint32_t *KH, int *rid, uint32_t lbase, uint32_t lcap)
 {
     constexpr int kPer = kFBins / kThreads;
     const int t = threadIdx.x;
@@ -568,6 +569,7 @@ __device__ bool f3_plan_runs(RowSmem &sm, Full3Smem &f, int s, int bH, const uin
     }
     uint32_t tot;
     uint32_t o = block_excl_u32(n, &tot, sm);
+    if (s == 1) F3_TS(19);
     if (tot > (uint32_t)kF3Runs) return false;
     int cur = (int)o - 1;
 #pragma unroll
@@ -577,13 +579,14 @@ __device__ bool f3_plan_runs(RowSmem &sm, Full3Smem &f, int s, int bH, const uin
         if (st[q]) {
             cur++;
             f.run[s][cur].e = (int)key[q] - 256;
-            f.run[s][cur].khi = khi[q];
+            f.run[s][cur].khi = KH[b];
         }
         rid[q] = in ? cur : -1;
         const uint32_t nk = q + 1 < kPer ? key[q + 1] : nxt;
-        if (in && (b == kFBins - 1 || nk != key[q])) f.run[s][cur].klo = klo[q];
+        if (in && (b == kFBins - 1 || nk != key[q])) f.run[s][cur].klo = KL[b];
     }
     __syncthreads();
+    if (s == 1) F3_TS(20);
     if (t < 64) {
         uint32_t span = 0;
         if (t < (int)tot) {
@@ -1011,6 +1014,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             }
             f.lvl[b] = key[q];
             f.lvl[kFBins + b] = khi[q];
+            reinterpret_cast<uint32_t *>(f.u.w23)[b] = klo[q];
         }
         __syncthreads();
         // level slots a bin adds to its run, counted from the bottom of the
@@ -1050,7 +1054,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         for (int q = 0; q < kPer; q++) if (kPer * t + q < bH) key[q] = kF3KeyListed;
         int rid[kPer];
         F3_TS(27);
-        if (!f3_plan_runs(sm, f, 0, bH, key, klo, khi, rid, 0u, (uint32_t)kF3L1)) F3_FAIL();
+        if (!f3_plan_runs(sm, f, 0, bH, key, reinterpret_cast<const uint32_t *>(f.u.w23), f.lvl + kFBins, rid, 0u,
+                          (uint32_t)kF3L1))
+            F3_FAIL();
         F3_TS(28);
         uint32_t capv[kPer], capl = 0;
 #pragma unroll
@@ -1262,15 +1268,16 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         band3 = (float)((double)kF3Band23 * 2.0 + (s2hi / s2lo - 1.0));
         __syncthreads();
         const double is2hi = 1.0 / s2hi, is2lo = 1.0 / s2lo;
-        uint32_t key2[kPer], key3[kPer], klo2[kPer], khi2[kPer], klo3[kPer], khi3[kPer], rl[kPer], ku2[kPer],
-            ku3[kPer];
+        // the bins' level ranges go to LDS (free here: the top of lvl holds
+        // the run planner's keys), the rest stays in registers
+        uint32_t *KL2 = reinterpret_cast<uint32_t *>(f.u.w23), *KL3 = KL2 + kFBins;
+        uint32_t *KH2 = f.lvl, *KH3 = f.lvl + kFBins;
+        uint32_t key2[kPer], key3[kPer], rl[kPer], ku2[kPer], ku3[kPer], hk = 0u;
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
             const int b = kPer * t + q;
             const double lo2 = (double)f.pre[b] * iP, hi2 = (double)f.pre[b + 1] * iP;
             key2[q] = key3[q] = kF3KeyNone;
-            klo2[q] = klo3[q] = 1u;
-            khi2[q] = khi3[q] = 0u;
             ku2[q] = ku3[q] = kF3NoU;
             rl[q] = 0u;
             if (b < bH) continue;
@@ -1290,8 +1297,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                     const int e2 = f_dexp(lo2);
                     key2[q] = (uint32_t)(e2 + 256);
                     const double sc = ldexp(1.0, 23 - e2);
-                    klo2[q] = (uint32_t)fmin(floor(plo * sc), 1073741824.0);
-                    khi2[q] = (uint32_t)fmin(floor(phi * sc + 0.5), 1073741824.0);
+                    KL2[b] = (uint32_t)fmin(floor(plo * sc), 1073741824.0);
+                    const uint32_t kh = (uint32_t)fmin(floor(phi * sc + 0.5), 1073741824.0);
+                    KH2[b] = kh;
+                    hk |= kh >= 1u ? 1u << q : 0u;
                     ku2[q] = f3_uniform(pl * sc, ph * sc);
                 }
             }
@@ -1305,15 +1314,19 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 const int e3 = f_dexp(c3lo);
                 key3[q] = (uint32_t)(e3 + 256);
                 const double sc = ldexp(1.0, 23 - e3);
-                klo3[q] = (uint32_t)fmin(floor(plo * is2hi * sc), 1073741824.0);
-                khi3[q] = (uint32_t)fmin(floor(phi * is2lo * sc + 0.5), 1073741824.0);
+                KL3[b] = (uint32_t)fmin(floor(plo * is2hi * sc), 1073741824.0);
+                const uint32_t kh = (uint32_t)fmin(floor(phi * is2lo * sc + 0.5), 1073741824.0);
+                KH3[b] = kh;
+                hk |= kh >= 1u ? 16u << q : 0u;
                 ku3[q] = f3_uniform(pl * is2hi * sc, ph * is2lo * sc);
             }
         }
         F3_TS(31);
         int rid2[kPer], rid3[kPer];
-        if (!f3_plan_runs(sm, f, 0, bH, key2, klo2, khi2, rid2, 0u, (uint32_t)kF3L23)) F3_FAIL();
-        if (!f3_plan_runs(sm, f, 1, bH, key3, klo3, khi3, rid3, (uint32_t)kF3L23, (uint32_t)kF3L23)) F3_FAIL();
+        if (!f3_plan_runs(sm, f, 0, bH, key2, KL2, KH2, rid2, 0u, (uint32_t)kF3L23)) F3_FAIL();
+        F3_TS(16);
+        if (!f3_plan_runs(sm, f, 1, bH, key3, KL3, KH3, rid3, (uint32_t)kF3L23, (uint32_t)kF3L23)) F3_FAIL();
+        F3_TS(17);
         // list segments of pass 3: the bins listed for seq 2 or 3 (room for
         // the raw values of penalized ids: counted in lvl, free until pass 3)
         for (int b = t; b < kFBins; b += kThreads) f.lvl[b] = 0u;
@@ -1349,11 +1362,11 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 wv[q].x = kF3Listed | o;
                 stg(segst + b, o);
             } else {
-                if (rid2[q] >= 0 && khi2[q] >= 1u && ku2[q] == kF3NoU) {
+                if (rid2[q] >= 0 && ((hk >> q) & 1u) && ku2[q] == kF3NoU) {
                     const F3Run &R = f.run[0][rid2[q]];
                     wv[q].x = kF3In2 | ((uint32_t)(23 - R.e) << 24) | (uint32_t)(R.off + (1 << 23));
                 }
-                if (rid3[q] >= 0 && khi3[q] >= 1u && ku3[q] == kF3NoU) {
+                if (rid3[q] >= 0 && ((hk >> (4 + q)) & 1u) && ku3[q] == kF3NoU) {
                     const F3Run &R = f.run[1][rid3[q]];
                     wv[q].y = kF3W3 | ((uint32_t)(23 - R.e) << 24) | (uint32_t)(R.off + (1 << 23));
                 }
@@ -1378,6 +1391,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         for (int j = t; j <= kF3Lvl; j += kThreads) f.lvl[j] = 0u;
         __syncthreads();
+        F3_TS(18);
         // uniform bins of the runs (not listed): every element adds ku
         uint32_t nadd2 = 0, nadd3 = 0;
 #pragma unroll
