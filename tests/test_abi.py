@@ -41,7 +41,12 @@ def test_gemv_arguments_rejected_without_gpu():
     # cols not a multiple of the block size: the reference's upload returns None
     assert lib.gs_qmatrix_upload(14, blk, 1, 128, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
     assert lib.gs_qmatrix_upload(8, blk, 1, 48, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
-    assert lib.gs_qmatrix_upload(11, blk, 1, 256, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED   # Q3_K
+    for qt in (2, 3):                  # Q4_0, Q4_1: 32-weight blocks
+        assert lib.gs_qmatrix_upload(qt, blk, 1, 48, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
+    assert lib.gs_qmatrix_upload(11, blk, 1, 128, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED  # Q3_K
+    # block types the reference's upload does not take (F32, F16, Q5_0, Q5_1, Q8_1, Q2_K, Q8_K)
+    for qt in (0, 1, 6, 7, 9, 10, 15):
+        assert lib.gs_qmatrix_upload(qt, blk, 1, 256, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
     assert lib.gs_qmatrix_upload(14, blk, 1, 256 * 65, C.byref(h)) == gs_sampler.GS_ERR_UNSUPPORTED
     assert lib.gs_qmatrix_destroy(None) == gs_sampler.GS_ERR_INVALID
     assert lib.gs_gemv(None, None, 1, None, None) == gs_sampler.GS_ERR_INVALID
