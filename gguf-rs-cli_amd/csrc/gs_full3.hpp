@@ -927,8 +927,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     const double dl = 1.0 - kFDelta, dh = 1.0 + kFDelta;
 
     // ---- plan A: the running seq-1 sum before each bin, predicted from the
-    // masses (top bins) and the counts times the rounded increment of the
-    // bin's centre (the rest), refined twice --------------------------------
+    // masses (top bins) and, for the rest, the counts times the mean rounded
+    // increment over the bin's range of summands (as if the summands were
+    // spread evenly over it), refined twice --------------------------------
     {
         double osum = 0.0;
         for (int j = t; j < nover; j += kThreads) {
@@ -939,15 +940,16 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         f_block_excl_f64_buf(osum, &otot, sm.red_f64);
         osum = otot;
         uint32_t cn[kPer];
-        double mb[kPer], ctr[kPer];
+        double mb[kPer], ed[kPer + 1];      // ed[q]: the summand at bin kPer t + q's upper edge
         const double mscale = exp((double)m0 - (double)m) / (double)kFMassScale;
         double loc = 0.0;
+#pragma unroll
+        for (int q = 0; q <= kPer; q++) ed[q] = e_at((double)(kPer * t + q));
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
             const int b = kPer * t + q;
             cn[q] = f.cnt[b];
-            ctr[q] = e_at((double)b + 0.5);
-            mb[q] = b < kFMassBins ? (double)(int64_t)f.u.mass64[b] * mscale : (double)cn[q] * ctr[q];
+            mb[q] = b < kFMassBins ? (double)(int64_t)f.u.mass64[b] * mscale : (double)cn[q] * 0.5 * (ed[q] + ed[q + 1]);
             if (mb[q] < 0.0) mb[q] = 0.0;
             loc += mb[q];
         }
@@ -962,8 +964,14 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 const int b = kPer * t + q;
                 ct[q] = mb[q];
                 if (b >= kFMassBins && cn[q] && lo > 0.0) {
-                    const int ge = f_dexp(lo) - 23;      // the grid 2^ge
-                    ct[q] = (double)cn[q] * ldexp(rint(ldexp(ctr[q], -ge)), ge);
+                    // the mean of rint(u) over u in [ul, uh] (the bin's summands in
+                    // units of the grid 2^ge): (F(uh) - F(ul)) / (uh - ul) with
+                    // F(u) = (u^2 - (u - rint u)^2) / 2
+                    const int ge = f_dexp(lo) - 23;
+                    const double uh = ldexp(ed[q], -ge), ul = ldexp(ed[q + 1], -ge);
+                    const double sh = uh - rint(uh), sl = ul - rint(ul);
+                    const double mean = uh > ul ? 0.5 * (uh + ul) - 0.5 * (sh * sh - sl * sl) / (uh - ul) : rint(uh);
+                    ct[q] = (double)cn[q] * ldexp(mean, ge);
                 }
                 lo += ct[q];
                 loc += ct[q];
