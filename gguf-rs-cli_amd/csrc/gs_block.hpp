@@ -160,6 +160,29 @@ __device__ __forceinline__ uint32_t wave_scan_add(uint32_t v)
     return v;
 }
 
+// Wave64 sum of a u64, returned in every lane (the inclusive DPP scan's
+// last lane).
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_mov_u64(uint64_t v)
+{
+    return ((uint64_t)dpp_mov<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_mov<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v)
+{
+    const int lane = lane_id();
+    v += dpp_mov_u64<0x111>(v);
+    v += dpp_mov_u64<0x112>(v);
+    v += dpp_mov_u64<0x114>(v);
+    v += dpp_mov_u64<0x118>(v);
+    uint64_t o = dpp_mov_u64<0x142>(v);
+    if ((lane & 31) >= 16) v += o;
+    o = dpp_mov_u64<0x143>(v);
+    if (lane >= 32) v += o;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 // Wave64 maximum / minimum of a u32, returned in every lane.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {

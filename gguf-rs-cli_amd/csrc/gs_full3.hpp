@@ -181,16 +181,29 @@ __device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *
         ParFn fc[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) fc[c] = elem_fn(a[c], e);
-        ParFn loc = fc[0];
-#pragma unroll
-        for (int c = 1; c < 4; c++) loc = par_compose(loc, fc[c]);
-        const ParFn incl = f3_wave_scan(loc);
-        ParFn ex;
-        ex.f0 = __shfl_up(incl.f0, 1, 64);
-        ex.f1 = __shfl_up(incl.f1, 1, 64);
-        if (lane == 0) ex = ParFn{0u, 0u};
         const uint32_t P0 = (uint32_t)ldexpf(cum, 23 - e);      // cum = P0 2^(e-23), P0 < 2^24
-        const uint32_t Pst = P0 + par_apply(ex, P0 & 1u);       // the sum before this lane's first value
+        // A step with no rounding tie and no value of 2^22 grid units or
+        // more (the common case past the head) has increments that do not
+        // depend on parity: an integer wave scan gives the sums.  Otherwise
+        // the increment functions are composed.
+        bool spec = false;
+#pragma unroll
+        for (int c = 0; c < 4; c++) spec |= fc[c].f0 != fc[c].f1 || fc[c].f0 >= (1u << 22);
+        uint32_t Pst;                                             // the sum before this lane's first value
+        if (!__any(spec)) {
+            const uint32_t ks = fc[0].f0 + fc[1].f0 + fc[2].f0 + fc[3].f0;   // < 2^24: the scan stays below 2^30
+            Pst = P0 + (wave_incl_u32(ks) - ks);
+        } else {
+            ParFn loc = fc[0];
+#pragma unroll
+            for (int c = 1; c < 4; c++) loc = par_compose(loc, fc[c]);
+            const ParFn incl = f3_wave_scan(loc);
+            ParFn ex;
+            ex.f0 = __shfl_up(incl.f0, 1, 64);
+            ex.f1 = __shfl_up(incl.f1, 1, 64);
+            if (lane == 0) ex = ParFn{0u, 0u};
+            Pst = P0 + par_apply(ex, P0 & 1u);
+        }
         // per lane: the first value whose add leaves the binade (fl), the
         // first after which pred holds (fs), the sums around them
         uint32_t Pc = Pst, Plast = Pst;
@@ -293,7 +306,7 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
         }
         if (part) atomicAdd((unsigned long long *)&f.rtot[s][r], (unsigned long long)part);
     }
-    for (int d = 32; d > 0; d >>= 1) ncount += __shfl_xor(ncount, d, 64);
+    ncount = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_u32(ncount), 63);
     if (lane_id() == 0 && ncount) atomicSub(&f.lcount[s], ncount);
     for (int i = 0; i < nt; i++) {
         const F3Tie T = f.tie[s][i];
@@ -301,22 +314,23 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
         const uint32_t a0 = max(j0, (uint32_t)(R.off + (int)T.k + 1)), a1 = min(j1, R.base + R.span);
         uint64_t part = 0;
         for (uint32_t j = a0; j < a1; j++) part += (uint64_t)((int)j - R.off) * f3_lvl_get(f, j);
-        for (int d = 32; d > 0; d >>= 1) part += __shfl_xor(part, d, 64);
+        part = wave_sum_u64(part);
         if (lane_id() == 0 && part) atomicAdd((unsigned long long *)&f.tie[s][i].A, (unsigned long long)part);
     }
     __syncthreads();
     if (f.lcount[s] != 0u) f.fail = 1;    // a 16-bit counter wrapped
-    if (t == 0) {
-        for (int i = 1; i < nt; i++) {
-            const F3Tie x = f.tie[s][i];
-            int j = i - 1;
-            while (j >= 0 && (f.tie[s][j].run > x.run || (f.tie[s][j].run == x.run && f.tie[s][j].k < x.k))) {
-                f.tie[s][j + 1] = f.tie[s][j];
-                j--;
-            }
-            f.tie[s][j + 1] = x;
+    // the ties ranked by (run, k descending, index), one per thread
+    F3Tie mine;
+    uint32_t rank = 0;
+    if (t < nt) {
+        mine = f.tie[s][t];
+        for (int i = 0; i < nt; i++) {
+            const F3Tie o = f.tie[s][i];
+            rank += (o.run < mine.run || (o.run == mine.run && (o.k > mine.k || (o.k == mine.k && i < t)))) ? 1u : 0u;
         }
     }
+    __syncthreads();
+    if (t < nt) f.tie[s][rank] = mine;
     __syncthreads();
 }
 
