@@ -435,12 +435,15 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
     return 0;
 }
 
-// Table index of scaled logit y: bin b = floor(cb - y / w) (fma; the same
-// value in every pass) at 1 + b, above the bins at 0, below at kFBins + 1.
+// Table index of scaled logit y: bin b = floor(cb - y / w) at 1 + b, above
+// the bins at 0, below at kFBins + 1.  One fma (cb + 1 - y / w, the same
+// value in every pass), a clamp to [0, kFBins + 1] and a truncation, which
+// is the floor there.  (The bins' edges as f3_range gives them carry a
+// margin far above the rounding of this fma.)
 __device__ __forceinline__ int f3_tidx(float y, float cb)
 {
-    const float tb = __builtin_amdgcn_fmed3f(fmaf(y, -kFInvW, cb), -1.0f, (float)kFBins);
-    return (int)floorf(tb) + 1;
+    const float tb = __builtin_amdgcn_fmed3f(fmaf(y, -kFInvW, cb + 1.0f), 0.0f, (float)(kFBins + 1));
+    return (int)tb;
 }
 // The bin of y clamped to [0, kFBins) (for entries known to lie in a bin).
 __device__ __forceinline__ int f3_bin(float y, float cb) { return min(max(f3_tidx(y, cb) - 1, 0), kFBins - 1); }
@@ -775,6 +778,10 @@ __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD wo
     F3_STAT(sb, (clock64() - c_beg) / 100);
     F3_STAT(sb + 1, c_work / 100);
     F3_STAT(sb + 2, n_fl);
+    if (lane == 0 && blockIdx.x < 1024) {
+        atomicMax(&g_v3diag[blockIdx.x * 32 + (QN == 256 ? 16 : 17)], (int)((clock64() - c_beg) / 100));
+        atomicMax(&g_v3diag[blockIdx.x * 32 + (QN == 256 ? 18 : 19)], (int)n_fl);
+    }
 #endif
 }
 
