@@ -25,8 +25,8 @@ struct RowArgs {
     uint64_t lcg_state;            // used when u == null: row b draws jump(state, b)
     uint32_t *tokens;
     int32_t *status;
-    int32_t *fb;                   // per row: 1 = binned path failed, use the sort path
-    uint32_t *scratch;             // full-vocabulary path: 4*V u32 per row
+    int32_t *fb;                   // per row: 1 = the increment histogram failed, a fallback form finished the row
+    uint32_t *scratch;             // full-vocabulary paths: scratch_stride u32 per row
     size_t scratch_stride;         // u32 elements per row
     uint64_t *done;                // optional (single-row calls, B = 1): receives
     uint32_t done_val;             // (done_val << 32) | (status & 0xff) << 24 | token in one store,
@@ -73,7 +73,8 @@ inline size_t scratch_u32_per_row(size_t V)
 
 // The row kernels of a batch: the small-path rows (and, when a.chunked is
 // set, the chunked rows' virtual rows), then the full-vocabulary rows by the
-// exact binned path and, for rows whose checks failed, by the sort path.
+// increment-histogram path and, for rows whose checks failed, by its
+// fallback forms in the same workgroup.
 hipError_t launch_sample_rows(const RowArgs &a, int B, hipStream_t st);
 // The same for a batch with per-row params (rows of both kinds): the small
 // rows run on `side` beside the full-vocabulary rows on st (fork / join by

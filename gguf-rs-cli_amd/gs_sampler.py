@@ -231,8 +231,8 @@ class Sampler:
         _check(self._lib.gs_sampler_set_params(self._h, ctypes.byref(self.params)), "set_params")
 
     def fallback_rows(self, stream=None):
-        """Rows of the last full-vocabulary call finished by the sort-based
-        path instead of the binned one (waits for the stream)."""
+        """Rows of the last full-vocabulary call finished by the fallback
+        forms instead of the increment-histogram path (waits for the stream)."""
         n = ctypes.c_size_t()
         _check(self._lib.gs_sampler_fallback_rows(self._h, _stream_handle(stream), ctypes.byref(n)), "fallback_rows")
         return n.value

@@ -65,9 +65,10 @@ int gs_sampler_set_params(gs_sampler *s, const gs_params *params);
 int gs_sampler_get_params(const gs_sampler *s, gs_params *params);
 /* Diagnostic, no counterpart in the reference: how many rows of this
  * sampler's last sampling call on the full-vocabulary path (top_k = 0 or
- * beyond the small-k limit) were finished by the exact sort-based path
- * instead of the binned one (same tokens, slower).  Waits for `stream`, the
- * stream that call ran on; 0 if the last call did not use that path. */
+ * beyond the small-k limit) were not finished by the increment-histogram
+ * path but by its fallbacks (the first binned form, then the sort; same
+ * tokens, slower).  Waits for `stream`, the stream that call ran on; 0 if
+ * the last call did not use that path. */
 int gs_sampler_fallback_rows(gs_sampler *s, void *stream, size_t *n);
 /* set_seed (src/sampler.rs:5) for this sampler's stream. */
 int gs_sampler_set_seed(gs_sampler *s, uint64_t seed);
