@@ -394,6 +394,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
         const bool at = lim && lim_arr == 0u;
         if (at) end = lim_pos + 1u;
         const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 64u);
+        F_TS(8 + 8 * (roff == 0u ? 0 : s + 1));
         if (s == 1) F3_TS(16 + 5 * s);
         *cum_out = cum;
         if (p < end) { *arr = 0u; *pos = p; return 1; }
@@ -410,6 +411,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
             const bool at = lim && lim_arr == 1u && lim_pos >= beg && lim_pos < end;
             if (at) end = lim_pos + 1u;
             const uint32_t p = f3_chain(st, roff + beg, roff + end, &cum, pred);
+            F_TS(9 + 8 * (roff == 0u ? 0 : s + 1) + min(g, 6));
             if (s == 1) F3_TS(17 + 5 * s + min(g, 3));
             *cum_out = cum;
             if (p < roff + end) { *arr = 1u; *pos = p - roff; return 1; }
@@ -469,16 +471,16 @@ template <class CE>
 __device__ void f3_sort_list(Full3Smem &f, const uint64_t *lst, uint32_t n, uint32_t nover,
                              const uint32_t *segst, CE cend, uint64_t *se, float *sa, uint32_t *stage, uint32_t scap)
 {
-    // the entries' high words (the value keys) staged in LDS when they fit:
-    // a rank counts the higher keys there, and only an element whose key
-    // another entry of its segment shares compares the full entries
-    const bool staged = n <= scap;
-    if (staged) {
-        for (uint32_t j = threadIdx.x; j < n; j += kThreads) stage[j] = (uint32_t)(ldg(lst + j) >> 32);
-        __syncthreads();
-    }
+    // The last scap / 2 entries (the deep-tail window segments, which are
+    // the large ones) are staged in LDS: a rank there costs one 64-bit
+    // compare per entry of the segment.  Segments that start before them
+    // rank from the list in global memory.
+    uint64_t *stage64 = reinterpret_cast<uint64_t *>(stage);
+    const uint32_t s0 = n > scap / 2u ? n - scap / 2u : 0u;
+    for (uint32_t j = s0 + threadIdx.x; j < n; j += kThreads) stage64[j - s0] = ldg(lst + j);
+    __syncthreads();
     for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
-        const uint64_t en = ldg(lst + j);
+        const uint64_t en = j >= s0 ? stage64[j - s0] : ldg(lst + j);
         const float y = f_entry_y(en);
         uint32_t st = 0, end = nover;
         if (j >= nover) {
@@ -490,39 +492,26 @@ __device__ void f3_sort_list(Full3Smem &f, const uint64_t *lst, uint32_t n, uint
         if (!(st <= j && j < end && end <= n)) { f.fail = 1; continue; }
         uint32_t rank = 0;
         uint32_t q = st;
-        bool full = !staged;
-        if (staged) {
-            const uint32_t hi = (uint32_t)(en >> 32);
-            uint32_t eq = 0;
+        if (st >= s0) {
+            const uint64_t *sg = stage64 - s0;
             for (; q + 8 <= end; q += 8) {
-                uint32_t k8[8];
+                uint64_t e8[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) k8[u] = stage[q + u];
+                for (int u = 0; u < 8; u++) e8[u] = sg[q + u];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    rank += k8[u] > hi ? 1u : 0u;
-                    eq += k8[u] == hi ? 1u : 0u;
-                }
+                for (int u = 0; u < 8; u++) rank += e8[u] > en ? 1u : 0u;
             }
-            for (; q < end; q++) {
-                const uint32_t k = stage[q];
-                rank += k > hi ? 1u : 0u;
-                eq += k == hi ? 1u : 0u;
+            for (; q < end; q++) rank += sg[q] > en ? 1u : 0u;
+        } else {
+            for (; q + 8 <= end; q += 8) {
+                uint64_t e8[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) e8[u] = ldg(lst + q + u);
+#pragma unroll
+                for (int u = 0; u < 8; u++) rank += e8[u] > en ? 1u : 0u;
             }
-            if (eq > 1u) {
-                full = true;
-                rank = 0;
-                q = st;
-            }
+            for (; q < end; q++) rank += ldg(lst + q) > en ? 1u : 0u;
         }
-        for (; full && q + 8 <= end; q += 8) {
-            uint64_t e8[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) e8[u] = ldg(lst + q + u);
-#pragma unroll
-            for (int u = 0; u < 8; u++) rank += e8[u] > en ? 1u : 0u;
-        }
-        for (; full && q < end; q++) rank += ldg(lst + q) > en ? 1u : 0u;
         if (st + rank >= end) { f.fail = 1; continue; }
         stg(se + st + rank, en);
         stg(sa + st + rank, f3_live(en) ? glibc_expf_tab(y - f.m, f.exptab) : 0.0f);
@@ -687,14 +676,16 @@ __device__ __forceinline__ F3K23 f3_k23(uint2 w, float y, float m, float cS, flo
 }
 
 // A pass over the row with the elements that need work compacted per wave.
-// Each thread holds 4 kUnroll elements (kUnroll float4 loads in flight); their
-// role words are read together (word), those that ask for work (act) are
+// A wave takes the row in chunks of 64 kUnroll float4s (*ctr: the next free
+// chunk); each lane holds 4 kUnroll elements of a chunk; their role words are
+// read together (word), those that ask for work (act) are
 // appended to the wave's ring in LDS (q, QN entries of (y, index)), and each
 // time 64 have gathered every lane of the wave processes one (work).  An
 // element of a bin without work costs its bin lookup only.  The 0-3 elements
 // before the 16-byte boundary and the ragged end go to work directly.
 template <int QN, bool NT, class YF, class WORD, class ACT, class WORK>
-__device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD word, ACT act, WORK work, uint2 *q)
+__device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD word, ACT act, WORK work, uint2 *q,
+                                         uint32_t *ctr)
 {
     static_assert(QN >= 128 && (QN & (QN - 1)) == 0, "ring");
     const int t = threadIdx.x, lane = lane_id();
@@ -707,26 +698,41 @@ __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD wo
     uint64_t c_work = 0, n_fl = 0;
     const uint64_t c_beg = clock64();
 #endif
-    // software-pipelined: the next round's loads are in flight while this
-    // round's words are looked up and its active elements processed
+    // Chunks of kCh float4s, one wave's round: wave w takes chunks w and
+    // kWaves + w, then the next free one from *ctr (2 kWaves before the
+    // pass), so waves that the SIMDs issue more often take more chunks and
+    // the pass ends when the work does, not when the least favoured wave
+    // finishes an equal share.  Each wave's chunk numbers only grow.  The
+    // next chunk's loads are in flight while this one's words are looked up
+    // and its active elements processed.
+    constexpr int kCh = 64 * kUnroll;
+    const int nch = (n4 + kCh - 1) / kCh;
+    auto grab = [&]() {
+        uint32_t c = 0u;
+        if (lane == 0) c = atomicAdd(ctr, 1u);
+        return __builtin_amdgcn_readfirstlane((int)c);
+    };
     float4 nv[kUnroll];
+    auto load = [&](int c) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) nv[u] = NT ? ldg_nt(r4 + min(u * kThreads + t, n4 - 1)) : ldg(r4 + min(u * kThreads + t, n4 - 1));
-    for (int base = 0; base < n4; base += kThreads * kUnroll) {
+        for (int u = 0; u < kUnroll; u++) {
+            const float4 *pa = r4 + min(c * kCh + u * 64 + lane, n4 - 1);
+            nv[u] = NT ? ldg_nt(pa) : ldg(pa);
+        }
+    };
+    int cur = wave_id(), nxt = kWaves + wave_id();
+    if (cur < nch) load(cur);
+    while (cur < nch) {
         float4 v[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) v[u] = nv[u];
-        if (base + kThreads * kUnroll < n4) {
-#pragma unroll
-            for (int u = 0; u < kUnroll; u++) {
-                const float4 *pa = r4 + min(base + kThreads * kUnroll + u * kThreads + t, n4 - 1);
-                nv[u] = NT ? ldg_nt(pa) : ldg(pa);
-            }
-        }
+        if (nxt < nch) load(nxt);
+        const int nn = grab();
+        const int base = cur * kCh + lane;
         float y[kE];
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
-            const bool in = base + u * kThreads + t < n4;
+            const bool in = base + u * 64 < n4;
             y[4 * u + 0] = in ? yf(v[u].x) : -INFINITY;
             y[4 * u + 1] = in ? yf(v[u].y) : -INFINITY;
             y[4 * u + 2] = in ? yf(v[u].z) : -INFINITY;
@@ -744,7 +750,7 @@ __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD wo
                     __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
                 if (a)
                     q[(qt + off) & (QN - 1)] =
-                        make_uint2(__float_as_uint(y[e]), (uint32_t)(h0 + 4 * (base + (e >> 2) * kThreads + t) + (e & 3)));
+                        make_uint2(__float_as_uint(y[e]), (uint32_t)(h0 + 4 * (base + (e >> 2) * 64) + (e & 3)));
                 qt += (uint32_t)__popcll(bm);
                 if (qt - qh >= 64u) {
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -764,6 +770,8 @@ __device__ __forceinline__ void f3_qpass(const float *row, int V, YF yf, WORD wo
                 }
             }
         }
+        cur = nxt;
+        nxt = nn;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -822,7 +830,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     for (int b = t; b < kFBins; b += kThreads) f.cnt[b] = 0u;
     for (int b = t; b < kFMassBins; b += kThreads) f.u.mass64[b] = 0ull;
     if (t < 32) f.exptab[t] = kExp2Tab[t];
-    if (t == 0) { f.nover = 0; f.fail = 0; f.namb = 0; f.ndef = 0; f.ntie[0] = 0; f.ntie[1] = 0; }
+    if (t == 0) {
+        f.nover = 0; f.fail = 0; f.namb = 0; f.ndef = 0; f.ntie[0] = 0; f.ntie[1] = 0;
+        f.qctr[0] = f.qctr[1] = 2u * kWaves;
+    }
 
     // ---- pass 1 (HBM): counts, masses of the top bins, max, NaN -------------
     // Bins are of t = cb - y / w, cb = (m0 + 3) / w, m0 the maximum of the
@@ -960,6 +971,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         double otot;
         f_block_excl_f64_buf(osum, &otot, sm.red_f64);
         osum = otot;
+        F_TS(40);
         uint32_t cn[kPer];
         double mb[kPer], ed[kPer + 1];      // ed[q]: the summand at bin kPer t + q's upper edge
         const double mscale = exp((double)m0 - (double)m) / (double)kFMassScale;
@@ -976,6 +988,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         double tot;
         double pre = f_block_excl_f64_buf(loc, &tot, sm.red_f64b) + osum;
+        F_TS(41);
         double ct[kPer];
         for (int round = 0; round < 2; round++) {
             double lo = pre;
@@ -998,6 +1011,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 loc += ct[q];
             }
             pre = f_block_excl_f64_buf(loc, &tot, round == 0 ? sm.red_f64 : sm.red_f64b) + osum;
+            F_TS(42 + round);
         }
         double lo = pre;
 #pragma unroll
@@ -1096,6 +1110,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         uint32_t ltot;
         uint32_t o = block_excl_u32(capl, &ltot, sm) + (uint32_t)nover;   // (its barriers: w read)
+        F_TS(44);
         uint32_t wv[kPer];
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
@@ -1125,6 +1140,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         for (int j = t; j <= kF3Lvl; j += kThreads) f.lvl[j] = 0u;
         __syncthreads();
+        F_TS(45);
         // uniform bins: every element adds ku (the count is exact)
         uint32_t nadd = 0;
 #pragma unroll
@@ -1183,8 +1199,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         };
         auto act = [](uint32_t w) { return w != 0u; };
         uint2 *ring = reinterpret_cast<uint2 *>(f.u.w23) + 256 * wave_id();
-        if (t_one) f3_qpass<256, false>(row, V, [](float x) { return x; }, word, act, one, ring);
-        else f3_qpass<256, false>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
+        if (t_one) f3_qpass<256, false>(row, V, [](float x) { return x; }, word, act, one, ring, &f.qctr[0]);
+        else f3_qpass<256, false>(row, V, [&](float x) { return x / T; }, word, act, one, ring, &f.qctr[0]);
         __syncthreads();
         if (has_pen) {
             // the raw values of penalized ids leave (the pass marked their
@@ -1280,6 +1296,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             }
         }
         __syncthreads();
+        F_TS(46);
         double s2lo = 1.0, s2hi = 1.0;
         if (nuc) {
             const int bc = f.nreg;
@@ -1292,6 +1309,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             s2lo = (double)top_p;
             s2hi = (double)__double2float_ru(tp + vmax + ldexp(tp, -22));
         }
+        F_TS(47);
         cS = (float)iS;
         cS3lo = __double2float_rd(iS / s2hi);
         band3 = (float)((double)kF3Band23 * 2.0 + (s2hi / s2lo - 1.0));
@@ -1377,7 +1395,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             capl += capv[q];
         }
         uint32_t ltot;
+        F_TS(48);
         uint32_t o = block_excl_u32(capl, &ltot, sm);
+        F_TS(49);
         uint2 wv[kPer];
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
@@ -1492,8 +1512,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         };
         auto act = [](uint2 w) { return (w.x | w.y) != 0u; };
         uint2 *ring = reinterpret_cast<uint2 *>(f.pre) + 128 * wave_id();
-        if (t_one) f3_qpass<128, true>(row, V, [](float x) { return x; }, word, act, one, ring);
-        else f3_qpass<128, true>(row, V, [&](float x) { return x / T; }, word, act, one, ring);
+        if (t_one) f3_qpass<128, true>(row, V, [](float x) { return x; }, word, act, one, ring, &f.qctr[1]);
+        else f3_qpass<128, true>(row, V, [&](float x) { return x / T; }, word, act, one, ring, &f.qctr[1]);
         __syncthreads();
         F3_TS(10);
         if (has_pen) {
@@ -1524,6 +1544,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         f3_lcount(f, 0, nok2);
         f3_lcount(f, 1, nok3);
+        F_TS(0);
         F3_STAT(7, f.list_end);
         F3_STAT(8, f.ndef);
         F3_STAT(9, f.namb);
@@ -1546,8 +1567,10 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const float p = glibc_expf_tab(y - m, f.exptab) / S;
             f3_count_exact(f, 0, rr, ldexpf(p, 23 - f.run[0][rr].e));
         }
+        F_TS(1);
         __threadfence_block();
         __syncthreads();
+        F_TS(2);
         if (nuc) {
             for (uint32_t j = t; j < f.list_end; j += kThreads) {
                 const uint64_t en = ldg(se3 + j);
@@ -1559,6 +1582,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 f3_count_exact(f, 0, rr, ldexpf(p, 23 - f.run[0][rr].e));
             }
         }
+        F_TS(3);
         __syncthreads();
         if (f.fail || f.ntie[0] > kF3Ties) F3_FAIL();
     }

@@ -130,6 +130,7 @@ struct Full3Smem {
     float m0, m, S, s2, s2lo, s2hi, cb;
     int nover, fail, namb, ndef, bH, walk_res;
     uint32_t headend, list_end, cut_arr, cut_pos, tok_pos, tok_arr, list2;
+    uint32_t qctr[2];          // passes 2 and 3: the next free chunk of the row
 };
 
 } // namespace gs
