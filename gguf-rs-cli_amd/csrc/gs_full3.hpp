@@ -122,6 +122,35 @@ __device__ __forceinline__ ParFn f3_wave_scan(ParFn v)
     return v;
 }
 
+// Stop conditions of a walk (monotone in the sum).  thr(e): the smallest
+// sum P 2^(e-23) (P an integer, in units of the grid 2^(e-23)) for which
+// the condition holds, as P, or at least 2^25 if it holds for none below
+// 2^24 units.  A multiple of the grid with P < 2^24 is an exact float and
+// v 2^(23-e) is exact (a power-of-two scaling), so P >= thr(e) is the
+// condition itself.
+struct F3Never {
+    __device__ bool operator()(float) const { return false; }
+    __device__ uint32_t thr(int) const { return kSat; }
+};
+struct F3AtLeast {      // cum >= v
+    float v;
+    __device__ bool operator()(float cc) const { return cc >= v; }
+    __device__ uint32_t thr(int e) const
+    {
+        const float q = ceilf(ldexpf(v, 23 - e));
+        return q < (float)kSat ? (uint32_t)fmaxf(q, 0.0f) : kSat;
+    }
+};
+struct F3Above {        // v < cum
+    float v;
+    __device__ bool operator()(float cc) const { return v < cc; }
+    __device__ uint32_t thr(int e) const
+    {
+        const float q = floorf(ldexpf(v, 23 - e)) + 1.0f;
+        return q < (float)kSat ? (uint32_t)fmaxf(q, 0.0f) : kSat;
+    }
+};
+
 // Exact sequential f32 adds cum = RN(cum + v[j]) over LDS values v[beg, end)
 // on one wave (every lane calls with the same arguments), stopping at the
 // first j after which pred(cum) holds (pred is monotone: the sums only
@@ -137,7 +166,8 @@ __device__ __forceinline__ ParFn f3_wave_scan(ParFn v)
 // same chain, reading broadcasts): the sum crosses binades often while it is
 // small (at the head of the row), and each crossing would cost a step.
 template <class P>
-__device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *cum_io, P pred, uint32_t nseq = 0)
+__device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *cum_io, P pred, uint32_t nseq = 0,
+                            int diag = -1)
 {
     const int lane = lane_id();
     float cum = *cum_io;
@@ -173,27 +203,44 @@ __device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *
         }
     }
     while (j0 < end) {
+#ifdef GS_TIMING
+        if (diag >= 0 && lane == 0 && blockIdx.x < 256) g_vt[blockIdx.x * 64 + 56 + diag]++;
+#endif
         const uint32_t jl = j0 + 4u * (uint32_t)lane;
+        // this lane's live values: [jl, jl + nl); the reads past them stay
+        // inside the workgroup's LDS and are replaced by 0
+        const uint32_t nl = jl < end ? min(end - jl, 4u) : 0u;
         float a[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) a[c] = jl + c < end ? v[jl + c] : 0.0f;
+        for (int c = 0; c < 4; c++) {
+            const float x = v[jl + c];
+            a[c] = (uint32_t)c < nl ? x : 0.0f;
+        }
         const int e = grid_exp(cum);
-        ParFn fc[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) fc[c] = elem_fn(a[c], e);
         const uint32_t P0 = (uint32_t)ldexpf(cum, 23 - e);      // cum = P0 2^(e-23), P0 < 2^24
-        // A step with no rounding tie and no value of 2^22 grid units or
-        // more (the common case past the head) has increments that do not
-        // depend on parity: an integer wave scan gives the sums.  Otherwise
-        // the increment functions are composed.
+        // The common step (no rounding tie, no value of 2^22 grid units or
+        // more) adds k = rint(a 2^(23-e)) per value whatever the parities:
+        // an integer wave scan gives the sums.  Otherwise each value's
+        // increment is a function of the parity before it (elem_fn) and the
+        // functions are composed.
+        uint32_t k[4];
         bool spec = false;
 #pragma unroll
-        for (int c = 0; c < 4; c++) spec |= fc[c].f0 != fc[c].f1 || fc[c].f0 >= (1u << 22);
-        uint32_t Pst;                                             // the sum before this lane's first value
+        for (int c = 0; c < 4; c++) {
+            const float m = ldexpf(a[c], 23 - e);
+            spec |= !(m < 4194304.0f) || m - floorf(m) == 0.5f;
+            k[c] = (uint32_t)rintf(m);
+        }
+        uint32_t Pc[5];                                           // the sums before value c, and after the last
         if (!__any(spec)) {
-            const uint32_t ks = fc[0].f0 + fc[1].f0 + fc[2].f0 + fc[3].f0;   // < 2^24: the scan stays below 2^30
-            Pst = P0 + (wave_incl_u32(ks) - ks);
+            const uint32_t ks = k[0] + k[1] + k[2] + k[3];        // < 2^24: the scan stays below 2^30
+            Pc[0] = P0 + (wave_incl_u32(ks) - ks);
+#pragma unroll
+            for (int c = 0; c < 4; c++) Pc[c + 1] = Pc[c] + k[c];
         } else {
+            ParFn fc[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) fc[c] = elem_fn(a[c], e);
             ParFn loc = fc[0];
 #pragma unroll
             for (int c = 1; c < 4; c++) loc = par_compose(loc, fc[c]);
@@ -202,40 +249,44 @@ __device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *
             ex.f0 = __shfl_up(incl.f0, 1, 64);
             ex.f1 = __shfl_up(incl.f1, 1, 64);
             if (lane == 0) ex = ParFn{0u, 0u};
-            Pst = P0 + par_apply(ex, P0 & 1u);
-        }
-        // per lane: the first value whose add leaves the binade (fl), the
-        // first after which pred holds (fs), the sums around them
-        uint32_t Pc = Pst, Plast = Pst;
-        int fl = 4, fs = 4;
-        uint32_t Pbef = Pst, Pstop = 0u;
+            Pc[0] = P0 + par_apply(ex, P0 & 1u);
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t Pn = Pc + par_apply(fc[c], Pc & 1u);
-            const bool live = jl + c < end;
-            if (fl == 4 && fs == 4) {
-                if (live && (Pc >= (1u << 24) || Pn >= (1u << 24))) { fl = c; Pbef = Pc; }
-                else if (live && pred(ldexpf((float)Pn, e - 23))) { fs = c; Pstop = Pn; }
-            }
-            if (live) Plast = Pn;
-            Pc = Pn;
+            for (int c = 0; c < 4; c++) Pc[c + 1] = Pc[c] + par_apply(fc[c], Pc[c] & 1u);
         }
-        const uint64_t bl = __ballot(fl < 4), bs = __ballot(fs < 4);
+        // per lane: the first live value whose add leaves the binade (a sum
+        // of 2^24 grid units or more) or after which pred holds (a sum of
+        // pred.thr(e) units or more; the sums only grow, so each event is a
+        // threshold on the sums after the values)
+        const uint32_t lim = min(pred.thr(e), 1u << 24);
+        uint32_t cev = 0;
+#pragma unroll
+        for (int c = 1; c <= 4; c++) cev += Pc[c] < lim ? 1u : 0u;
+        const bool ev = cev < nl;
+        uint32_t Pb = Pc[0], Pa = Pc[1], Pl = Pc[0];
+#pragma unroll
+        for (int c = 1; c < 4; c++) {
+            Pb = cev == (uint32_t)c ? Pc[c] : Pb;
+            Pa = cev == (uint32_t)c ? Pc[c + 1] : Pa;
+        }
+#pragma unroll
+        for (int c = 1; c <= 4; c++) Pl = nl == (uint32_t)c ? Pc[c] : Pl;
+        const bool cross = Pa >= (1u << 24);
+        const uint64_t bl = __ballot(ev && cross), bs = __ballot(ev && !cross);
         const int Ll = bl ? (int)__builtin_ctzll(bl) : 64;
         const int Ls = bs ? (int)__builtin_ctzll(bs) : 64;
         if (Ls < Ll) {
-            const int c = __builtin_amdgcn_readlane(fs, Ls);
-            *cum_io = ldexpf((float)(uint32_t)__builtin_amdgcn_readlane((int)Pstop, Ls), e - 23);
+            const int c = __builtin_amdgcn_readlane((int)cev, Ls);
+            *cum_io = ldexpf((float)(uint32_t)__builtin_amdgcn_readlane((int)Pa, Ls), e - 23);
             return j0 + 4u * (uint32_t)Ls + (uint32_t)c;
         }
         if (Ll == 64) {
             const int last = (int)min(end - j0, 256u) - 1;
-            cum = ldexpf((float)(uint32_t)__builtin_amdgcn_readlane((int)Plast, last >> 2), e - 23);
+            cum = ldexpf((float)(uint32_t)__builtin_amdgcn_readlane((int)Pl, last >> 2), e - 23);
             j0 += 256u;
             continue;
         }
-        const int c = __builtin_amdgcn_readlane(fl, Ll);
-        const uint32_t pb = (uint32_t)__builtin_amdgcn_readlane((int)Pbef, Ll);
+        const int c = __builtin_amdgcn_readlane((int)cev, Ll);
+        const uint32_t pb = (uint32_t)__builtin_amdgcn_readlane((int)Pb, Ll);
         const float before = pb >= (1u << 24) ? cum : ldexpf((float)pb, e - 23);
         const uint32_t p = j0 + 4u * (uint32_t)Ll + (uint32_t)c;
         const float after = before + v[p];
@@ -393,7 +444,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
         uint32_t end = f.headend;
         const bool at = lim && lim_arr == 0u;
         if (at) end = lim_pos + 1u;
-        const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 64u);
+        const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 64u, roff == 0u ? 0 : s + 1);
         F_TS(8 + 8 * (roff == 0u ? 0 : s + 1));
         if (s == 1) F3_TS(16 + 5 * s);
         *cum_out = cum;
@@ -410,8 +461,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
             uint32_t end = cend(b1);
             const bool at = lim && lim_arr == 1u && lim_pos >= beg && lim_pos < end;
             if (at) end = lim_pos + 1u;
-            const uint32_t p = f3_chain(st, roff + beg, roff + end, &cum, pred);
-            F_TS(9 + 8 * (roff == 0u ? 0 : s + 1) + min(g, 6));
+            const uint32_t p = f3_chain(st, roff + beg, roff + end, &cum, pred, 0u, 3 + (roff == 0u ? 0 : s + 1));
             if (s == 1) F3_TS(17 + 5 * s + min(g, 3));
             *cum_out = cum;
             if (p < roff + end) { *arr = 1u; *pos = p - roff; return 1; }
@@ -421,6 +471,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
             *cum_out = cum;
             if (pred(cum)) return -1;
         }
+        F_TS(9 + 8 * (roff == 0u ? 0 : s + 1) + min(g, 6));
 #ifdef GS_TIMING
         {
             // the predicted sums' relative error at region ends (2^-30 units)
@@ -1266,7 +1317,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         float S;
         uint32_t arr, pos;
         const int res = f3_walk(f, stg_lds, 0u, 0, segst, [&](uint32_t b) { return f.w[1 + b] & kF3Cur; },
-                                [](float) { return false; }, false, 0u, 0u, &S, &arr, &pos);
+                                F3Never{}, false, 0u, 0u, &S, &arr, &pos);
         if (lane_id() == 0) { f.S = S; f.walk_res = res; }
     }
     __syncthreads();
@@ -1608,9 +1659,19 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         if (wave_id() == 0) {
             float c;
             uint32_t arr = 0u, pos = 0u;
-            const int res = f3_walk(f, stg_lds, headend, 0, segst, cend3, [top_p](float cc) { return cc >= top_p; },
+#ifdef GS_WALKTWICE
+            for (int rep = 0; rep < 2; rep++) {
+                if (rep == 1) F_TS(50);
+#endif
+            const int res = f3_walk(f, stg_lds, headend, 0, segst, cend3, F3AtLeast{top_p},
                                     false, 0u, 0u, &c, &arr, &pos);
+#ifdef GS_WALKTWICE
+            if (rep == 0) continue;
+#endif
             if (lane_id() == 0) { f.s2 = c; f.walk_res = res; f.cut_arr = arr; f.cut_pos = pos; }
+#ifdef GS_WALKTWICE
+            }
+#endif
         }
         __syncthreads();
         F3_STAT(14, f.walk_res);
@@ -1665,7 +1726,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         if (wave_id() == 0) {
             float c;
             uint32_t arr = 0u, pos = 0u;
-            const int res = f3_walk(f, stg_lds, headend, 1, segst, cend3, [r](float cc) { return r < cc; }, nuc,
+            const int res = f3_walk(f, stg_lds, headend, 1, segst, cend3, F3Above{r}, nuc,
                                     cut_arr, cut_pos, &c, &arr, &pos);
             if (lane_id() == 0) {
                 f.walk_res = res;
