@@ -333,9 +333,7 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
     const int t = threadIdx.x;
     const int nrun = f.nrun[s], nt = f.ntie[s];
     const uint32_t ltot = f.ltot[s];
-    if (t < nrun) f.rtot[s][t] = 0ull;
-    if (t < nt) f.tie[s][t].A = 0ull;
-    __syncthreads();
+    // (rtot[s] was cleared by the run planner, a tie's A when it was made)
     const uint32_t lb = s ? (uint32_t)kF3L23 : 0u;
     const uint32_t per = (ltot + kThreads - 1) / kThreads;
     const uint32_t j0 = lb + min((uint32_t)t * per, ltot), j1 = min(j0 + per, lb + ltot);
@@ -357,6 +355,7 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
         }
         if (part) atomicAdd((unsigned long long *)&f.rtot[s][r], (unsigned long long)part);
     }
+    F_TS(50 + 3 * s);
     ncount = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_u32(ncount), 63);
     if (lane_id() == 0 && ncount) atomicSub(&f.lcount[s], ncount);
     for (int i = 0; i < nt; i++) {
@@ -368,8 +367,11 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
         part = wave_sum_u64(part);
         if (lane_id() == 0 && part) atomicAdd((unsigned long long *)&f.tie[s][i].A, (unsigned long long)part);
     }
+    F_TS(51 + 3 * s);
     __syncthreads();
     if (f.lcount[s] != 0u) f.fail = 1;    // a 16-bit counter wrapped
+    if (t == 0 && blockIdx.x < 256) F_TS_VAL(62 + s, nt);
+    if (nt < 2) return;
     // the ties ranked by (run, k descending, index), one per thread
     F3Tie mine;
     uint32_t rank = 0;
@@ -665,6 +667,7 @@ __device__ bool f3_plan_runs(RowSmem &sm, Full3Smem &f, int s, int bH, const uin
         // (the role words hold off + 2^23 in 24 bits)
         const bool big = t < (int)tot && f.run[s][t].klo > (1u << 22);
         if (t == 63) { f.nrun[s] = (int)tot; f.ltot[s] = incl; }
+        f.rtot[s][t] = 0ull;
         if (__any(big) && lane_id() == 0) f.ltot[s] = lcap + 1u;
     }
     __syncthreads();
@@ -1322,6 +1325,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     }
     __syncthreads();
     const float S = f.S;
+    F3_STAT(30, __float_as_int(S));
+    F3_STAT(31, __float_as_int(f.pre[kFBins]));
     if (f.walk_res != 0 || !(S > 0.0f) || !isfinite(S)) F3_FAIL();
     F3_TS(5);
 
@@ -1645,11 +1650,14 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     const uint32_t headend = f.headend, nl3 = f.list_end;
     auto cend3 = [&](uint32_t b) { return f.u.w23[1 + b].x & kF3Cur; };
     if (nuc) {
+        // the summands of seq 2 are staged in cnt and w (free since plan B
+        // and walk S; contiguous), the seq-3 levels stay in lvl
+        float *stg2 = reinterpret_cast<float *>(f.cnt);
+        if (headend + nl3 > (uint32_t)(kFBins + kF3Tab)) F3_FAIL();
         f3_totals(sm, f, 0);
         F3_TS(12);
-        if (headend + nl3 > (uint32_t)kF3L23 / 2u) F3_FAIL();   // (the words of the seq-2 levels)
-        for (uint32_t j = t; j < headend; j += kThreads) stg_lds[j] = ldg(sa1 + j) / S;
-        for (uint32_t j = t; j < nl3; j += kThreads) stg_lds[headend + j] = ldg(sa3 + j) / S;
+        for (uint32_t j = t; j < headend; j += kThreads) stg2[j] = ldg(sa1 + j) / S;
+        for (uint32_t j = t; j < nl3; j += kThreads) stg2[headend + j] = ldg(sa3 + j) / S;
         if (!f3_regions(sm, f, bH, segst, [&](int b) {
                 const uint32_t rw = ldg(role + b);
                 return (rw & kF3L2Bit) ? kF3KeyListed : (rw & kF3In2) ? ((rw >> 8) & 63u) : kF3KeyNone;
@@ -1663,7 +1671,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             for (int rep = 0; rep < 2; rep++) {
                 if (rep == 1) F_TS(50);
 #endif
-            const int res = f3_walk(f, stg_lds, headend, 0, segst, cend3, F3AtLeast{top_p},
+            const int res = f3_walk(f, stg2, headend, 0, segst, cend3, F3AtLeast{top_p},
                                     false, 0u, 0u, &c, &arr, &pos);
 #ifdef GS_WALKTWICE
             if (rep == 0) continue;

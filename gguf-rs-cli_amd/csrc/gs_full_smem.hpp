@@ -1,5 +1,6 @@
 // gs_full_smem.hpp -- LDS layout of the exact full-vocabulary path (gs_full.hpp).
 #pragma once
+#include <stddef.h>
 #include <stdint.h>
 #include "gs_block.hpp"
 
@@ -132,5 +133,7 @@ struct Full3Smem {
     uint32_t headend, list_end, cut_arr, cut_pos, tok_pos, tok_arr, list2;
     uint32_t qctr[2];          // passes 2 and 3: the next free chunk of the row
 };
+// walk 2 stages its summands over cnt and w as one array
+static_assert(offsetof(Full3Smem, w) == offsetof(Full3Smem, cnt) + sizeof(uint32_t) * kFBins, "cnt, w adjacent");
 
 } // namespace gs
