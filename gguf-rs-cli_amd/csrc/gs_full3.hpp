@@ -1015,7 +1015,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
     // ---- plan A: the running seq-1 sum before each bin, predicted from the
     // masses (top bins) and, for the rest, the counts times the mean rounded
     // increment over the bin's range of summands (as if the summands were
-    // spread evenly over it), refined twice --------------------------------
+    // spread evenly over it), refined once ---------------------------------
     {
         double osum = 0.0;
         for (int j = t; j < nover; j += kThreads) {
@@ -1043,8 +1043,11 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         double tot;
         double pre = f_block_excl_f64_buf(loc, &tot, sm.red_f64b) + osum;
         F_TS(41);
+        // one refinement: a second one (with the refined sums' grids) left
+        // the largest error of the predicted sums at the region ends, and
+        // the rows that take this path, unchanged on C3 and C4
         double ct[kPer];
-        for (int round = 0; round < 2; round++) {
+        {
             double lo = pre;
             loc = 0.0;
 #pragma unroll
@@ -1064,8 +1067,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 lo += ct[q];
                 loc += ct[q];
             }
-            pre = f_block_excl_f64_buf(loc, &tot, round == 0 ? sm.red_f64 : sm.red_f64b) + osum;
-            F_TS(42 + round);
+            pre = f_block_excl_f64_buf(loc, &tot, sm.red_f64) + osum;
+            F_TS(42);
         }
         double lo = pre;
 #pragma unroll
@@ -1182,7 +1185,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             if (b == bH) f.headend = o;
             o += capv[q];
         }
+        F_TS(33);
         __syncthreads();
+        F_TS(34);
 #pragma unroll
         for (int q = 0; q < kPer; q++) f.w[1 + kPer * t + q] = wv[q];
         if (t == 0) {
@@ -1344,6 +1349,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         // (or 1/S if the cut may lie in the head)
         if (t == 0) f.nreg = kFBins;
         __syncthreads();
+        F_TS(32);
         if (nuc) {
 #pragma unroll
             for (int q = 0; q < kPer; q++) {
