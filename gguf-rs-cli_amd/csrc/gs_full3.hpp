@@ -325,6 +325,18 @@ __device__ bool f3_seg(const Full3Smem &f, int s, int r, float *c)
     return true;
 }
 
+// The smallest of every thread's v (all threads call; one barrier).
+__device__ __forceinline__ int f3_block_min(Full3Smem &f, uint32_t v)
+{
+    const uint32_t w = wave_min_u32(v);
+    if (lane_id() == 0) f.wlast[wave_id()] = w;
+    __syncthreads();
+    uint32_t r = f.wlast[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; i++) r = min(r, f.wlast[i]);
+    return (int)r;
+}
+
 // Level totals of table s: rtot[r] = sum of k * count over run r, and for
 // each tie, A = the same sum over its run's levels above it.  Then the ties
 // are sorted by run, then k descending (one thread; at most kF3Ties).
@@ -1135,17 +1147,14 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         F3_TS(26);
         uint32_t call;
         const uint32_t sp = block_excl_u32(ssum, &call, sm);
-        if (t == 0) f.bH = kFBins;
-        __syncthreads();
-        uint32_t run_pre = sp;
+        uint32_t run_pre = sp, cand = kFBins;
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
             const int b = kPer * t + q;
-            if (b > bmax && b >= 1 && call - run_pre <= (uint32_t)kF3L1) { atomicMin(&f.bH, b); break; }
+            if (cand == (uint32_t)kFBins && b > bmax && b >= 1 && call - run_pre <= (uint32_t)kF3L1) cand = (uint32_t)b;
             run_pre += c[q];
         }
-        __syncthreads();
-        const int bH = f.bH;
+        const int bH = f3_block_min(f, cand);
         if (bH >= kFBins) F3_FAIL();
         // runs of seq 1 and the role words; listed bins (the head and the
         // windows) get list segments (room for the raw values of penalized
@@ -1347,21 +1356,19 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         // s2 lies in [top_p, top_p + the cut element's summand + a rounding
         // step]: the summand is at most the first cut-window bin's largest
         // (or 1/S if the cut may lie in the head)
-        if (t == 0) f.nreg = kFBins;
-        __syncthreads();
-        F_TS(32);
+        uint32_t cand = kFBins;
         if (nuc) {
 #pragma unroll
             for (int q = 0; q < kPer; q++) {
                 const int b = kPer * t + q;
-                if (b >= bH && (double)f.pre[b + 1] * iP * dh >= tp) { atomicMin(&f.nreg, b); break; }
+                if (cand == (uint32_t)kFBins && b >= bH && (double)f.pre[b + 1] * iP * dh >= tp) cand = (uint32_t)b;
             }
         }
-        __syncthreads();
+        const int bcut = f3_block_min(f, cand);     // the first bin the cut may lie in
         F_TS(46);
         double s2lo = 1.0, s2hi = 1.0;
         if (nuc) {
-            const int bc = f.nreg;
+            const int bc = bcut;
             double vmax = iS;
             if (bc > bH && bc < kFBins) {
                 float ylo, yhi;
