@@ -52,10 +52,8 @@ __device__ int g_vdiag[1024 * 16];
 // sub-phase timestamps per row (< 256): 64 slots
 __device__ uint32_t g_vt[256 * 64];
 #define F_TS(k) do { if (threadIdx.x == 0 && blockIdx.x < 256) g_vt[blockIdx.x * 64 + (k)] = (uint32_t)__builtin_amdgcn_s_memrealtime(); } while (0)
-#define F_TS_VAL(k, v) do { g_vt[blockIdx.x * 64 + (k)] = (uint32_t)(v); } while (0)
 #else
 #define F_TS(k) do { } while (0)
-#define F_TS_VAL(k, v) do { } while (0)
 #endif
 #define F_FAIL() do { F_NOTE(0); return false; } while (0)
 #define F_WFAIL() do { F_NOTE(1); return -1; } while (0)

@@ -166,8 +166,7 @@ struct F3Above {        // v < cum
 // same chain, reading broadcasts): the sum crosses binades often while it is
 // small (at the head of the row), and each crossing would cost a step.
 template <class P>
-__device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *cum_io, P pred, uint32_t nseq = 0,
-                            int diag = -1)
+__device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *cum_io, P pred, uint32_t nseq = 0)
 {
     const int lane = lane_id();
     float cum = *cum_io;
@@ -203,9 +202,6 @@ __device__ uint32_t f3_chain(const float *v, uint32_t beg, uint32_t end, float *
         }
     }
     while (j0 < end) {
-#ifdef GS_TIMING
-        if (diag >= 0 && lane == 0 && blockIdx.x < 256) g_vt[blockIdx.x * 64 + 56 + diag]++;
-#endif
         const uint32_t jl = j0 + 4u * (uint32_t)lane;
         // this lane's live values: [jl, jl + nl); the reads past them stay
         // inside the workgroup's LDS and are replaced by 0
@@ -367,7 +363,6 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
         }
         if (part) atomicAdd((unsigned long long *)&f.rtot[s][r], (unsigned long long)part);
     }
-    F_TS(50 + 3 * s);
     ncount = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_u32(ncount), 63);
     if (lane_id() == 0 && ncount) atomicSub(&f.lcount[s], ncount);
     for (int i = 0; i < nt; i++) {
@@ -379,10 +374,8 @@ __device__ void f3_totals(RowSmem &sm, Full3Smem &f, int s)
         part = wave_sum_u64(part);
         if (lane_id() == 0 && part) atomicAdd((unsigned long long *)&f.tie[s][i].A, (unsigned long long)part);
     }
-    F_TS(51 + 3 * s);
     __syncthreads();
     if (f.lcount[s] != 0u) f.fail = 1;    // a 16-bit counter wrapped
-    if (t == 0 && blockIdx.x < 256) F_TS_VAL(62 + s, nt);
     if (nt < 2) return;
     // the ties ranked by (run, k descending, index), one per thread
     F3Tie mine;
@@ -458,8 +451,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
         uint32_t end = f.headend;
         const bool at = lim && lim_arr == 0u;
         if (at) end = lim_pos + 1u;
-        const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 64u, roff == 0u ? 0 : s + 1);
-        F_TS(8 + 8 * (roff == 0u ? 0 : s + 1));
+        const uint32_t p = f3_chain(st, 0u, end, &cum, pred, 64u);
         if (s == 1) F3_TS(16 + 5 * s);
         *cum_out = cum;
         if (p < end) { *arr = 0u; *pos = p; return 1; }
@@ -475,7 +467,7 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
             uint32_t end = cend(b1);
             const bool at = lim && lim_arr == 1u && lim_pos >= beg && lim_pos < end;
             if (at) end = lim_pos + 1u;
-            const uint32_t p = f3_chain(st, roff + beg, roff + end, &cum, pred, 0u, 3 + (roff == 0u ? 0 : s + 1));
+            const uint32_t p = f3_chain(st, roff + beg, roff + end, &cum, pred);
             if (s == 1) F3_TS(17 + 5 * s + min(g, 3));
             *cum_out = cum;
             if (p < roff + end) { *arr = 1u; *pos = p - roff; return 1; }
@@ -485,7 +477,6 @@ __device__ int f3_walk(Full3Smem &f, const float *st, uint32_t roff, int s, cons
             *cum_out = cum;
             if (pred(cum)) return -1;
         }
-        F_TS(9 + 8 * (roff == 0u ? 0 : s + 1) + min(g, 6));
 #ifdef GS_TIMING
         {
             // the predicted sums' relative error at region ends (2^-30 units)
@@ -1037,7 +1028,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         double otot;
         f_block_excl_f64_buf(osum, &otot, sm.red_f64);
         osum = otot;
-        F_TS(40);
         uint32_t cn[kPer];
         double mb[kPer], ed[kPer + 1];      // ed[q]: the summand at bin kPer t + q's upper edge
         const double mscale = exp((double)m0 - (double)m) / (double)kFMassScale;
@@ -1054,7 +1044,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         double tot;
         double pre = f_block_excl_f64_buf(loc, &tot, sm.red_f64b) + osum;
-        F_TS(41);
         // one refinement: a second one (with the refined sums' grids) left
         // the largest error of the predicted sums at the region ends, and
         // the rows that take this path, unchanged on C3 and C4
@@ -1080,7 +1069,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 loc += ct[q];
             }
             pre = f_block_excl_f64_buf(loc, &tot, sm.red_f64) + osum;
-            F_TS(42);
         }
         double lo = pre;
 #pragma unroll
@@ -1176,7 +1164,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         uint32_t ltot;
         uint32_t o = block_excl_u32(capl, &ltot, sm) + (uint32_t)nover;   // (its barriers: w read)
-        F_TS(44);
         uint32_t wv[kPer];
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
@@ -1194,9 +1181,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             if (b == bH) f.headend = o;
             o += capv[q];
         }
-        F_TS(33);
         __syncthreads();
-        F_TS(34);
 #pragma unroll
         for (int q = 0; q < kPer; q++) f.w[1 + kPer * t + q] = wv[q];
         if (t == 0) {
@@ -1208,7 +1193,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         for (int j = t; j <= kF3Lvl; j += kThreads) f.lvl[j] = 0u;
         __syncthreads();
-        F_TS(45);
         // uniform bins: every element adds ku (the count is exact)
         uint32_t nadd = 0;
 #pragma unroll
@@ -1365,7 +1349,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             }
         }
         const int bcut = f3_block_min(f, cand);     // the first bin the cut may lie in
-        F_TS(46);
         double s2lo = 1.0, s2hi = 1.0;
         if (nuc) {
             const int bc = bcut;
@@ -1378,7 +1361,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             s2lo = (double)top_p;
             s2hi = (double)__double2float_ru(tp + vmax + ldexp(tp, -22));
         }
-        F_TS(47);
         cS = (float)iS;
         cS3lo = __double2float_rd(iS / s2hi);
         band3 = (float)((double)kF3Band23 * 2.0 + (s2hi / s2lo - 1.0));
@@ -1464,9 +1446,7 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             capl += capv[q];
         }
         uint32_t ltot;
-        F_TS(48);
         uint32_t o = block_excl_u32(capl, &ltot, sm);
-        F_TS(49);
         uint2 wv[kPer];
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
@@ -1613,7 +1593,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         }
         f3_lcount(f, 0, nok2);
         f3_lcount(f, 1, nok3);
-        F_TS(0);
         F3_STAT(7, f.list_end);
         F3_STAT(8, f.ndef);
         F3_STAT(9, f.namb);
@@ -1636,10 +1615,8 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
             const float p = glibc_expf_tab(y - m, f.exptab) / S;
             f3_count_exact(f, 0, rr, ldexpf(p, 23 - f.run[0][rr].e));
         }
-        F_TS(1);
         __threadfence_block();
         __syncthreads();
-        F_TS(2);
         if (nuc) {
             for (uint32_t j = t; j < f.list_end; j += kThreads) {
                 const uint64_t en = ldg(se3 + j);
@@ -1651,7 +1628,6 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
                 f3_count_exact(f, 0, rr, ldexpf(p, 23 - f.run[0][rr].e));
             }
         }
-        F_TS(3);
         __syncthreads();
         if (f.fail || f.ntie[0] > kF3Ties) F3_FAIL();
     }
@@ -1680,19 +1656,9 @@ __device__ bool full_v3_row(RowSmem &sm, const float *row, int V, float T, float
         if (wave_id() == 0) {
             float c;
             uint32_t arr = 0u, pos = 0u;
-#ifdef GS_WALKTWICE
-            for (int rep = 0; rep < 2; rep++) {
-                if (rep == 1) F_TS(50);
-#endif
             const int res = f3_walk(f, stg2, headend, 0, segst, cend3, F3AtLeast{top_p},
                                     false, 0u, 0u, &c, &arr, &pos);
-#ifdef GS_WALKTWICE
-            if (rep == 0) continue;
-#endif
             if (lane_id() == 0) { f.s2 = c; f.walk_res = res; f.cut_arr = arr; f.cut_pos = pos; }
-#ifdef GS_WALKTWICE
-            }
-#endif
         }
         __syncthreads();
         F3_STAT(14, f.walk_res);
