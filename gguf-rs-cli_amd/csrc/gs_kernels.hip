@@ -74,6 +74,7 @@ struct RowSmem {
     alignas(16) float fin[256];                 // finish_wave: the values being accumulated
     int tok;
     int flag_snan;                              // a NaN in the streamed part of a row (topk_row_reg)
+    uint32_t reg_sel;                           // topk_row_reg: the bound's histogram bin
     union {
         TopkSmem tk;
         FullSmem fs;
@@ -762,8 +763,9 @@ __device__ int topk_row_tmax(RowSmem &sm, const float *row, int V, int k, float 
 // table is built.  The bound is the one of topk_row_tmax (the (k + U)-th
 // largest of the 1024 thread maxima), found with one histogram level over
 // the spread of the thread maxima: bin = (max key - key) >> shift, with the
-// shift that maps that spread onto kSelBins bins.  Every wave scans the
-// histogram itself, so the bound costs one barrier.  The candidates are
+// shift that maps that spread onto kSelBins bins.  Wave 0 scans the
+// histogram and publishes the bin (a barrier: the scan is VALU work that
+// every wave of a SIMD would otherwise repeat there).  The candidates are
 // compacted per wave (one LDS atomic per wave), the penalized ids are left
 // out through the id bitmap and come back from the penalty table with their
 // penalized value, and a rank sort places only the first k.
@@ -886,9 +888,12 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
     // Slots past the row (clamped loads) become -inf, below every bound
     // used.  Done here, after the table inserts: overwriting a register that
     // a load is still filling waits for that load.
+    const int wfirst = __builtin_amdgcn_readfirstlane(t & ~63);   // the wave's first thread
 #pragma unroll
     for (int u = 0; u < kRegF4; u++)
-        if (u * kThreads + t >= n4r) rv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (u * kThreads + wfirst + 63 >= n4r) {                     // wave-uniform: most waves skip
+            if (u * kThreads + t >= n4r) rv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
     // Thread maximum and NaN test.
     float fmx = -INFINITY;
     uint64_t nanm = 0;
@@ -960,9 +965,9 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
     // paths the caller falls back to).
     if (sm.flag_nan) { *ok = true; *status = GS_ERR_NAN; return 0; }
     if (need > nmax) return 0;
-    // Bin of the need-th largest thread maximum, scanned by every wave.
-    uint32_t sel;
-    {
+    // Bin of the need-th largest thread maximum, scanned by wave 0 (the
+    // scan is VALU work that every other wave would repeat on its SIMD).
+    if (w == 0) {
         const uint4 *h4 = reinterpret_cast<const uint4 *>(sm.x.tk.u.hist) + lane;
         uint32_t hv[kSelBins / 64];
 #pragma unroll
@@ -985,8 +990,12 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
             c += hv[q];
             b += c < need ? 1u : 0u;
         }
-        sel = (uint32_t)L * (kSelBins / 64) + (uint32_t)__builtin_amdgcn_readlane((int)b, L);
+        // the readlane stays out of the lane-0 branch: b must be computed in lane L
+        const uint32_t bin = (uint32_t)L * (kSelBins / 64) + (uint32_t)__builtin_amdgcn_readlane((int)b, L);
+        if (lane == 0) sm.reg_sel = bin;
     }
+    __syncthreads();
+    const uint32_t sel = sm.reg_sel;
     // Keys >= tau are exactly those whose bin is <= sel; at least `need`
     // thread maxima are among them.  tf is the same bound as a float
     // (x >= tf <=> f2key(x) >= tau for every non-NaN x).  A bound at -inf
@@ -1777,7 +1786,10 @@ chunk_topk_kernel(RowArgs a, int nch, float *vrow, uint32_t *vidx, size_t vld)
 // report a NaN through the row's flags instead).  n <= kCandCap
 // (kChunkSelfMaxN).  All threads of the block call it.
 static_assert(kChunkSelfMaxN <= kCandCap, "virtual row of the one-launch chunked path");
-__device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int b, const gs_params &p)
+// The loads of the virtual row into sm.x.tk.cand (device-scope atomic
+// loads: the device-coherent level, where the chunks' stores are); the
+// caller's barrier completes them.
+__device__ __forceinline__ void load_vrow_y(RowSmem &sm, const RowArgs &a, int b, const gs_params &p)
 {
     const int t = threadIdx.x;
     const int kp = ((int)p.top_k + 3) & ~3;
@@ -1790,7 +1802,14 @@ __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int
                                                           __HIP_MEMORY_SCOPE_AGENT));
         cand[i] = cand_of(f2key(y), __hip_atomic_load(vi + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     }
-    __syncthreads();
+}
+// After load_vrow_y and a barrier; r is the row's draw.
+__device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int b, const gs_params &p, float r)
+{
+    const int t = threadIdx.x;
+    const int kp = ((int)p.top_k + 3) & ~3;
+    const int n = a.cnch * kp;
+    uint64_t *cand = sm.x.tk.cand;
     // Each chunk's kp entries are sorted (descending): an entry's rank is
     // its place in its chunk plus, for every other chunk, the length of the
     // prefix of larger entries there (binary lifting over all chunks at once).
@@ -1828,7 +1847,6 @@ __device__ __forceinline__ void finish_vrow_y(RowSmem &sm, const RowArgs &a, int
 #ifdef GS_TIMING
     if (t == 0 && b == (int)g_row) g_fails[1006] = (int)__builtin_amdgcn_s_memrealtime();
 #endif
-    const float r = a.u ? a.u[b] : lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
     auto yv = [&](int j) { return key2f((uint32_t)(top[j] >> 32)); };
     auto ix = [&](int j) { return ~(uint32_t)top[j]; };
     const int tok = finish_sorted(sm, k, yv, ix, p.top_p, r);
@@ -1866,6 +1884,8 @@ chunk_rows_kernel(RowArgs a)
 #define CR_TS(i) do { } while (0)
 #endif
     CR_TS(0);
+    // the draw, for the block that finishes the row (loaded now: off the tail)
+    const float r = a.u ? a.u[b] : lcg_value(lcg_jump(a.lcg_state, (uint64_t)b));
     const int nch = a.cnch;
     const int kp = ((int)p.top_k + 3) & ~3;
     const int q4 = a.V >> 2;
@@ -1935,7 +1955,11 @@ chunk_rows_kernel(RowArgs a)
     // measured: C2 21.6 -> 38.2 us per batch.)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     CR_TS(4);
+    // Every thread reads the flags (final: every chunk set its bits before
+    // its counter add); the slots are loaded in the same round trip, and
+    // used when no flag is set.
     const uint32_t flags = __hip_atomic_load(a.csync + 2 * (size_t)b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    load_vrow_y(sm, a, b, p);
     __syncthreads();
     if (t == 0) {
         __hip_atomic_store(a.csync + 2 * (size_t)b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1946,7 +1970,7 @@ chunk_rows_kernel(RowArgs a)
     } else if (flags & 1u) {
         sample_row<kModeSmall>(sm, a, b, 0);
     } else {
-        finish_vrow_y(sm, a, b, p);
+        finish_vrow_y(sm, a, b, p, r);
     }
     CR_TS(5);
 }
