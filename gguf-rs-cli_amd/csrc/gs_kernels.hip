@@ -896,10 +896,12 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
         }
     // Thread maximum and NaN test.
     float fmx = -INFINITY;
+    float mu[kRegF4];        // per float4 maxima: the candidate passes skip float4s with no hit in the wave
     uint64_t nanm = 0;
 #pragma unroll
     for (int u = 0; u < kRegF4; u++) {
-        fmx = fmaxf(fmx, fmaxf(fmaxf(rv[u].x, rv[u].y), fmaxf(rv[u].z, rv[u].w)));
+        mu[u] = fmaxf(fmaxf(rv[u].x, rv[u].y), fmaxf(rv[u].z, rv[u].w));
+        fmx = fmaxf(fmx, mu[u]);
         nanm |= __ballot(__builtin_isunordered(rv[u].x, rv[u].y));
         nanm |= __ballot(__builtin_isunordered(rv[u].z, rv[u].w));
     }
@@ -1010,8 +1012,11 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
     // the same order.  Entries hold the raw (value, id); the penalty bitmap
     // and the division by T are applied afterwards, one candidate per thread.
     uint32_t wcnt = 0u;
+    uint32_t uany = 0u;      // bit u: some lane of the wave holds a hit in float4 u
 #pragma unroll
     for (int u = 0; u < kRegF4; u++) {
+        if (__ballot(mu[u] >= tf) == 0) continue;
+        uany |= 1u << u;
         wcnt += (uint32_t)__popcll(__ballot(rv[u].x >= tf));
         wcnt += (uint32_t)__popcll(__ballot(rv[u].y >= tf));
         wcnt += (uint32_t)__popcll(__ballot(rv[u].z >= tf));
@@ -1023,6 +1028,7 @@ __device__ __forceinline__ int topk_row_reg(RowSmem &sm, const float *row, float
     wpos = (uint32_t)__builtin_amdgcn_readfirstlane((int)wpos);
 #pragma unroll
     for (int u = 0; u < kRegF4; u++) {
+        if (!((uany >> u) & 1u)) continue;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const float x = f4c(rv[u], c);
